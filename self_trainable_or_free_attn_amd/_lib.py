@@ -1,0 +1,75 @@
+"""ctypes binding of the C ABI in include/echosparse_hip.h (libechosparse_hip.so, built in-tree by build_lib).
+
+There is no fallback: if the library is missing or fails to load, every kernel call raises. Arguments are torch
+tensors (device pointers taken with data_ptr) or Python scalars; each call is enqueued on the current HIP stream
+of torch, so the kernels order with the surrounding torch work exactly like the reference's launches do.
+"""
+import ctypes
+import os
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libechosparse_hip.so")
+
+P, I, F, Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+
+# name -> argument types (the trailing hipStream_t is added below); mirrors include/echosparse_hip.h
+SIGNATURES = {
+    "es_block_attention": [P, P, P, P, P, P, I, P, P, P, P, F, I, I, I],
+    "es_sparse_attention": [P, P, P, P, P, P, P, P, P, P, I, P, P, P, P, P, I, P, P, P, P, F, I, I, I, I],
+    "es_exact_fallback": [P, P, P, P, P, P, I, P, P, I, I, I],
+    "es_compensate_fallback": [P, P, P, P, P, P, P, I, I, I],
+    "es_dense_attention": [P, P, P, P, P, I, I, I],
+    "es_block_means": [P, P, P, P, I, I, I],
+    "es_estimate_skipped": [P, P, P, P, P, P, P, P, I, I, I],
+    "es_full_step_scales": [P, P, P, P, I, I],
+    "es_select_blocks": [P, P, P, P, P, P, P, P, P, I, P, I, I, I, I, I, I],
+    "es_pack_plan": [P, P, I, I, I, I],
+    "es_rebuild_plan": [P, P, I, P, P, P, P, P, I, P, P, I, I, I],
+    "es_representatives": [P, P, P, P, P, P, P, P, P, Z, I, I, I, I],
+}
+NO_STREAM = {"es_representatives_workspace": ([I, I, I], Z), "es_last_error_string": ([], ctypes.c_char_p),
+             "es_abi_version": ([], I)}
+
+_lib = None
+
+
+def lib():
+    """The loaded library (loaded on first use; raises if it is not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built; run `python -m self_trainable_or_free_attn_amd.build_lib`")
+        so = ctypes.CDLL(LIB_PATH)
+        for name, args in SIGNATURES.items():
+            fn = getattr(so, name)
+            fn.argtypes = [*args, P]
+            fn.restype = I
+        for name, (args, res) in NO_STREAM.items():
+            fn = getattr(so, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = so
+    return _lib
+
+
+def ptr(x):
+    """Device pointer of a tensor (None -> NULL)."""
+    if x is None:
+        return None
+    return ctypes.c_void_p(x.data_ptr())
+
+
+def call(name, *args):
+    """Call an entry point on torch's current stream; raise RuntimeError with the library's message on failure."""
+    so = lib()
+    conv = [ptr(a) if isinstance(a, torch.Tensor) or a is None else a for a in args]
+    stream = torch.cuda.current_stream().cuda_stream
+    status = getattr(so, name)(*conv, ctypes.c_void_p(stream))
+    if status != 0:
+        msg = so.es_last_error_string().decode()
+        raise RuntimeError(f"{name} failed (status {status}): {msg}")
+
+
+def workspace_bytes(L, H, D):
+    return int(lib().es_representatives_workspace(L, H, D))

@@ -1,0 +1,223 @@
+"""LSE-guided block-sparse self-attention (EchoSparse) on MI355X: the schedule of the reference's
+`echosparse/attention.py` (EchoSparseAttention, attention.py:133-330), driving the gfx950 kernel set.
+
+Between two denoising steps the log-sum-exp (LSE) of every attention row barely changes. Each (CFG branch, layer)
+keeps the previous step's LSE and uses it three ways: as a fixed softmax offset (no running maximum, no
+rescaling); to sum the exponentials per kv block while computing the selected blocks (the block-probability map that
+selects the next step's blocks); and to compensate skipped blocks inside the same softmax (block-mean key/value for
+every skipped block, four clustered representatives for the most probable third of them).
+
+Schedule of a (branch, layer): dense attention for the first `dense_steps - 1` steps, then one step with every
+block through the fixed-offset kernel (exact output and the first map), then sparse steps that compute the top
+`density` blocks of every 128-row query tile.
+
+State model: the reference's compact one (H100 / RTX 5090, attention.py:72-130, 272-330), which is also the one that
+suits 288 GB of HBM best: per layer only the offsets of each branch and the next step's selection as two bit masks
+per tile; the map, the lists and the scales are scratch shared by all layers.
+"""
+import torch
+
+from . import backends
+
+BM = 128
+BK = 64
+LOG2E = 1.4426950408889634
+MIN_BLOCKS = 64          # sequences shorter than 64 kv blocks (4096 tokens) run dense
+
+
+def _cdiv(a, b):
+    return -(-a // b)
+
+
+def _next_pow2(n):
+    return 1 << (n - 1).bit_length()
+
+
+def dense_attention(q, k, v, return_lse=False):
+    """Dense attention on [1, L, H, D] bf16 tensors with the native kernel. With return_lse also the natural-log
+    LSE [1, H, L] (the FlashAttention-4 contract the reference calls, attention.py:33-35)."""
+    from .kernels import gfx950
+    out, lse2 = gfx950.dense_attention(q[0], k[0], v[0])
+    if not return_lse:
+        return out[None]
+    L = q.shape[1]
+    return out[None], (lse2[:L].t() / LOG2E)[None]
+
+
+class _CompactState:
+    """State of one layer: the offsets of every branch and the plans (exact and skip bit masks). One branch rewrites
+    its plan in place once the step has used it; with CFG branch 0 writes the other of two plans while later
+    branches still read the current one (reference attention.py:72-96)."""
+
+    def __init__(self, L, H, device):
+        nb = _cdiv(L, BK)
+        self.L, self.H, self.device = L, H, device
+        self.words = max(_next_pow2(nb) // 32, 4 * _cdiv(nb, 128))
+        self.plans = []
+        self.offsets = {}
+        self.ready = set()          # branches that have run the full step
+        self.current = None         # (plan, step) used by the branches of this step
+        self.pending = None         # (plan, step) made by branch 0 for the next step
+
+    def plan(self, i):
+        while len(self.plans) <= i:
+            shape = (self.H, _cdiv(self.L, BM), self.words)
+            self.plans.append(tuple(torch.full(shape, -1, device=self.device, dtype=torch.int32) for _ in range(2)))
+        return self.plans[i]
+
+    def offset(self, branch):
+        if branch not in self.offsets:
+            self.offsets[branch] = torch.full((_cdiv(self.L, BM) * BM, self.H), 1e30, device=self.device)
+        return self.offsets[branch]
+
+
+class _PlanScratch:
+    """Per-call tensors shared by all layers (reference attention.py:99-116)."""
+
+    def __init__(self, L, H, device, refine_width):
+        nq, nb = _cdiv(L, BM), _cdiv(L, BK)
+        self.shape = (L, H, refine_width)
+        self.mass = torch.empty(H, nq, nb, device=device)
+        self.keep = torch.empty(H, nq, nb, device=device, dtype=torch.uint8)
+        self.next_keep = torch.empty(H, nq, nb, device=device, dtype=torch.uint8)
+        self.scale_exact = torch.empty(H, nq, device=device)
+        self.scale_skip = torch.empty(H, nq, device=device)
+        self.counts = torch.empty(nq, H, device=device, dtype=torch.int32)
+        self.blocks = torch.zeros(nq, H, nb, device=device, dtype=torch.int32)
+        self.refine = torch.empty(nq, H, refine_width, device=device, dtype=torch.int32)
+        self.refine_counts = torch.empty(nq, H, device=device, dtype=torch.int32)
+        self.means = torch.empty(nq, H, nb, device=device, dtype=torch.int32)
+        self.mean_counts = torch.empty(nq, H, device=device, dtype=torch.int32)
+        self.next_offset = torch.empty(nq * BM, H, device=device)
+
+
+class _Buffers:
+    """Per-call scratch for one sequence shape (reference attention.py:119-130)."""
+
+    def __init__(self, L, H, D, device, refine_iters, K):
+        nq, nb = _cdiv(L, BM), _cdiv(L, BK)
+        self.shape = (L, H, D)
+        self.k_mean = torch.empty(nb, H, D, device=device, dtype=torch.bfloat16)
+        self.v_mean = torch.empty(nb, H, D, device=device, dtype=torch.bfloat16)
+        self.flags = torch.empty(nq, H, device=device, dtype=torch.int32)
+        self.all_counts = torch.full((nq, H), nb, device=device, dtype=torch.int32)
+        self.all_blocks = torch.arange(nb, device=device, dtype=torch.int32).expand(nq, H, nb).contiguous()
+        self.reps = K.Representatives(L, H, D, device, iters=refine_iters)
+
+
+class EchoSparseAttention:
+    """Self-attention for one video at a time; call `reset()` before each video.
+
+    `__call__(q, k, v, step, branch, layer)` takes [1, L, H, 128] bf16 tensors. `branch` numbers the transformer
+    forwards of a denoising step (0: conditional, 1: unconditional); later branches reuse branch 0's block selection
+    of the same step and layer. `sink`: first kv block that every query tile computes exactly. `rows`: the caller
+    uses only the first `rows` output rows; the query tiles past them are skipped.
+
+    `gpu`: "auto" (from the device of q) or "mi355x"; see `backends`.
+    """
+
+    def __init__(self, density=0.10, dense_steps=10, dense_layers=(0,), refine_iters=6, threshold=60.0, gpu="auto"):
+        assert dense_steps >= 2, "the first sparse step needs the LSE of a dense step and a full-block step"
+        self.density = density
+        self.dense_steps = dense_steps
+        self.dense_layers = set(dense_layers)
+        self.refine_iters = refine_iters
+        self.threshold = threshold
+        backends.check_name(gpu)
+        self.gpu = gpu
+        self.backend = None             # resolved from the device of the first call
+        self._device = None
+        self.K = None
+        self._states = {}
+        self._buffers = None
+        self._plan_scratch = None
+
+    def reset(self):
+        for st in self._states.values():
+            st.ready.clear()
+            st.current = st.pending = None
+
+    def __call__(self, q, k, v, step, branch, layer, sink=None, rows=None):
+        B, L, H, D = q.shape
+        assert B == 1, "batch size 1 only"
+        if q.device != self._device:
+            self.backend = backends.resolve(self.gpu, q.device)
+            self.K = backends.kernels(self.backend)
+            self._states.clear()
+            self._buffers = self._plan_scratch = None
+            self._device = q.device
+        if layer in self.dense_layers or _cdiv(L, BK) < MIN_BLOCKS:
+            return dense_attention(q, k, v)
+        return self._call_compact(q, k, v, step, branch, layer, sink, rows)
+
+    def _scratch(self, L, H, D, device):
+        if self._buffers is None or self._buffers.shape != (L, H, D):
+            self._buffers = None                           # one sequence shape at a time
+            self._buffers = _Buffers(L, H, D, device, self.refine_iters, self.K)
+        return self._buffers
+
+    def _budget(self, nb):
+        """Exactly computed blocks per tile, and refined blocks (four representatives each) per tile."""
+        top = max(1, int(round(self.density * nb)))
+        return top, max(0, int(round((nb - top) / 3)))
+
+    def _call_compact(self, q, k, v, step, branch, layer, sink, rows):
+        L, H, D = q[0].shape
+        st = self._states.get(layer)
+        if st is None or st.L != L:
+            self._states[layer] = None
+            st = self._states[layer] = _CompactState(L, H, q.device)
+        offset = st.offset(branch)
+        if branch == 0 and step >= self.dense_steps:
+            st.current = st.pending if st.pending is not None and st.pending[1] == step else None
+            st.pending = None
+        full = step == self.dense_steps - 1
+        sparse = step >= self.dense_steps and branch in st.ready and st.current is not None and st.current[1] == step
+        K = self.K
+        if not (full or sparse):
+            out, lse2 = K.dense_attention(q[0], k[0], v[0])
+            offset.copy_(lse2)
+            return out[None]
+        q, k, v = q[0], k[0], v[0]
+        top, refined = self._budget(_cdiv(L, BK))
+        rw = -(-refined // 32) * 32
+        buf = self._scratch(L, H, D, q.device)
+        ps = self._plan_scratch
+        if ps is None or ps.shape != (L, H, rw):
+            self._plan_scratch = None
+            ps = self._plan_scratch = _PlanScratch(L, H, q.device, rw)
+        out = torch.empty_like(q)
+        if full:
+            ps.keep.fill_(1)
+            ps.mass.zero_()
+            K.block_attention(q, k, v, out, buf.all_counts, buf.all_blocks, offset, ps.next_offset, buf.flags,
+                              mass=ps.mass, threshold=self.threshold)
+            K.exact_fallback(q, k, v, out, buf.all_counts, buf.all_blocks, ps.next_offset, buf.flags)
+            K.full_step_scales(offset, ps.next_offset, ps.scale_exact, ps.scale_skip, L)
+            st.ready.add(branch)
+        else:
+            exact, skip = st.plan(st.current[0])
+            K.rebuild_plan(exact, skip, ps.keep, ps.counts, ps.blocks, ps.refine, ps.refine_counts, ps.means,
+                           ps.mean_counts)
+            buf.reps.build(q, k, v, buf.k_mean, buf.v_mean)
+            if branch == 0:
+                ps.mass.zero_()
+            K.sparse_attention(q, k, v, buf.k_mean, buf.v_mean, ps.means, ps.mean_counts, out, ps.counts, ps.blocks,
+                               offset, ps.next_offset, buf.flags, ps.refine, ps.refine_counts, buf.reps.k, buf.reps.v,
+                               buf.reps.log_counts, mass=ps.mass if branch == 0 else None, threshold=self.threshold,
+                               rows=rows)
+            K.exact_fallback(q, k, v, out, ps.counts, ps.blocks, ps.next_offset, buf.flags)
+            K.compensate_fallback(q, buf.k_mean, buf.v_mean, ps.keep, ps.next_offset, out, buf.flags)
+            if branch == 0:
+                K.estimate_skipped(q, buf.k_mean, ps.keep, offset, ps.next_offset, ps.mass, ps.scale_exact,
+                                   ps.scale_skip)
+        if branch == 0:
+            # the next step's plan, after this step's last use of the current one in a single branch
+            plan = 0 if st.current is None else st.current[0] ^ (len(st.offsets) > 1)
+            exact, skip = st.plan(plan)
+            K.select_blocks(ps.mass, ps.keep, ps.scale_exact, ps.scale_skip, ps.next_keep, ps.counts, ps.blocks,
+                            buf.flags, skip, ps.refine, top, refined, L, sink=1 << 30 if sink is None else sink)
+            K.pack_plan(ps.next_keep, exact)
+            st.pending = (plan, step + 1)
+        offset.copy_(ps.next_offset)
+        return out[None]

@@ -1,0 +1,495 @@
+// Column-stream attention kernels for 128-row query tiles (gfx950, bf16 MFMA 32x32x16).
+//
+// One workgroup = one (query tile, head), 4 waves x 32 query rows. The keys the tile attends to arrive as a
+// stream of 64-column chunks, each staged in LDS (double-buffered, direct global->LDS 16-byte loads, swizzled
+// 256-byte rows) while the previous chunk is computed:
+//   FIXED       the fixed-softmax-offset pass (reference echosparse/kernels/sm90.py:54-115): exact 64-token
+//               blocks from the tile's block list, then (COMP) one column per listed mean block and four per
+//               listed refined block, p = 2^(s*log2e/sqrt(D) + bias - prior); per-block mass (MASS), O, LSE,
+//               flag.
+//   ONLINE      online softmax over the block list (reference sm120.py:143-180 exact_fallback, flagged tiles
+//               only); with no list and no flags it is dense attention with a log2 LSE.
+//   COMPENSATE  block-mean columns of the skipped blocks appended at the new LSE (reference
+//               triton_ops.py:251-295, flagged tiles only).
+// Row sources per chunk kind: exact block b -> token rows b*64 + r of k / v (rows >= L clamped, bias -inf);
+// mean block b -> row (b*H + h) of k_mean / v_mean; refined block b, rep c -> row h*(nb+1)*4 + 4b + c of
+// k_rep / v_rep.
+#include "../../include/echosparse_hip.h"
+#include "common.h"
+
+namespace es {
+
+constexpr int LISTCAP = 2048;  // stream ids staged in LDS; ids past it are read from global memory
+enum { FIXED = 0, ONLINE = 1, COMPENSATE = 2 };
+
+struct AttnArgs {
+  const bf16_t* q;
+  const bf16_t* k;
+  const bf16_t* v;
+  const bf16_t* k_mean;
+  const bf16_t* v_mean;
+  const int* means;
+  const int* mean_counts;
+  const int* counts;
+  const int* blocks;  // nullptr: every block (dense)
+  const int* refine;
+  const int* refine_counts;
+  const bf16_t* k_rep;
+  const bf16_t* v_rep;
+  const float* log_counts;
+  const uint8_t* keep;
+  const float* prior;  // FIXED: offset; COMPENSATE: LSE after the fallback
+  bf16_t* out;
+  float* lse;
+  int* flags;  // FIXED: written; ONLINE / COMPENSATE: read (nullptr = every tile)
+  float* mass;
+  int L, H, nq, nb, NK, RW, tiles, per_xcd;
+  float threshold, tail_log2, scale;
+};
+
+template <int MODE, bool COMP>
+struct Stream {
+  int n, nm, nr, cm, nc, staged;
+  const int* g_exact;
+  const int* g_means;
+  const int* g_refine;
+};
+
+template <int MODE, bool COMP, bool MASS>
+__global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) char kv_s[2][2][BK * 256];
+  __shared__ __attribute__((aligned(16))) float bias_s[2][BK];
+  __shared__ int list_s[LISTCAP];
+  __shared__ float mass_s[4][128];
+
+  // XCD-aware tile order: dispatch slot w runs on XCD w % 8; each XCD walks a contiguous run of tiles of one head
+  const int w = blockIdx.x;
+  const int xcd = w & 7, slot = w >> 3;
+  const int h = slot / a.per_xcd;
+  const int t = xcd * a.per_xcd + slot % a.per_xcd;
+  if (h >= a.H || t >= a.tiles) return;
+  const int th = t * a.H + h;
+  if (MODE != FIXED && a.flags != nullptr && a.flags[th] == 0) return;
+
+  const int L = a.L, H = a.H, nb = a.nb;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, hi = l >> 5, lq = l & 31;
+  const int row = t * BM + wv * 32 + lq;
+  const bool rvalid = row < L;
+
+  // ---------------------------------------------------------------- column stream and its staged ids
+  int n = 0, nm = 0, nr = 0;
+  const int* g_ex = nullptr;
+  const int* g_me = nullptr;
+  const int* g_rf = nullptr;
+  if (MODE == COMPENSATE) {
+    n = 0;
+  } else if (a.blocks == nullptr) {
+    n = nb;
+  } else {
+    n = a.counts[th];
+    g_ex = a.blocks + (size_t)th * a.NK;
+  }
+  if (COMP) {
+    nm = a.mean_counts[th];
+    nr = a.refine_counts[th];
+    g_me = a.means + (size_t)th * a.NK;
+    g_rf = a.refine + (size_t)th * a.RW;
+  }
+  const int cm = (nm + BK - 1) / BK, cr = (4 * nr + BK - 1) / BK;
+  const int nc = MODE == COMPENSATE ? (nb + BK - 1) / BK : n + (COMP ? cm + cr : 0);
+  const int ntot = n + nm + nr;
+  if (g_ex != nullptr || COMP) {
+    for (int i = tid; i < min(ntot, LISTCAP); i += 256)
+      list_s[i] = i < n ? g_ex[i] : i < n + nm ? g_me[i - n] : g_rf[i - n - nm];
+  }
+  __syncthreads();
+  auto stream_id = [&](int i) -> int {
+    if (i < LISTCAP) return list_s[i];
+    return i < n ? g_ex[i] : i < n + nm ? g_me[i - n] : g_rf[i - n - nm];
+  };
+  auto exact_id = [&](int j) -> int { return a.blocks == nullptr ? j : stream_id(j); };
+
+  // source rows of chunk cj: row R of the chunk -> (k row, v row) pointers
+  auto row_src = [&](int cj, int R, const bf16_t*& ks, const bf16_t*& vs) {
+    if (MODE == COMPENSATE) {
+      int b = cj * BK + R;
+      b = b < nb ? b : 0;
+      size_t o = ((size_t)b * H + h) * HD;
+      ks = a.k_mean + o;
+      vs = a.v_mean + o;
+    } else if (cj < n) {
+      int key = exact_id(cj) * BK + R;
+      key = key < L ? key : L - 1;
+      size_t o = ((size_t)key * H + h) * HD;
+      ks = a.k + o;
+      vs = a.v + o;
+    } else if (cj < n + cm) {
+      int col = (cj - n) * BK + R;
+      int b = col < nm ? stream_id(n + col) : 0;
+      size_t o = ((size_t)b * H + h) * HD;
+      ks = a.k_mean + o;
+      vs = a.v_mean + o;
+    } else {
+      int col = (cj - n - cm) * BK + R;
+      int b = col < 4 * nr ? stream_id(n + nm + (col >> 2)) : nb;
+      size_t o = ((size_t)h * (nb + 1) * 4 + (size_t)b * 4 + (col & 3)) * HD;
+      ks = a.k_rep + o;
+      vs = a.v_rep + o;
+    }
+  };
+  // additive log2 bias of column R of chunk cj (-inf masks the column)
+  auto col_bias = [&](int cj, int R) -> float {
+    if (MODE == COMPENSATE) {
+      int b = cj * BK + R;
+      if (b >= nb) return -INFINITY;
+      if (a.keep[((size_t)h * a.nq + t) * nb + b] != 0) return -INFINITY;
+      return b == nb - 1 ? a.tail_log2 : 6.0f;
+    } else if (cj < n) {
+      return exact_id(cj) * BK + R < L ? 0.0f : -INFINITY;
+    } else if (cj < n + cm) {
+      int col = (cj - n) * BK + R;
+      if (col >= nm) return -INFINITY;
+      return stream_id(n + col) == nb - 1 ? a.tail_log2 : 6.0f;
+    } else {
+      int col = (cj - n - cm) * BK + R;
+      if (col >= 4 * nr) return -INFINITY;
+      int b = stream_id(n + nm + (col >> 2));
+      return a.log_counts[(size_t)h * (nb + 1) * 4 + (size_t)b * 4 + (col & 3)];
+    }
+  };
+  // stage chunk cj into buffer sb: 16 instructions of 1 KB for K and 16 for V, 4 + 4 per wave
+  auto issue = [&](int cj, int sb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int P = (wv * 4 + i) * 64 + l;  // 16-byte position in the 16 KB tile
+      const int R = P >> 4, c = (P & 15) ^ swz(R);
+      const bf16_t *ks, *vs;
+      row_src(cj, R, ks, vs);
+      g2lds16(ks + c * 8, kv_s[sb][0] + (wv * 4 + i) * 1024);
+      g2lds16(vs + c * 8, kv_s[sb][1] + (wv * 4 + i) * 1024);
+    }
+  };
+
+  // ---------------------------------------------------------------- per-lane query state
+  bf16x8 qreg[8];
+  {
+    const bf16_t* qr = a.q + ((size_t)(rvalid ? row : 0) * H + h) * HD;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      bf16x8 z = {};
+      qreg[ks] = rvalid ? *reinterpret_cast<const bf16x8*>(qr + 16 * ks + 8 * hi) : z;
+    }
+  }
+  const float pr = (MODE != ONLINE && rvalid) ? a.prior[(size_t)row * H + h] : 0.0f;
+  const float nprior = rvalid ? -pr : -INFINITY;
+  const float scale = a.scale;
+
+  f32x16 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) o[db] = f32x16{};
+  float lsum = 0.0f;        // this lane's share of the row sum (its 32 keys of every chunk)
+  float mrun = -INFINITY;   // ONLINE running max (same in both half-waves)
+
+  if (nc > 0) {
+    issue(0, 0);
+    if (wv == 0) bias_s[0][l] = col_bias(0, l);
+  }
+  wait_vmem();
+  __syncthreads();
+
+  for (int j = 0; j < nc; ++j) {
+    const int sb = j & 1;
+    float bnext = 0.0f;
+    if (j + 1 < nc) {
+      issue(j + 1, sb ^ 1);
+      if (wv == 0) bnext = col_bias(j + 1, l);
+    }
+    const char* kb = kv_s[sb][0];
+    const char* vb = kv_s[sb][1];
+
+    // S^T = K Q^T for the chunk's 64 keys (two 32-key C tiles)
+    f32x16 s0 = {}, s1 = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      bf16x8 a0 = lds_read16(kb, tile_off(lq, 2 * ks + hi));
+      bf16x8 a1 = lds_read16(kb, tile_off(32 + lq, 2 * ks + hi));
+      s0 = mfma32(a0, qreg[ks], s0);
+      s1 = mfma32(a1, qreg[ks], s1);
+    }
+    float p[32];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 b0 = *reinterpret_cast<const f32x4*>(&bias_s[sb][8 * i + 4 * hi]);
+      f32x4 b1 = *reinterpret_cast<const f32x4*>(&bias_s[sb][32 + 8 * i + 4 * hi]);
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        p[4 * i + jj] = fmaf(s0[4 * i + jj], scale, b0[jj]);
+        p[16 + 4 * i + jj] = fmaf(s1[4 * i + jj], scale, b1[jj]);
+      }
+    }
+    float csum = 0.0f;
+    if (MODE == ONLINE) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 32; ++r) mx = fmaxf(mx, p[r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mnew = fmaxf(mrun, mx);
+      const float msub = mnew == -INFINITY ? 0.0f : mnew;
+      const float alpha = exp2f_fast(mrun - msub);
+#pragma unroll
+      for (int r = 0; r < 32; ++r) {
+        p[r] = exp2f_fast(p[r] - msub);
+        csum += p[r];
+      }
+      lsum = lsum * alpha + csum;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      mrun = mnew;
+    } else {
+#pragma unroll
+      for (int r = 0; r < 32; ++r) {
+        float x = p[r] + nprior;
+        if (MODE == COMPENSATE) x = fminf(x, 100.0f);
+        p[r] = exp2f_fast(x);
+        csum += p[r];
+      }
+      lsum += csum;
+    }
+    if (MODE == FIXED && MASS && j < n) {
+      const float bs = wave_sum(csum);
+      if (l == 0) mass_s[wv][j & 127] = bs;
+    }
+
+    // O^T += V^T P^T: P^T (keys x queries) is the B operand straight from the exponentiated registers
+    bf16x8 pk[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) pk[kk] = pack8(&p[(kk >> 1) * 16 + (kk & 1) * 8]);
+    const int g1 = (l >> 4) & 1;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int rowA = (kk >> 1) * 32 + (kk & 1) * 16 + 4 * hi + ((l & 15) >> 2);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int c = 4 * db + 2 * g1 + ((l & 3) >> 1);
+        const int sub = (l & 1) * 8;
+        s16x4 ta = lds_read_tr(vb, tile_off(rowA, c) + sub);
+        s16x4 tb = lds_read_tr(vb, tile_off(rowA + 8, c) + sub);
+        o[db] = mfma32(cat_tr(ta, tb), pk[kk], o[db]);
+      }
+    }
+
+    if (j + 1 < nc && wv == 0) bias_s[sb ^ 1][l] = bnext;
+    wait_vmem();
+    __syncthreads();
+    if (MODE == FIXED && MASS && j < n && ((j & 63) == 63 || j == n - 1) && tid < 64) {
+      const int idx = (j & ~63) + tid;
+      if (idx <= j) {
+        const float m = mass_s[0][idx & 127] + mass_s[1][idx & 127] + mass_s[2][idx & 127] + mass_s[3][idx & 127];
+        a.mass[((size_t)h * a.nq + t) * nb + stream_id(idx)] = m;
+      }
+    }
+  }
+
+  // ---------------------------------------------------------------- epilogue
+  const float tot = lsum + __shfl_xor(lsum, 32, 64);
+  bf16_t* orow = a.out + ((size_t)(rvalid ? row : 0) * H + h) * HD;
+  float* lrow = a.lse + (size_t)row * H + h;
+  if (MODE == FIXED) {
+    const float lg = log2f(tot);
+    const bool bad = rvalid && !(lg >= -a.threshold && lg <= a.threshold);
+    const int any = __syncthreads_or(bad);
+    const float inv = 1.0f / tot;
+    if (rvalid) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ushort4 v4;
+          v4.x = f2bf(o[db][4 * i + 0] * inv);
+          v4.y = f2bf(o[db][4 * i + 1] * inv);
+          v4.z = f2bf(o[db][4 * i + 2] * inv);
+          v4.w = f2bf(o[db][4 * i + 3] * inv);
+          *reinterpret_cast<ushort4*>(orow + 32 * db + 8 * i + 4 * hi) = v4;
+        }
+    }
+    if (hi == 0) *lrow = rvalid ? pr + lg : 1e30f;
+    if (tid == 0) a.flags[th] = any;
+  } else if (MODE == ONLINE) {
+    const bool empty = n == 0;
+    const float inv = empty ? 0.0f : 1.0f / tot;
+    if (rvalid) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ushort4 v4;
+          v4.x = f2bf(o[db][4 * i + 0] * inv);
+          v4.y = f2bf(o[db][4 * i + 1] * inv);
+          v4.z = f2bf(o[db][4 * i + 2] * inv);
+          v4.w = f2bf(o[db][4 * i + 3] * inv);
+          *reinterpret_cast<ushort4*>(orow + 32 * db + 8 * i + 4 * hi) = v4;
+        }
+    }
+    if (hi == 0) *lrow = !rvalid ? 1e30f : empty ? -1e30f : mrun + log2f(tot);
+  } else {
+    const float den = 1.0f + tot;
+    const float inv = 1.0f / den;
+    if (rvalid) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ushort4* dst = reinterpret_cast<ushort4*>(orow + 32 * db + 8 * i + 4 * hi);
+          ushort4 old = *dst, v4;
+          v4.x = f2bf((bf2f(old.x) + o[db][4 * i + 0]) * inv);
+          v4.y = f2bf((bf2f(old.y) + o[db][4 * i + 1]) * inv);
+          v4.z = f2bf((bf2f(old.z) + o[db][4 * i + 2]) * inv);
+          v4.w = f2bf((bf2f(old.w) + o[db][4 * i + 3]) * inv);
+          *dst = v4;
+        }
+    }
+    if (hi == 0) *lrow = rvalid ? pr + log2f(den) : 1e30f;
+  }
+}
+
+template <int MODE, bool COMP, bool MASS>
+static int launch(const AttnArgs& a0, hipStream_t stream, const char* what) {
+  AttnArgs a = a0;
+  a.per_xcd = (a.tiles + 7) / 8;
+  const long long grid = 8LL * a.H * a.per_xcd;
+  if (grid <= 0) return ES_OK;
+  hipLaunchKernelGGL((attn_kernel<MODE, COMP, MASS>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+  return check_launch(what);
+}
+
+static int check_common(const void* q, const void* k, const void* v, int L, int H, int D) {
+  ES_REQUIRE(q && k && v, ES_ERR_INVALID, "q, k and v must be non-null");
+  ES_REQUIRE(L > 0 && H > 0, ES_ERR_INVALID, "L and H must be positive");
+  ES_REQUIRE(D == HD, ES_ERR_UNSUPPORTED, "head dimension must be 128");
+  return ES_OK;
+}
+
+static AttnArgs base_args(const void* q, const void* k, const void* v, int L, int H) {
+  AttnArgs a = {};
+  a.q = (const bf16_t*)q;
+  a.k = (const bf16_t*)k;
+  a.v = (const bf16_t*)v;
+  a.L = L;
+  a.H = H;
+  a.nq = (L + BM - 1) / BM;
+  a.nb = (L + BK - 1) / BK;
+  a.tiles = a.nq;
+  a.tail_log2 = log2f((float)(L - (a.nb - 1) * BK));
+  a.scale = LOG2E / sqrtf((float)HD);
+  a.threshold = 60.0f;
+  return a;
+}
+
+}  // namespace es
+
+using namespace es;
+
+extern "C" int es_block_attention(const void* q, const void* k, const void* v, void* out, const int* counts,
+                                  const int* blocks, int nk, const float* offset, float* lse, int* flags,
+                                  float* mass, float threshold, int L, int H, int D, hipStream_t stream) {
+  int st = check_common(q, k, v, L, H, D);
+  if (st) return st;
+  ES_REQUIRE(out && counts && blocks && offset && lse && flags, ES_ERR_INVALID, "null output or list pointer");
+  AttnArgs a = base_args(q, k, v, L, H);
+  ES_REQUIRE(nk >= 1, ES_ERR_INVALID, "block list width must be positive");
+  a.out = (bf16_t*)out;
+  a.counts = counts;
+  a.blocks = blocks;
+  a.NK = nk;
+  a.prior = offset;
+  a.lse = lse;
+  a.flags = flags;
+  a.mass = mass;
+  a.threshold = threshold;
+  if (mass) return launch<FIXED, false, true>(a, stream, "es_block_attention");
+  return launch<FIXED, false, false>(a, stream, "es_block_attention");
+}
+
+extern "C" int es_sparse_attention(const void* q, const void* k, const void* v, const void* k_mean,
+                                   const void* v_mean, const int* means, const int* mean_counts, void* out,
+                                   const int* counts, const int* blocks, int nk, const float* offset, float* lse,
+                                   int* flags, const int* refine, const int* refine_counts, int rw,
+                                   const void* k_rep, const void* v_rep, const float* log_counts, float* mass,
+                                   float threshold, int tiles, int L, int H, int D, hipStream_t stream) {
+  int st = check_common(q, k, v, L, H, D);
+  if (st) return st;
+  ES_REQUIRE(out && counts && blocks && offset && lse && flags && k_mean && v_mean && means && mean_counts &&
+                 refine && refine_counts && k_rep && v_rep && log_counts,
+             ES_ERR_INVALID, "null tensor pointer");
+  AttnArgs a = base_args(q, k, v, L, H);
+  ES_REQUIRE(nk >= 1 && rw >= 0, ES_ERR_INVALID, "bad list widths");
+  ES_REQUIRE(tiles >= 0 && tiles <= a.nq, ES_ERR_INVALID, "tiles out of range");
+  a.k_mean = (const bf16_t*)k_mean;
+  a.v_mean = (const bf16_t*)v_mean;
+  a.means = means;
+  a.mean_counts = mean_counts;
+  a.out = (bf16_t*)out;
+  a.counts = counts;
+  a.blocks = blocks;
+  a.NK = nk;
+  a.prior = offset;
+  a.lse = lse;
+  a.flags = flags;
+  a.refine = refine;
+  a.refine_counts = refine_counts;
+  a.RW = rw;
+  a.k_rep = (const bf16_t*)k_rep;
+  a.v_rep = (const bf16_t*)v_rep;
+  a.log_counts = log_counts;
+  a.mass = mass;
+  a.threshold = threshold;
+  a.tiles = tiles;
+  if (mass) return launch<FIXED, true, true>(a, stream, "es_sparse_attention");
+  return launch<FIXED, true, false>(a, stream, "es_sparse_attention");
+}
+
+extern "C" int es_exact_fallback(const void* q, const void* k, const void* v, void* out, const int* counts,
+                                 const int* blocks, int nk, float* lse, const int* flags, int L, int H, int D,
+                                 hipStream_t stream) {
+  int st = check_common(q, k, v, L, H, D);
+  if (st) return st;
+  ES_REQUIRE(out && counts && blocks && lse && flags, ES_ERR_INVALID, "null tensor pointer");
+  AttnArgs a = base_args(q, k, v, L, H);
+  a.out = (bf16_t*)out;
+  a.counts = counts;
+  a.blocks = blocks;
+  a.NK = nk;
+  a.lse = lse;
+  a.flags = (int*)flags;
+  return launch<ONLINE, false, false>(a, stream, "es_exact_fallback");
+}
+
+extern "C" int es_dense_attention(const void* q, const void* k, const void* v, void* out, float* lse2, int L,
+                                  int H, int D, hipStream_t stream) {
+  int st = check_common(q, k, v, L, H, D);
+  if (st) return st;
+  ES_REQUIRE(out && lse2, ES_ERR_INVALID, "null tensor pointer");
+  AttnArgs a = base_args(q, k, v, L, H);
+  a.out = (bf16_t*)out;
+  a.lse = lse2;
+  return launch<ONLINE, false, false>(a, stream, "es_dense_attention");
+}
+
+extern "C" int es_compensate_fallback(const void* q, const void* k_mean, const void* v_mean, const uint8_t* keep,
+                                      float* lse, void* out, const int* flags, int L, int H, int D,
+                                      hipStream_t stream) {
+  int st = check_common(q, k_mean, v_mean, L, H, D);
+  if (st) return st;
+  ES_REQUIRE(keep && lse && out && flags, ES_ERR_INVALID, "null tensor pointer");
+  AttnArgs a = base_args(q, k_mean, v_mean, L, H);
+  a.k_mean = (const bf16_t*)k_mean;
+  a.v_mean = (const bf16_t*)v_mean;
+  a.keep = keep;
+  a.prior = lse;
+  a.lse = lse;
+  a.out = (bf16_t*)out;
+  a.flags = (int*)flags;
+  return launch<COMPENSATE, false, false>(a, stream, "es_compensate_fallback");
+}
