@@ -1,0 +1,206 @@
+"""Headline benchmark: the EchoSparse sparse step on one MI355X at the Wan2.1-14B shape.
+
+Workload: per layer two CFG branch calls (B = 2), H = 40, D = 128, bf16, tokens on a
+21 x 45 x 80 latent grid (L = 75 600, 1182 kv blocks of 64, 591 query tiles of 128), Morton order; Q / K a
+low-frequency random Fourier field plus 0.3 N(0, 1), scaled per head so the mean row-softmax entropy is 20 % of
+ln L; V ~ N(0, 1). The previous step's LSE comes from a dense pass on inputs perturbed by 1 % Gaussian noise, and a
+full-block step on those inputs gives the map that selects the top 10 % blocks. A timed step is one layer of a
+sparse denoising step: branch 0 (plan rebuild, representatives + block means, fixed-offset attention, fallback,
+compensation, estimate, selection, plan pack) and branch 1 (the same without estimate / selection).
+
+Printed (one JSON line, rank 0): value = TFLOP/s on executed blocks over the whole layer time; ms_per_step =
+ms / layer; `roofline` for the dominant kernel (the fixed-offset sparse attention) from HIP events on its stream;
+the dense comparison (torch SDPA and this build's dense kernel); `cpu_baseline` = the numpy oracle on a bounded
+sample of (tile, head) pairs of the same step.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+PEAK_BF16 = 2.5e15
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--heads", type=int, default=40)
+    ap.add_argument("--grid", type=str, default="21,45,80")
+    ap.add_argument("--density", type=float, default=0.10)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def executed_flops(ps, D=128):
+    """4 * 128 * D * (64 * exact + means + 4 * refined), summed over (tile, head): one branch's sparse kernel."""
+    cols = 64 * ps.counts.double().sum() + ps.mean_counts.double().sum() + 4 * ps.refine_counts.double().sum()
+    return float(4 * 128 * D * cols)
+
+
+def cpu_baseline(q, k, v, attn, seconds):
+    """The numpy oracle's fixed-offset sparse step on a bounded sample of (tile, head) pairs (head 0, first tiles),
+    timed on this host; returned as TFLOP/s on executed blocks, like `value`."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import numpy as np
+    from oracle import echosparse_ref as ref
+    ps, buf = attn._plan_scratch, attn._buffers
+    st = attn._states[1]
+    h = 0
+    f = lambda x: x.float().cpu().numpy()
+    qs, ks, vs = (f(x[:, h:h + 1]) for x in (q, k, v))
+    comp = dict(k_mean=f(buf.k_mean[:, h:h + 1]), v_mean=f(buf.v_mean[:, h:h + 1]),
+                means=ps.means[:, h:h + 1].cpu().numpy(), mean_counts=ps.mean_counts[:, h:h + 1].cpu().numpy(),
+                refine=ps.refine[:, h:h + 1].cpu().numpy(), refine_counts=ps.refine_counts[:, h:h + 1].cpu().numpy(),
+                k_rep=f(buf.reps.k[h:h + 1]), v_rep=f(buf.reps.v[h:h + 1]),
+                log_counts=f(buf.reps.log_counts[h:h + 1]))
+    counts, blocks = ps.counts[:, h:h + 1].cpu().numpy(), ps.blocks[:, h:h + 1].cpu().numpy()
+    offset = f(st.offset(0)[:, h:h + 1])
+    tiles, t0, elapsed = 1, time.perf_counter(), 0.0
+    ref.fixed_offset_attention(qs, ks, vs, counts, blocks, offset, comp=comp, tiles=1)      # warm-up
+    while True:
+        t0 = time.perf_counter()
+        ref.fixed_offset_attention(qs, ks, vs, counts, blocks, offset, comp=comp, tiles=tiles)
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds or tiles >= counts.shape[0]:
+            break
+        tiles = min(counts.shape[0], max(tiles + 1, int(tiles * seconds / max(elapsed, 1e-3) * 1.05)))
+    cols = (64 * counts[:tiles].sum() + comp["mean_counts"][:tiles].sum() + 4 * comp["refine_counts"][:tiles].sum())
+    flops = 4 * 128 * 128 * float(cols)
+    return {"value": flops / elapsed / 1e12, "unit": "TFLOP/s (executed blocks)", "cores": os.cpu_count(),
+            "kind": "port", "sample": f"numpy oracle fixed-offset sparse step (exact + mean + representative "
+            f"columns), head 0, query tiles 0..{tiles - 1} of {counts.shape[0]}, one branch; {elapsed:.1f} s",
+            "ms_per_layer_extrapolated": elapsed / tiles * counts.shape[0] * q.shape[1] * 2 * 1e3}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py runs on one GPU only: the EchoSparse path shards by head with no exchange inside the "
+              "attention, so this build measures one GPU's share; --gpus must be 1", file=sys.stderr)
+        sys.exit(2)
+    from self_trainable_or_free_attn_amd import EchoSparseAttention
+    from self_trainable_or_free_attn_amd import synthetic
+    from self_trainable_or_free_attn_amd.kernels import gfx950
+
+    dev = torch.device("cuda:0")
+    grid = tuple(int(x) for x in args.grid.split(","))
+    H, D = args.heads, 128
+    L = grid[0] * grid[1] * grid[2]
+    t_setup = time.time()
+    print(f"[bench] inputs grid={grid} L={L} H={H}", file=sys.stderr, flush=True)
+    branches = []
+    for b in range(2):        # two CFG branches: independent fields (seed per branch)
+        q, k, v, _ = synthetic.fourier_qkv(grid, H, D, seed=11 + b, device=dev)
+        prev = [synthetic.perturbed(x, 0.01, seed=100 + 10 * b + i) for i, x in enumerate((q, k, v))]
+        branches.append(((q, k, v), prev))
+    attn = EchoSparseAttention(density=args.density, dense_steps=2, dense_layers=())
+    layer = 1
+    # step 0: dense (offsets), step 1: full-block step (first map and plan), both on the perturbed inputs
+    for step in range(2):
+        for b in range(2):
+            p = branches[b][1]
+            attn(p[0][None], p[1][None], p[2][None], step, b, layer)
+    torch.cuda.synchronize()
+    print(f"[bench] setup {time.time() - t_setup:.1f}s", file=sys.stderr, flush=True)
+
+    # time the dominant kernel with events on the stream it runs on (torch's current stream)
+    K = attn.K
+    orig = K.sparse_attention
+    events = []
+
+    def timed_sparse(*a, **kw):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        orig(*a, **kw)
+        e1.record()
+        events.append((e0, e1))
+
+    K.sparse_attention = timed_sparse
+    step = 2
+
+    def one_layer(step):
+        for b in range(2):
+            c = branches[b][0]
+            attn(c[0][None], c[1][None], c[2][None], step, b, layer)
+
+    for _ in range(args.warmup):
+        one_layer(step)
+        step += 1
+    torch.cuda.synchronize()
+    events.clear()
+    flops_steps = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        one_layer(step)
+        step += 1
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    K.sparse_attention = orig
+    ms_layer = elapsed / args.steps * 1e3
+    kern_ms = sum(a.elapsed_time(b) for a, b in events) / max(1, len(events))
+    ps = attn._plan_scratch
+    fl_branch = executed_flops(ps, D)
+    fl_layer = 2 * fl_branch
+    value = fl_layer / (ms_layer * 1e-3) / 1e12
+    achieved = fl_branch / (kern_ms * 1e-3) / 1e12
+    nq, nb = -(-L // 128), -(-L // 64)
+    mean_exact = float(ps.counts.double().mean())
+    result = {
+        "metric": "ms/layer + TFLOPS on executed blocks (% bf16 MFMA peak), Wan2.1-14B shape",
+        "value": round(value, 2), "unit": "TFLOP/s (executed blocks, whole sparse-step layer)",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_layer, 3),
+        "ms_per_layer": round(ms_layer, 3), "pct_bf16_peak": round(100 * value * 1e12 / PEAK_BF16, 2),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (Fourier-field Q/K, N(0,1) V, Morton order; random init, no checkpoint)",
+        "config": {"workload": "echosparse_sparse_step_wan2.1_14b", "cfg_branches": 2, "heads": H, "seq_len": L,
+                   "head_dim": D, "grid": list(grid), "density": args.density, "query_tiles": nq, "kv_blocks": nb,
+                   "mean_exact_blocks_per_tile": round(mean_exact, 2),
+                   "mean_mean_columns_per_tile": round(float(ps.mean_counts.double().mean()), 2),
+                   "mean_refined_blocks_per_tile": round(float(ps.refine_counts.double().mean()), 2),
+                   "executed_tflop_per_layer": round(fl_layer / 1e12, 3)},
+        "roofline": {"kernel": "attn_kernel<FIXED,COMP,MASS> (es_sparse_attention)", "bound": "mfma",
+                     "achieved": round(achieved, 2), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+                     "frac": round(achieved * 1e12 / PEAK_BF16, 4), "traffic": None,
+                     "avg_launch_ms": round(kern_ms, 3), "launches": len(events),
+                     "flop_per_launch": fl_branch},
+    }
+    if not args.no_dense:
+        q, k, v = branches[0][0]
+        qt, kt, vt = (x.permute(1, 0, 2)[None] for x in (q, k, v))
+        for _ in range(2):
+            torch.nn.functional.scaled_dot_product_attention(qt, kt, vt)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            torch.nn.functional.scaled_dot_product_attention(qt, kt, vt)
+        torch.cuda.synchronize()
+        sdpa_ms = (time.perf_counter() - t0) / 3 * 1e3
+        gfx950.dense_attention(q, k, v)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            gfx950.dense_attention(q, k, v)
+        torch.cuda.synchronize()
+        own_ms = (time.perf_counter() - t0) / 3 * 1e3
+        dense_flops = 4.0 * L * L * D * H
+        result["dense"] = {"torch_sdpa_ms_per_layer": round(2 * sdpa_ms, 3),
+                           "own_dense_ms_per_layer": round(2 * own_ms, 3),
+                           "torch_sdpa_tflops": round(dense_flops / (sdpa_ms * 1e-3) / 1e12, 1),
+                           "own_dense_tflops": round(dense_flops / (own_ms * 1e-3) / 1e12, 1),
+                           "speedup_vs_sdpa": round(2 * sdpa_ms / ms_layer, 2)}
+    if not args.no_cpu:
+        c0, c1 = branches[0][0], None
+        result["cpu_baseline"] = cpu_baseline(*c0, attn, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()
