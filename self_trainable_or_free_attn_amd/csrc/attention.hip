@@ -17,9 +17,10 @@
 #include "../../include/echosparse_hip.h"
 #include "common.h"
 
+#include <type_traits>
+
 namespace es {
 
-constexpr int LISTCAP = 2048;  // stream ids staged in LDS; ids past it are read from global memory
 enum { FIXED = 0, ONLINE = 1, COMPENSATE = 2 };
 
 struct AttnArgs {
@@ -47,19 +48,16 @@ struct AttnArgs {
   float threshold, tail_log2, scale;
 };
 
-template <int MODE, bool COMP>
-struct Stream {
-  int n, nm, nr, cm, nc, staged;
-  const int* g_exact;
-  const int* g_means;
-  const int* g_refine;
+// Per-lane prefetched sources of one chunk: the ids of this lane's four load rows and (wave 0) of its bias row.
+struct ChunkIds {
+  int row[4];  // exact: token block id (uniform); mean: mean block id; rep: rep row h-relative; -1 = padding
+  int brow;    // the same for bias row = lane (wave 0)
 };
 
 template <int MODE, bool COMP, bool MASS>
 __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char kv_s[2][2][BK * 256];
   __shared__ __attribute__((aligned(16))) float bias_s[2][BK];
-  __shared__ int list_s[LISTCAP];
   __shared__ float mass_s[4][128];
 
   // XCD-aware tile order: dispatch slot w runs on XCD w % 8; each XCD walks a contiguous run of tiles of one head
@@ -75,8 +73,9 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, hi = l >> 5, lq = l & 31;
   const int row = t * BM + wv * 32 + lq;
   const bool rvalid = row < L;
+  const size_t nb4 = (size_t)(nb + 1) * 4;
 
-  // ---------------------------------------------------------------- column stream and its staged ids
+  // ---------------------------------------------------------------- the column stream
   int n = 0, nm = 0, nr = 0;
   const int* g_ex = nullptr;
   const int* g_me = nullptr;
@@ -97,77 +96,97 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   }
   const int cm = (nm + BK - 1) / BK, cr = (4 * nr + BK - 1) / BK;
   const int nc = MODE == COMPENSATE ? (nb + BK - 1) / BK : n + (COMP ? cm + cr : 0);
-  const int ntot = n + nm + nr;
-  if (g_ex != nullptr || COMP) {
-    for (int i = tid; i < min(ntot, LISTCAP); i += 256)
-      list_s[i] = i < n ? g_ex[i] : i < n + nm ? g_me[i - n] : g_rf[i - n - nm];
-  }
-  __syncthreads();
-  auto stream_id = [&](int i) -> int {
-    if (i < LISTCAP) return list_s[i];
-    return i < n ? g_ex[i] : i < n + nm ? g_me[i - n] : g_rf[i - n - nm];
-  };
-  auto exact_id = [&](int j) -> int { return a.blocks == nullptr ? j : stream_id(j); };
+  const bool tail_block = (L & (BK - 1)) != 0;
 
-  // source rows of chunk cj: row R of the chunk -> (k row, v row) pointers
-  auto row_src = [&](int cj, int R, const bf16_t*& ks, const bf16_t*& vs) {
-    if (MODE == COMPENSATE) {
-      int b = cj * BK + R;
-      b = b < nb ? b : 0;
-      size_t o = ((size_t)b * H + h) * HD;
-      ks = a.k_mean + o;
-      vs = a.v_mean + o;
-    } else if (cj < n) {
-      int key = exact_id(cj) * BK + R;
-      key = key < L ? key : L - 1;
-      size_t o = ((size_t)key * H + h) * HD;
-      ks = a.k + o;
-      vs = a.v + o;
-    } else if (cj < n + cm) {
-      int col = (cj - n) * BK + R;
-      int b = col < nm ? stream_id(n + col) : 0;
-      size_t o = ((size_t)b * H + h) * HD;
-      ks = a.k_mean + o;
-      vs = a.v_mean + o;
-    } else {
-      int col = (cj - n - cm) * BK + R;
-      int b = col < 4 * nr ? stream_id(n + nm + (col >> 2)) : nb;
-      size_t o = ((size_t)h * (nb + 1) * 4 + (size_t)b * 4 + (col & 3)) * HD;
-      ks = a.k_rep + o;
-      vs = a.v_rep + o;
-    }
-  };
-  // additive log2 bias of column R of chunk cj (-inf masks the column)
-  auto col_bias = [&](int cj, int R) -> float {
-    if (MODE == COMPENSATE) {
-      int b = cj * BK + R;
-      if (b >= nb) return -INFINITY;
-      if (a.keep[((size_t)h * a.nq + t) * nb + b] != 0) return -INFINITY;
-      return b == nb - 1 ? a.tail_log2 : 6.0f;
-    } else if (cj < n) {
-      return exact_id(cj) * BK + R < L ? 0.0f : -INFINITY;
-    } else if (cj < n + cm) {
-      int col = (cj - n) * BK + R;
-      if (col >= nm) return -INFINITY;
-      return stream_id(n + col) == nb - 1 ? a.tail_log2 : 6.0f;
-    } else {
-      int col = (cj - n - cm) * BK + R;
-      if (col >= 4 * nr) return -INFINITY;
-      int b = stream_id(n + nm + (col >> 2));
-      return a.log_counts[(size_t)h * (nb + 1) * 4 + (size_t)b * 4 + (col & 3)];
-    }
-  };
-  // stage chunk cj into buffer sb: 16 instructions of 1 KB for K and 16 for V, 4 + 4 per wave
-  auto issue = [&](int cj, int sb) {
+  // Loads go through buffer resources (32-bit offsets; offsets past the end read as zero). Token tensors and the
+  // mean table are row-strided by H * 256 bytes from this head's first row; representatives are contiguous rows.
+  const unsigned hstride = (unsigned)H * HD * 2;
+  const rsrc_t rk = make_rsrc(a.k + (size_t)h * HD, (unsigned)(((size_t)L * H - h) * HD * 2));
+  const rsrc_t rv = make_rsrc(a.v + (size_t)h * HD, (unsigned)(((size_t)L * H - h) * HD * 2));
+  rsrc_t rkm = rk, rvm = rv, rkr = rk, rvr = rv;
+  if (COMP || MODE == COMPENSATE) {
+    rkm = make_rsrc(a.k_mean + (size_t)h * HD, (unsigned)(((size_t)nb * H - h) * HD * 2));
+    rvm = make_rsrc(a.v_mean + (size_t)h * HD, (unsigned)(((size_t)nb * H - h) * HD * 2));
+  }
+  if (COMP) {
+    rkr = make_rsrc(a.k_rep + (size_t)h * nb4 * HD, (unsigned)(nb4 * HD * 2));
+    rvr = make_rsrc(a.v_rep + (size_t)h * nb4 * HD, (unsigned)(nb4 * HD * 2));
+  }
+  // this lane's four load rows R_i = 16 wv + 4 i + l / 16 and its swizzled 16-byte chunk within them
+  const int rbase = wv * 16 + (l >> 4);
+  unsigned chb[4], tok_off[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int P = (wv * 4 + i) * 64 + l;  // 16-byte position in the 16 KB tile
-      const int R = P >> 4, c = (P & 15) ^ swz(R);
-      const bf16_t *ks, *vs;
-      row_src(cj, R, ks, vs);
-      g2lds16(ks + c * 8, kv_s[sb][0] + (wv * 4 + i) * 1024);
-      g2lds16(vs + c * 8, kv_s[sb][1] + (wv * 4 + i) * 1024);
+  for (int i = 0; i < 4; ++i) {
+    const int P = (wv * 4 + i) * 64 + l, R = P >> 4;
+    chb[i] = (unsigned)(((P & 15) ^ swz(R)) * 16);
+    tok_off[i] = (unsigned)R * hstride + chb[i];
+  }
+
+  auto fetch = [&](int cj, ChunkIds& c) {
+    if (cj >= nc || MODE == COMPENSATE) return;
+    if (cj < n) {
+      c.row[0] = g_ex == nullptr ? cj : sload(g_ex + cj);
+    } else if (cj < n + cm) {
+      const int c0 = (cj - n) * BK;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int col = c0 + rbase + 4 * i;
+        c.row[i] = col < nm ? g_me[col] : -1;
+      }
+      c.brow = (wv == 0 && c0 + l < nm) ? g_me[c0 + l] : -1;
+    } else {
+      const int c0 = (cj - n - cm) * BK;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int col = c0 + rbase + 4 * i;
+        c.row[i] = col < 4 * nr ? g_rf[col >> 2] * 4 + (col & 3) : -1;
+      }
+      const int col = c0 + l;
+      c.brow = (wv == 0 && col < 4 * nr) ? g_rf[col >> 2] * 4 + (col & 3) : -1;
     }
+  };
+  // stage chunk cj into buffer sb (16 + 16 one-KB instructions, 4 + 4 per wave); returns wave 0's bias value
+  auto issue = [&](int cj, const ChunkIds& c, int sb) -> float {
+    char* kd = kv_s[sb][0] + wv * 4096;
+    char* vd = kv_s[sb][1] + wv * 4096;
+    float bias = 0.0f;
+    if (MODE == COMPENSATE || cj < n) {
+      // 64 consecutive rows: token block b (exact) or mean blocks 64 cj .. (compensation)
+      const int b0 = MODE == COMPENSATE ? cj * BK : c.row[0] * BK;
+      const unsigned soff = (unsigned)b0 * hstride;
+      const rsrc_t r1 = MODE == COMPENSATE ? rkm : rk, r2 = MODE == COMPENSATE ? rvm : rv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        buf2lds16(r1, kd + i * 1024, tok_off[i], soff);
+        buf2lds16(r2, vd + i * 1024, tok_off[i], soff);
+      }
+      if (wv == 0) {
+        if (MODE == COMPENSATE) {
+          const int b = b0 + l;
+          bias = (b < nb && a.keep[((size_t)h * a.nq + t) * nb + b] == 0) ? (b == nb - 1 ? a.tail_log2 : 6.0f)
+                                                                           : -INFINITY;
+        } else {
+          bias = b0 + l < L ? 0.0f : -INFINITY;
+        }
+      }
+    } else {
+      const bool mean = cj < n + cm;
+      const rsrc_t r1 = mean ? rkm : rkr, r2 = mean ? rvm : rvr;
+      const unsigned stride = mean ? hstride : (unsigned)HD * 2;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const unsigned off = c.row[i] < 0 ? 0x80000000u : (unsigned)c.row[i] * stride + chb[i];
+        buf2lds16(r1, kd + i * 1024, off, 0);
+        buf2lds16(r2, vd + i * 1024, off, 0);
+      }
+      if (wv == 0) {
+        if (mean)
+          bias = c.brow < 0 ? -INFINITY : c.brow == nb - 1 ? a.tail_log2 : 6.0f;
+        else
+          bias = c.brow < 0 ? -INFINITY : a.log_counts[(size_t)h * nb4 + c.brow];
+      }
+    }
+    return bias;
   };
 
   // ---------------------------------------------------------------- per-lane query state
@@ -184,51 +203,58 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   const float nprior = rvalid ? -pr : -INFINITY;
   const float scale = a.scale;
 
+  // loop-invariant LDS offsets. K (A operand of S^T): row 32 mb + lq, chunk 2 ks + hi; the swizzle only sees the
+  // low 4 row bits, so the mb = 1 rows sit 8 KB further. V^T (transposed reads): row block kk adds 4 KB.
+  int koff[8];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) koff[ks] = tile_off(lq, 2 * ks + hi);
+  int voff[2][4];  // [first / second four keys of the slot group][channel block]; rows 8 apart differ in swizzle
+  {
+    const int g1 = (l >> 4) & 1, sub = (l & 1) * 8;
+    const int rowA = 4 * hi + ((l & 15) >> 2);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      voff[0][db] = tile_off(rowA, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
+      voff[1][db] = tile_off(rowA + 8, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
+    }
+  }
+
   f32x16 o[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) o[db] = f32x16{};
   float lsum = 0.0f;        // this lane's share of the row sum (its 32 keys of every chunk)
   float mrun = -INFINITY;   // ONLINE running max (same in both half-waves)
 
-  if (nc > 0) {
-    issue(0, 0);
-    if (wv == 0) bias_s[0][l] = col_bias(0, l);
-  }
-  wait_vmem();
-  __syncthreads();
-
-  for (int j = 0; j < nc; ++j) {
-    const int sb = j & 1;
-    float bnext = 0.0f;
-    if (j + 1 < nc) {
-      issue(j + 1, sb ^ 1);
-      if (wv == 0) bnext = col_bias(j + 1, l);
-    }
+  // one chunk: S^T, exponentials (with or without per-column bias), mass, O^T += V^T P^T
+  auto compute = [&](int j, int sb, auto biased_tag) {
+    constexpr bool BIASED = decltype(biased_tag)::value;
     const char* kb = kv_s[sb][0];
     const char* vb = kv_s[sb][1];
-
-    // S^T = K Q^T for the chunk's 64 keys (two 32-key C tiles)
     f32x16 s0 = {}, s1 = {};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-      bf16x8 a0 = lds_read16(kb, tile_off(lq, 2 * ks + hi));
-      bf16x8 a1 = lds_read16(kb, tile_off(32 + lq, 2 * ks + hi));
-      s0 = mfma32(a0, qreg[ks], s0);
-      s1 = mfma32(a1, qreg[ks], s1);
+      s0 = mfma32(lds_read16(kb, koff[ks]), qreg[ks], s0);
+      s1 = mfma32(lds_read16(kb + 8192, koff[ks]), qreg[ks], s1);
     }
     float p[32];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x4 b0 = *reinterpret_cast<const f32x4*>(&bias_s[sb][8 * i + 4 * hi]);
-      f32x4 b1 = *reinterpret_cast<const f32x4*>(&bias_s[sb][32 + 8 * i + 4 * hi]);
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        p[4 * i + jj] = fmaf(s0[4 * i + jj], scale, b0[jj]);
-        p[16 + 4 * i + jj] = fmaf(s1[4 * i + jj], scale, b1[jj]);
-      }
+    for (int r = 0; r < 16; ++r) {
+      p[r] = s0[r];
+      p[16 + r] = s1[r];
     }
-    float csum = 0.0f;
+    if (BIASED) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bias_s[sb][8 * i + 4 * hi]);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) p[4 * i + jj] = fmaf(p[4 * i + jj], scale, b4[jj]) + nprior;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 32; ++r) p[r] = fmaf(p[r], scale, nprior);
+    }
     if (MODE == ONLINE) {
+      // nprior is 0 in ONLINE mode: p holds the scaled logits here
       float mx = -INFINITY;
 #pragma unroll
       for (int r = 0; r < 32; ++r) mx = fmaxf(mx, p[r]);
@@ -237,11 +263,8 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
       const float msub = mnew == -INFINITY ? 0.0f : mnew;
       const float alpha = exp2f_fast(mrun - msub);
 #pragma unroll
-      for (int r = 0; r < 32; ++r) {
-        p[r] = exp2f_fast(p[r] - msub);
-        csum += p[r];
-      }
-      lsum = lsum * alpha + csum;
+      for (int r = 0; r < 32; ++r) p[r] = exp2f_fast(p[r] - msub);
+      lsum *= alpha;
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -249,37 +272,50 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
       mrun = mnew;
     } else {
 #pragma unroll
-      for (int r = 0; r < 32; ++r) {
-        float x = p[r] + nprior;
-        if (MODE == COMPENSATE) x = fminf(x, 100.0f);
-        p[r] = exp2f_fast(x);
-        csum += p[r];
-      }
-      lsum += csum;
+      for (int r = 0; r < 32; ++r) p[r] = exp2f_fast(MODE == COMPENSATE ? fminf(p[r], 100.0f) : p[r]);
     }
-    if (MODE == FIXED && MASS && j < n) {
-      const float bs = wave_sum(csum);
-      if (l == 0) mass_s[wv][j & 127] = bs;
-    }
-
-    // O^T += V^T P^T: P^T (keys x queries) is the B operand straight from the exponentiated registers
     bf16x8 pk[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) pk[kk] = pack8(&p[(kk >> 1) * 16 + (kk & 1) * 8]);
-    const int g1 = (l >> 4) & 1;
+    float csum = 0.0f;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int rowA = (kk >> 1) * 32 + (kk & 1) * 16 + 4 * hi + ((l & 15) >> 2);
+    for (int kk = 0; kk < 4; ++kk) csum = sum8_bf16(pk[kk], csum);
+    lsum += csum;
+    if (MODE == FIXED && MASS && j < n) {
+      const float bs = wave_sum_dpp(csum);
+      if (l == 0) mass_s[wv][j & 127] = bs;
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const int c = 4 * db + 2 * g1 + ((l & 3) >> 1);
-        const int sub = (l & 1) * 8;
-        s16x4 ta = lds_read_tr(vb, tile_off(rowA, c) + sub);
-        s16x4 tb = lds_read_tr(vb, tile_off(rowA + 8, c) + sub);
+        const s16x4 ta = lds_read_tr(vb + 4096 * kk, voff[0][db]);
+        const s16x4 tb = lds_read_tr(vb + 4096 * kk, voff[1][db]);
         o[db] = mfma32(cat_tr(ta, tb), pk[kk], o[db]);
       }
-    }
+  };
 
+  ChunkIds cur = {}, nxt = {};
+  fetch(0, cur);
+  if (nc > 0) {
+    const float b0 = issue(0, cur, 0);
+    if (wv == 0) bias_s[0][l] = b0;
+  }
+  fetch(1, nxt);
+  wait_vmem();
+  __syncthreads();
+
+  for (int j = 0; j < nc; ++j) {
+    const int sb = j & 1;
+    float bnext = 0.0f;
+    if (j + 1 < nc) bnext = issue(j + 1, nxt, sb ^ 1);
+    ChunkIds nn = {};
+    fetch(j + 2, nn);
+    const bool biased = MODE == COMPENSATE || j >= n || (tail_block && cur.row[0] == nb - 1);
+    if (!COMP || biased)   // (non-COMP variants: one instantiation keeps them within 256 VGPRs)
+      compute(j, sb, std::true_type{});
+    else
+      compute(j, sb, std::false_type{});
     if (j + 1 < nc && wv == 0) bias_s[sb ^ 1][l] = bnext;
     wait_vmem();
     __syncthreads();
@@ -287,51 +323,42 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
       const int idx = (j & ~63) + tid;
       if (idx <= j) {
         const float m = mass_s[0][idx & 127] + mass_s[1][idx & 127] + mass_s[2][idx & 127] + mass_s[3][idx & 127];
-        a.mass[((size_t)h * a.nq + t) * nb + stream_id(idx)] = m;
+        const int b = g_ex == nullptr ? idx : g_ex[idx];
+        a.mass[((size_t)h * a.nq + t) * nb + b] = m;
       }
     }
+    cur = nxt;
+    nxt = nn;
   }
 
   // ---------------------------------------------------------------- epilogue
   const float tot = lsum + __shfl_xor(lsum, 32, 64);
   bf16_t* orow = a.out + ((size_t)(rvalid ? row : 0) * H + h) * HD;
   float* lrow = a.lse + (size_t)row * H + h;
+  auto store_rows = [&](float inv) {
+    if (!rvalid) return;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ushort4 v4;
+        v4.x = f2bf(o[db][4 * i + 0] * inv);
+        v4.y = f2bf(o[db][4 * i + 1] * inv);
+        v4.z = f2bf(o[db][4 * i + 2] * inv);
+        v4.w = f2bf(o[db][4 * i + 3] * inv);
+        *reinterpret_cast<ushort4*>(orow + 32 * db + 8 * i + 4 * hi) = v4;
+      }
+  };
   if (MODE == FIXED) {
     const float lg = log2f(tot);
     const bool bad = rvalid && !(lg >= -a.threshold && lg <= a.threshold);
     const int any = __syncthreads_or(bad);
-    const float inv = 1.0f / tot;
-    if (rvalid) {
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          ushort4 v4;
-          v4.x = f2bf(o[db][4 * i + 0] * inv);
-          v4.y = f2bf(o[db][4 * i + 1] * inv);
-          v4.z = f2bf(o[db][4 * i + 2] * inv);
-          v4.w = f2bf(o[db][4 * i + 3] * inv);
-          *reinterpret_cast<ushort4*>(orow + 32 * db + 8 * i + 4 * hi) = v4;
-        }
-    }
+    store_rows(1.0f / tot);
     if (hi == 0) *lrow = rvalid ? pr + lg : 1e30f;
     if (tid == 0) a.flags[th] = any;
   } else if (MODE == ONLINE) {
     const bool empty = n == 0;
-    const float inv = empty ? 0.0f : 1.0f / tot;
-    if (rvalid) {
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          ushort4 v4;
-          v4.x = f2bf(o[db][4 * i + 0] * inv);
-          v4.y = f2bf(o[db][4 * i + 1] * inv);
-          v4.z = f2bf(o[db][4 * i + 2] * inv);
-          v4.w = f2bf(o[db][4 * i + 3] * inv);
-          *reinterpret_cast<ushort4*>(orow + 32 * db + 8 * i + 4 * hi) = v4;
-        }
-    }
+    store_rows(empty ? 0.0f : 1.0f / tot);
     if (hi == 0) *lrow = !rvalid ? 1e30f : empty ? -1e30f : mrun + log2f(tot);
   } else {
     const float den = 1.0f + tot;
@@ -368,6 +395,8 @@ static int check_common(const void* q, const void* k, const void* v, int L, int 
   ES_REQUIRE(q && k && v, ES_ERR_INVALID, "q, k and v must be non-null");
   ES_REQUIRE(L > 0 && H > 0, ES_ERR_INVALID, "L and H must be positive");
   ES_REQUIRE(D == HD, ES_ERR_UNSUPPORTED, "head dimension must be 128");
+  ES_REQUIRE((size_t)L * H * D * 2 < (1ull << 31), ES_ERR_UNSUPPORTED,
+             "q / k / v larger than 2 GiB (32-bit buffer offsets)");
   return ES_OK;
 }
 

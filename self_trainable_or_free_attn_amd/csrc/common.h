@@ -21,6 +21,7 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned short bf16_t;  // raw bf16 bits in global memory
 
 #define LDS_PTR(T, p) ((__attribute__((address_space(3))) T*)(p))
@@ -63,6 +64,24 @@ __device__ __forceinline__ void g2lds16(const void* gsrc, char* lds_base) {
   __builtin_amdgcn_global_load_lds(gsrc, LDS_PTR(void, lds_base), 16, 0, 0);
 }
 
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// raw buffer resource over `bytes` bytes from `base` (offsets past it read as zero)
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+// one wave instruction: every lane moves 16 bytes at rsrc + voff + soff to lds_base + 16 * lane
+__device__ __forceinline__ void buf2lds16(rsrc_t r, char* lds_base, unsigned voff, unsigned soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, LDS_PTR(void, lds_base), 16, (int)voff, (int)soff, 0, 0);
+}
+
+// uniform load through the scalar cache (the value must not change during the kernel)
+template <typename T>
+__device__ __forceinline__ T sload(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)(p);
+}
+
 // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima)
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -82,6 +101,33 @@ __device__ __forceinline__ int wave_sum_i(int x) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
   return x;
+}
+
+// DPP lane shuffle with zero fill (bound_ctrl) and a row mask; lanes outside the mask read 0
+template <int CTRL, int ROWMASK = 0xF>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROWMASK, 0xF, true));
+}
+
+// sum over the 64 lanes with DPP row shifts / broadcasts (no LDS traffic); the result is wave-uniform
+__device__ __forceinline__ float wave_sum_dpp(float x) {
+  x += dpp_f<0x111>(x);        // row_shr:1
+  x += dpp_f<0x112>(x);        // row_shr:2
+  x += dpp_f<0x114>(x);        // row_shr:4
+  x += dpp_f<0x118>(x);        // row_shr:8   -> lane 16r + 15 holds row r's sum
+  x += dpp_f<0x142, 0xA>(x);   // row_bcast:15 -> lanes 31, 63 hold rows 0+1, 2+3
+  x += dpp_f<0x143, 0xC>(x);   // row_bcast:31 -> lane 63 holds the total
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
+// sum of the 8 bf16 values of a packed MFMA operand, fp32 accumulate (v_dot2_f32_bf16 against 1.0)
+__device__ __forceinline__ float sum8_bf16(bf16x8 v, float acc) {
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{v[0], v[1]}, one, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{v[2], v[3]}, one, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{v[4], v[5]}, one, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{v[6], v[7]}, one, acc, false);
+  return acc;
 }
 
 __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
