@@ -9,7 +9,9 @@ import os
 
 import torch
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libechosparse_hip.so")
+# ECHOSPARSE_HIP_LIB: load another build of the same ABI (development A/B measurements)
+LIB_PATH = os.environ.get("ECHOSPARSE_HIP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib",
+                                                                "libechosparse_hip.so")
 
 P, I, F, Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
 

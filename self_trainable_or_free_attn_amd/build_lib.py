@@ -15,7 +15,7 @@ LIB = os.path.join(LIBDIR, "libechosparse_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
-         "-packed-fp32-ops", "-Wno-unused-result"]
+         "-packed-fp32-ops", "-Wno-unused-result"] + os.environ.get("ECHOSPARSE_HIP_CFLAGS", "").split()
 
 
 def sources():
@@ -32,25 +32,28 @@ def _compile(src, obj_dir):
     return obj
 
 
-def build(verbose=False):
-    """Compile every source and link the shared library; returns its path."""
-    obj_dir = os.path.join(HERE, "_build")
+def build(verbose=False, out=None):
+    """Compile every source and link the shared library (to `out`, default lib/libechosparse_hip.so); returns its
+    path."""
+    lib_path = out or LIB
+    obj_dir = os.path.join(HERE, "_build", os.path.basename(lib_path))
     os.makedirs(obj_dir, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
     srcs = sources()
     with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(lambda s: _compile(s, obj_dir), srcs))
-    tmp = LIB + ".tmp"
+    os.makedirs(os.path.dirname(lib_path), exist_ok=True)
+    tmp = lib_path + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib_path)
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources")
-    return LIB
+        print(f"built {lib_path} from {len(srcs)} sources")
+    return lib_path
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, out=sys.argv[1] if len(sys.argv) > 1 else None)
     sys.exit(0)

@@ -67,10 +67,11 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   const int t = xcd * a.per_xcd + slot % a.per_xcd;
   if (h >= a.H || t >= a.tiles) return;
   const int th = t * a.H + h;
-  if (MODE != FIXED && a.flags != nullptr && a.flags[th] == 0) return;
+  if (MODE != FIXED && a.flags != nullptr && sload(a.flags + th) == 0) return;
 
   const int L = a.L, H = a.H, nb = a.nb;
-  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, hi = l >> 5, lq = l & 31;
+  const int tid = threadIdx.x, l = tid & 63, hi = l >> 5, lq = l & 31;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, made scalar
   const int row = t * BM + wv * 32 + lq;
   const bool rvalid = row < L;
   const size_t nb4 = (size_t)(nb + 1) * 4;
@@ -85,12 +86,12 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   } else if (a.blocks == nullptr) {
     n = nb;
   } else {
-    n = a.counts[th];
+    n = sload(a.counts + th);
     g_ex = a.blocks + (size_t)th * a.NK;
   }
   if (COMP) {
-    nm = a.mean_counts[th];
-    nr = a.refine_counts[th];
+    nm = sload(a.mean_counts + th);
+    nr = sload(a.refine_counts + th);
     g_me = a.means + (size_t)th * a.NK;
     g_rf = a.refine + (size_t)th * a.RW;
   }
@@ -152,7 +153,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
     float bias = 0.0f;
     if (MODE == COMPENSATE || cj < n) {
       // 64 consecutive rows: token block b (exact) or mean blocks 64 cj .. (compensation)
-      const int b0 = MODE == COMPENSATE ? cj * BK : c.row[0] * BK;
+      const int b0 = MODE == COMPENSATE ? cj * BK : __builtin_amdgcn_readfirstlane(c.row[0]) * BK;
       const unsigned soff = (unsigned)b0 * hstride;
       const rsrc_t r1 = MODE == COMPENSATE ? rkm : rk, r2 = MODE == COMPENSATE ? rvm : rv;
 #pragma unroll
