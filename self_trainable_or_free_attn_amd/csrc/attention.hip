@@ -226,74 +226,96 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   float lsum = 0.0f;        // this lane's share of the row sum (its 32 keys of every chunk)
   float mrun = -INFINITY;   // ONLINE running max (same in both half-waves)
 
-  // one chunk: S^T, exponentials (with or without per-column bias), mass, O^T += V^T P^T
-  auto compute = [&](int j, int sb, auto biased_tag) {
+  // exponentials of one 32-key half (C tile sh of the chunk) packed into two B operands of O^T += V^T P^T;
+  // returns this lane's share of the half's sum. FIXED / COMPENSATE only (fixed offset, no running max).
+  auto half = [&](const f32x16& sh, int boff, bf16x8& pa, bf16x8& pb, auto biased_tag) -> float {
     constexpr bool BIASED = decltype(biased_tag)::value;
+    float p[16];
+    if (BIASED) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bias_s[0][0] + boff + 8 * i + 4 * hi);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) p[4 * i + jj] = fmaf(sh[4 * i + jj], scale, b4[jj]) + nprior;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) p[r] = fmaf(sh[r], scale, nprior);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = exp2f_fast(MODE == COMPENSATE ? fminf(p[r], 100.0f) : p[r]);
+    pa = pack8(&p[0]);
+    pb = pack8(&p[8]);
+    return sum8_bf16(pb, sum8_bf16(pa, 0.0f));
+  };
+  auto pv = [&](const char* vb, int kk, const bf16x8& pk) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const s16x4 ta = lds_read_tr(vb + 4096 * kk, voff[0][db]);
+      const s16x4 tb = lds_read_tr(vb + 4096 * kk, voff[1][db]);
+      o[db] = mfma32(cat_tr(ta, tb), pk, o[db]);
+    }
+  };
+
+  // one chunk. FIXED / COMPENSATE: two 32-key halves, so the matrix cores compute S^T of the second half while
+  // the VALU exponentiates the first, and O^T += V^T P^T of the first half while the VALU does the second.
+  // ONLINE: the running maximum needs all 64 keys first.
+  auto compute = [&](int j, int sb, auto biased_tag) {
     const char* kb = kv_s[sb][0];
     const char* vb = kv_s[sb][1];
     f32x16 s0 = {}, s1 = {};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      s0 = mfma32(lds_read16(kb, koff[ks]), qreg[ks], s0);
-      s1 = mfma32(lds_read16(kb + 8192, koff[ks]), qreg[ks], s1);
+    for (int ks = 0; ks < 8; ++ks) s0 = mfma32(lds_read16(kb, koff[ks]), qreg[ks], s0);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) s1 = mfma32(lds_read16(kb + 8192, koff[ks]), qreg[ks], s1);
+    if (MODE != ONLINE) {
+      bf16x8 pk0, pk1, pk2, pk3;
+      float csum = half(s0, sb * BK, pk0, pk1, biased_tag);
+      pv(vb, 0, pk0);
+      pv(vb, 1, pk1);
+      csum += half(s1, sb * BK + 32, pk2, pk3, biased_tag);
+      pv(vb, 2, pk2);
+      pv(vb, 3, pk3);
+      lsum += csum;
+      if (MODE == FIXED && MASS && j < n) {
+        const float bs = wave_sum_dpp(csum);
+        if (l == 0) mass_s[wv][j & 127] = bs;
+      }
+      return;
     }
     float p[32];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      p[r] = s0[r];
-      p[16 + r] = s1[r];
+    for (int i = 0; i < 8; ++i) {
+      const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bias_s[sb][8 * i + 4 * hi]);
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+        p[4 * i + jj] = fmaf(i < 4 ? s0[4 * i + jj] : s1[4 * (i - 4) + jj], scale, b4[jj]) + nprior;
     }
-    if (BIASED) {
+    // nprior is 0 in ONLINE mode: p holds the scaled logits here
+    float mx = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bias_s[sb][8 * i + 4 * hi]);
+    for (int r = 0; r < 32; ++r) mx = fmaxf(mx, p[r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mnew = fmaxf(mrun, mx);
+    const float msub = mnew == -INFINITY ? 0.0f : mnew;
+    const float alpha = exp2f_fast(mrun - msub);
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) p[4 * i + jj] = fmaf(p[4 * i + jj], scale, b4[jj]) + nprior;
-      }
-    } else {
+    for (int r = 0; r < 32; ++r) p[r] = exp2f_fast(p[r] - msub);
+    lsum *= alpha;
 #pragma unroll
-      for (int r = 0; r < 32; ++r) p[r] = fmaf(p[r], scale, nprior);
-    }
-    if (MODE == ONLINE) {
-      // nprior is 0 in ONLINE mode: p holds the scaled logits here
-      float mx = -INFINITY;
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int r = 0; r < 32; ++r) mx = fmaxf(mx, p[r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(mrun, mx);
-      const float msub = mnew == -INFINITY ? 0.0f : mnew;
-      const float alpha = exp2f_fast(mrun - msub);
-#pragma unroll
-      for (int r = 0; r < 32; ++r) p[r] = exp2f_fast(p[r] - msub);
-      lsum *= alpha;
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-      mrun = mnew;
-    } else {
-#pragma unroll
-      for (int r = 0; r < 32; ++r) p[r] = exp2f_fast(MODE == COMPENSATE ? fminf(p[r], 100.0f) : p[r]);
-    }
+      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+    mrun = mnew;
     bf16x8 pk[4];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) pk[kk] = pack8(&p[(kk >> 1) * 16 + (kk & 1) * 8]);
+    for (int kk = 0; kk < 4; ++kk) pk[kk] = pack8(&p[kk * 8]);
     float csum = 0.0f;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) csum = sum8_bf16(pk[kk], csum);
     lsum += csum;
-    if (MODE == FIXED && MASS && j < n) {
-      const float bs = wave_sum_dpp(csum);
-      if (l == 0) mass_s[wv][j & 127] = bs;
-    }
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const s16x4 ta = lds_read_tr(vb + 4096 * kk, voff[0][db]);
-        const s16x4 tb = lds_read_tr(vb + 4096 * kk, voff[1][db]);
-        o[db] = mfma32(cat_tr(ta, tb), pk[kk], o[db]);
-      }
+    for (int kk = 0; kk < 4; ++kk) pv(vb, kk, pk[kk]);
   };
 
   ChunkIds cur = {}, nxt = {};
