@@ -274,7 +274,7 @@ def select_blocks(mass, keep_prev, scale_exact, scale_skip, flags, k, r, L, refi
     kernel does it. Returns keep (H,nq,nb) u8, counts (nq,H), blocks (nq,H,nb) (entries past the count are 0),
     refine (nq,H,RW) padded with nb, skip (H,nq,words) int32 (words past next_pow2(nb)/32 are -1)."""
     H, nq, nb = mass.shape
-    nbp = next_pow2(nb)
+    nbp = max(32, next_pow2(nb))       # (the reference needs nb >= 32; shorter maps use one word)
     keep = np.zeros((H, nq, nb), np.uint8)
     counts = np.zeros((nq, H), np.int32)
     blocks = np.zeros((nq, H, nb), np.int32)
@@ -333,7 +333,7 @@ def pack_plan(keep, words):
     echosparse/kernels/sm120.py:258-273). Words past next_pow2(nb)/32 are not written by the reference; they are
     -1 here (the plans' initial value)."""
     H, nq, nb = keep.shape
-    nbp = next_pow2(nb)
+    nbp = max(32, next_pow2(nb))
     out = np.full((H, nq, words), -1, np.int32)
     for h in range(H):
         for t in range(nq):

@@ -473,7 +473,7 @@ extern "C" int es_sparse_attention(const void* q, const void* k, const void* v, 
   int st = check_common(q, k, v, L, H, D);
   if (st) return st;
   ES_REQUIRE(out && counts && blocks && offset && lse && flags && k_mean && v_mean && means && mean_counts &&
-                 refine && refine_counts && k_rep && v_rep && log_counts,
+                 (refine || rw == 0) && refine_counts && k_rep && v_rep && log_counts,
              ES_ERR_INVALID, "null tensor pointer");
   AttnArgs a = base_args(q, k, v, L, H);
   ES_REQUIRE(nk >= 1 && rw >= 0, ES_ERR_INVALID, "bad list widths");

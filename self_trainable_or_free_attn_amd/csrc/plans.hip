@@ -271,7 +271,7 @@ extern "C" int es_select_blocks(const float* mass, const uint8_t* keep_prev, con
                                 int* skip_bits, int nw, int* refine, int rw, int k, int r, int L, int H, int sink,
                                 hipStream_t stream) {
   ES_REQUIRE(mass && keep_prev && scale_exact && scale_skip && keep && counts && blocks && flags && skip_bits &&
-                 refine,
+                 (refine || rw == 0),
              ES_ERR_INVALID, "null tensor pointer");
   ES_REQUIRE(L > 0 && H > 0, ES_ERR_INVALID, "L and H must be positive");
   const int nq = (L + BM - 1) / BM, nb = (L + BK - 1) / BK, nbp = next_pow2(nb);
@@ -308,7 +308,8 @@ extern "C" int es_pack_plan(const uint8_t* keep, int* exact_bits, int nw, int H,
 extern "C" int es_rebuild_plan(const int* exact_bits, const int* skip_bits, int nw, uint8_t* keep, int* counts,
                                int* blocks, int* refine, int* refine_counts, int rw, int* means, int* mean_counts,
                                int H, int nq, int nb, hipStream_t stream) {
-  ES_REQUIRE(exact_bits && skip_bits && keep && counts && blocks && refine && refine_counts && means && mean_counts,
+  ES_REQUIRE(exact_bits && skip_bits && keep && counts && blocks && (refine || rw == 0) && refine_counts && means &&
+                 mean_counts,
              ES_ERR_INVALID, "null tensor pointer");
   const int nwords = max(1, next_pow2(nb) / 32);
   ES_REQUIRE(nw >= nwords, ES_ERR_INVALID, "bit plans have too few words per tile");

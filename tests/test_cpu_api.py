@@ -1,0 +1,136 @@
+"""Host logic and the C ABI without a GPU: backend resolution, the per-layer state sizes the reference pins, and that
+libechosparse_hip.so loads and exports every entry point include/echosparse_hip.h declares (no compute calls)."""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+import types
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture
+def arch(monkeypatch):
+    def set_arch(name):
+        props = types.SimpleNamespace(gcnArchName=name)
+        monkeypatch.setattr(torch.cuda, "get_device_properties", lambda device=None: props)
+    return set_arch
+
+
+def test_auto_follows_the_device(arch):
+    from self_trainable_or_free_attn_amd import backends
+    arch("gfx950:sramecc+:xnack-")
+    assert backends.resolve("auto", "cuda:0") == "mi355x"
+    assert backends.resolve("mi355x", torch.device("cuda", 0)) == "mi355x"
+
+
+def test_mismatch_and_unsupported_devices_fail(arch):
+    from self_trainable_or_free_attn_amd import backends
+    arch("gfx942")
+    with pytest.raises(RuntimeError, match="gpu='mi355x' needs architecture gfx950, but cuda:0 is gfx942"):
+        backends.resolve("mi355x", "cuda:0")
+    with pytest.raises(RuntimeError, match="is gfx942; EchoSparse on ROCm supports gfx950"):
+        backends.resolve("auto", "cuda:0")
+    with pytest.raises(ValueError, match="GPU tensors"):
+        backends.resolve("auto", "cpu")
+    with pytest.raises(ValueError, match="gpu must be"):
+        backends.resolve("h100", "cuda:0")
+
+
+def test_attention_resolves_at_the_first_call():
+    from self_trainable_or_free_attn_amd import EchoSparseAttention
+    attn = EchoSparseAttention(gpu="mi355x")
+    assert attn.backend is None
+    q = torch.zeros(1, 128, 1, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        attn(q, q, q, step=0, branch=0, layer=0)
+    with pytest.raises(ValueError, match="gpu must be"):
+        EchoSparseAttention(gpu="5090")
+    with pytest.raises(AssertionError):
+        EchoSparseAttention(dense_steps=1)
+
+
+def test_import_does_not_load_kernels():
+    code = ("import sys; sys.path.insert(0, %r); import self_trainable_or_free_attn_amd; "
+            "print(any(m.endswith('kernels.gfx950') or m.endswith('._lib') for m in sys.modules))" % ROOT)
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, check=True).stdout
+    assert out == "False\n"
+
+
+@pytest.mark.parametrize("L, H, layers, branches, expected", [
+    (75600, 40, 39, 2, 1888174080),      # Wan2.1-14B 720p, layers 1-39, CFG
+    (118839, 24, 60, 1, 1369866240),     # HunyuanVideo 720p: 118800 video + 39 text tokens
+    (38247, 56, 49, 1, 630110208),       # MiniMax-H3 768p, layers 1-49
+])
+def test_state_size(L, H, layers, branches, expected):
+    """Persistent per-layer state (offsets of every branch + bit plans) equals the reference's pinned byte counts
+    (reference tests/test_api.py:129-143)."""
+    from self_trainable_or_free_attn_amd.attention import _CompactState
+    st = _CompactState(L, H, "meta")
+    for branch in range(branches):
+        st.offset(branch)
+    for plan in range(branches):
+        st.plan(plan)
+    tensors = [*st.offsets.values(), *(t for p in st.plans for t in p)]
+    assert layers * sum(t.numel() * t.element_size() for t in tensors) == expected
+
+
+def test_budget_matches_reference_rule():
+    from self_trainable_or_free_attn_amd import EchoSparseAttention
+    attn = EchoSparseAttention(density=0.1)
+    assert attn._budget(1182) == (118, 355) and attn._budget(65) == (6, 20)
+    assert EchoSparseAttention(density=1.0)._budget(65) == (65, 0)
+
+
+def declared_entry_points():
+    text = open(os.path.join(ROOT, "include", "echosparse_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(es_[a-z0-9_]+)\s*\(", text)))
+
+
+def library():
+    from self_trainable_or_free_attn_amd import _lib, build_lib
+    if not os.path.exists(_lib.LIB_PATH):
+        build_lib.build()
+    return ctypes.CDLL(_lib.LIB_PATH)
+
+
+def test_library_exports_every_declared_entry_point():
+    names = declared_entry_points()
+    assert len(names) >= 14 and "es_sparse_attention" in names
+    so = library()
+    missing = [n for n in names if not hasattr(so, n)]
+    assert not missing, missing
+    so.es_abi_version.restype = ctypes.c_int
+    assert so.es_abi_version() == 1
+
+
+def test_ctypes_signatures_cover_the_header():
+    """Every stream-taking entry point of the header has an argument list in the binding, with the header's
+    argument count (the binding appends the stream)."""
+    from self_trainable_or_free_attn_amd import _lib
+    text = open(os.path.join(ROOT, "include", "echosparse_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    for name, args in re.findall(r"\b(es_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        n = len([a for a in args.split(",") if a.strip() and a.strip() != "void"])
+        if "hipStream_t" in args:
+            assert name in _lib.SIGNATURES, name
+            assert len(_lib.SIGNATURES[name]) + 1 == n, name
+        else:
+            assert name in _lib.NO_STREAM, name
+
+
+def test_argument_errors_are_reported_without_a_gpu():
+    """Validation runs before any HIP call: a bad head dimension is reported with a message."""
+    so = library()
+    so.es_block_means.restype = ctypes.c_int
+    so.es_last_error_string.restype = ctypes.c_char_p
+    p = ctypes.c_void_p(16)
+    st = so.es_block_means(p, p, p, p, ctypes.c_int(64), ctypes.c_int(1), ctypes.c_int(64), ctypes.c_void_p(0))
+    assert st == 2 and b"head dimension must be 128" in so.es_last_error_string()
+    st = so.es_block_means(None, p, p, p, ctypes.c_int(64), ctypes.c_int(1), ctypes.c_int(128), ctypes.c_void_p(0))
+    assert st == 1 and b"null" in so.es_last_error_string()
