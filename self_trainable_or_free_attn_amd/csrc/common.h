@@ -120,6 +120,21 @@ __device__ __forceinline__ float wave_sum_dpp(float x) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
 }
 
+// max over the 64 lanes (DPP; lanes without a source keep their own value)
+template <int CTRL, int ROWMASK = 0xF>
+__device__ __forceinline__ float dpp_keep(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), CTRL, ROWMASK, 0xF, false));
+}
+__device__ __forceinline__ float wave_max_dpp(float x) {
+  x = fmaxf(x, dpp_keep<0x111>(x));
+  x = fmaxf(x, dpp_keep<0x112>(x));
+  x = fmaxf(x, dpp_keep<0x114>(x));
+  x = fmaxf(x, dpp_keep<0x118>(x));
+  x = fmaxf(x, dpp_keep<0x142, 0xA>(x));
+  x = fmaxf(x, dpp_keep<0x143, 0xC>(x));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
 // sum of the 8 bf16 values of a packed MFMA operand, fp32 accumulate (v_dot2_f32_bf16 against 1.0)
 __device__ __forceinline__ float sum8_bf16(bf16x8 v, float acc) {
   const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};

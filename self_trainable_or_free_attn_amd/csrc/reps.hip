@@ -105,17 +105,22 @@ __global__ __launch_bounds__(256) void gram_kernel(const bf16_t* __restrict__ q,
     }
 }
 
+// sum of the split partials of one head's Gram matrix, in split order, into the split-0 slot
+__global__ __launch_bounds__(256) void gram_reduce_kernel(float* __restrict__ gram, int splits) {
+  const int h = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+  float* g = gram + (size_t)h * splits * HD * HD + i;
+  float s = 0.0f;
+  for (int sp = 0; sp < splits; ++sp) s += g[(size_t)sp * HD * HD];
+  g[0] = s;
+}
+
 __global__ __launch_bounds__(256) void chol_kernel(const float* __restrict__ gram, bf16_t* __restrict__ metric_t,
                                                    int splits, float gscale) {
   __shared__ float A[HD][HD + 1];
-  __shared__ float col[HD];
   __shared__ float red[4];
   const int h = blockIdx.x, tid = threadIdx.x;
-  for (int i = tid; i < HD * HD; i += 256) {
-    float s = 0.0f;
-    for (int sp = 0; sp < splits; ++sp) s += gram[((size_t)h * splits + sp) * HD * HD + i];
-    A[i / HD][i % HD] = s * gscale;
-  }
+  // the split partials were summed into split 0 by gram_reduce_kernel
+  for (int i = tid; i < HD * HD; i += 256) A[i / HD][i % HD] = gram[(size_t)h * splits * HD * HD + i] * gscale;
   __syncthreads();
   float dsum = tid < HD ? A[tid][tid] : 0.0f;
   dsum = wave_sum(dsum);
@@ -131,17 +136,29 @@ __global__ __launch_bounds__(256) void chol_kernel(const float* __restrict__ gra
   __syncthreads();
   const float eps = (red[0] + red[1]) / (float)HD * 1e-12f;
   bf16_t* mt = metric_t + (size_t)h * HD * HD;
+  // Register-resident right-looking factorisation: thread (cc = tid % 128, r0 = tid / 128) holds column cc at
+  // rows r0, r0 + 2, ... Each step the owners of column j publish it, everyone reads the pivot and subtracts the
+  // rank-1 update from its own entries.
+  const int cc = tid & (HD - 1), r0 = tid >> 7;
+  float a[HD / 2];
+#pragma unroll
+  for (int i = 0; i < HD / 2; ++i) a[i] = A[r0 + 2 * i][cc];
+  __syncthreads();
+  float* colbuf = &A[0][0];  // the matrix now lives in registers; reuse the LDS as the column buffer
   for (int j = 0; j < HD; ++j) {
-    if (tid < HD) {
-      const float piv = fmaxf(A[j][j], eps);
-      const float c = tid >= j ? A[tid][j] / sqrtf(piv) : 0.0f;
-      col[tid] = c;
-      mt[j * HD + tid] = f2bf(c);  // metric_t[e = j][d = tid] = Lchol[tid][j]
+    if (cc == j) {
+#pragma unroll
+      for (int i = 0; i < HD / 2; ++i) colbuf[r0 + 2 * i] = a[i];
     }
     __syncthreads();
-    for (int i = tid; i < HD * HD; i += 256) {
-      const int r = i / HD, c = i % HD;
-      if (r >= j && c >= j) A[r][c] -= col[r] * col[c];
+    const float inv = 1.0f / sqrtf(fmaxf(colbuf[j], eps));
+    const float cv = cc >= j ? colbuf[cc] * inv : 0.0f;
+    if (tid < HD) mt[j * HD + tid] = f2bf(tid >= j ? colbuf[tid] * inv : 0.0f);  // metric_t[j][d] = Lchol[d][j]
+#pragma unroll
+    for (int i = 0; i < HD / 2; ++i) {
+      const int r = r0 + 2 * i;
+      const float cr = r >= j ? colbuf[r] * inv : 0.0f;
+      a[i] = fmaf(-cr, cv, a[i]);
     }
     __syncthreads();
   }
@@ -173,11 +190,13 @@ __global__ __launch_bounds__(256) void kmeans_kernel(const bf16_t* __restrict__ 
                                                      int NB, int iters) {
   __shared__ __attribute__((aligned(16))) char kt[BK * 256];
   __shared__ float X[BK][HD + 1];
-  __shared__ float sp[NPROBE][BK + 1];
+  __shared__ __attribute__((aligned(16))) float sp[NPROBE][BK + 1];  // probe logits, then the V tile
+  __shared__ float wpart[4][BK];
   __shared__ float wgt[BK];
   __shared__ float cen[4][HD];
   __shared__ float cw[4];
-  __shared__ float dist[BK][4];
+  __shared__ float part[4][BK][9];
+  char* vt = reinterpret_cast<char*>(&sp[0][0]);
   __shared__ int lab[BK];
   __shared__ int red_i[4];
   __shared__ float cnt_s[4];
@@ -223,95 +242,113 @@ __global__ __launch_bounds__(256) void kmeans_kernel(const bf16_t* __restrict__ 
     for (int r = 0; r < 16; ++r) sp[32 * pb + 8 * (r / 4) + 4 * hi + (r % 4)][32 * tb + lq] = acc[r];
   }
   __syncthreads();
-  if (tid < NPROBE) {  // softmax of probe tid over the valid tokens (natural exponent)
-    float m = -INFINITY;
-    for (int t = 0; t < nvalid; ++t) m = fmaxf(m, sp[tid][t]);
-    float s = 0.0f;
-    for (int t = 0; t < nvalid; ++t) {
-      const float e = expf(sp[tid][t] - m);
-      sp[tid][t] = e;
-      s += e;
+  // probe softmax weights: wave wv takes probes 16 wv .. 16 wv + 15, lane = token
+  {
+    const bool tv = l < nvalid;
+    float wpart_l = 0.0f;
+    for (int p = 16 * wv; p < 16 * wv + 16; ++p) {
+      const float x = tv ? sp[p][l] : -INFINITY;
+      const float m = wave_max_dpp(x);
+      const float e = tv ? exp2f_fast((x - m) * LOG2E) : 0.0f;
+      wpart_l += e / wave_sum_dpp(e);
     }
-    const float inv = 1.0f / s;
-    for (int t = 0; t < nvalid; ++t) sp[tid][t] *= inv;
+    wpart[wv][l] = wpart_l;
   }
   __syncthreads();
+  stage_rows(v, j * BK, L, H, h, vt);  // the V tile lands while the clustering runs
   if (tid < BK) {
-    float s = 0.0f;
-    for (int p = 0; p < NPROBE; ++p) s += tid < nvalid ? sp[p][tid] : 0.0f;
+    const float s = wpart[0][tid] + wpart[1][tid] + wpart[2][tid] + wpart[3][tid];
     wgt[tid] = tid < nvalid ? s * ((float)nvalid / (float)NPROBE) : 0.0f;
     lab[tid] = tid / (BK / 4);
   }
   __syncthreads();
 
-  // centroids of the current labels; cen keeps its old value for an empty (zero-weight) cluster unless `init`
+  // weighted centroids of the current labels: thread -> channel tid % 128, clusters 2 (tid / 128) + {0, 1};
+  // a cluster with zero weight keeps its previous centroid unless `init`
   auto centroids = [&](bool init) {
-    const int c = tid >> 6, e = 2 * (tid & 63);
-    float s0 = 0.f, s1 = 0.f, ws = 0.f;
+    const int e = tid & (HD - 1), c0 = 2 * (tid >> 7);
+    float s0 = 0.f, s1 = 0.f, w0 = 0.f, w1 = 0.f;
+#pragma unroll 4
     for (int t = 0; t < nvalid; ++t) {
-      if (lab[t] == c) {
-        const float w = wgt[t];
-        ws += w;
-        s0 += w * X[t][e];
-        s1 += w * X[t][e + 1];
-      }
+      const int lb = lab[t];
+      const float w = wgt[t], x = X[t][e];
+      const float a0 = lb == c0 ? w : 0.0f, a1 = lb == c0 + 1 ? w : 0.0f;
+      w0 += a0;
+      w1 += a1;
+      s0 = fmaf(a0, x, s0);
+      s1 = fmaf(a1, x, s1);
     }
     __syncthreads();
-    const float d = fmaxf(ws, 1e-6f);
-    if (init || ws > 0.0f) {
-      cen[c][e] = s0 / d;
-      cen[c][e + 1] = s1 / d;
+    if (init || w0 > 0.0f) cen[c0][e] = s0 / fmaxf(w0, 1e-6f);
+    if (init || w1 > 0.0f) cen[c0 + 1][e] = s1 / fmaxf(w1, 1e-6f);
+    if (e == 0) {
+      cw[c0] = w0;
+      cw[c0 + 1] = w1;
     }
-    if ((tid & 63) == 0) cw[c] = ws;
     __syncthreads();
   };
   centroids(true);
   for (int it = 0; it < iters; ++it) {
-    {  // distances: thread (token tid & 63, cluster tid >> 6)
-      const int t = tid & 63, c = tid >> 6;
-      float cc = 0.f, xc = 0.f;
-      for (int e = 0; e < HD; ++e) {
-        const float z = cen[c][e];
-        cc += z * z;
-        xc += X[t][e] * z;
+    {  // partial dots over channels 32 wv .. 32 wv + 31 for token l
+      float d[4] = {0.f, 0.f, 0.f, 0.f}, nn[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+      for (int e = 32 * wv; e < 32 * wv + 32; ++e) {
+        const float x = X[l][e];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float z = cen[c][e];
+          d[c] = fmaf(x, z, d[c]);
+          nn[c] = fmaf(z, z, nn[c]);
+        }
       }
-      dist[t][c] = cw[c] > 0.0f ? cc - 2.0f * xc : INFINITY;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        part[wv][l][c] = d[c];
+        part[wv][l][4 + c] = nn[c];
+      }
     }
     __syncthreads();
-    int changed = 0;
     if (tid < BK) {
       int best = 0;
-      float bd = dist[tid][0];
-      for (int c = 1; c < 4; ++c)
-        if (dist[tid][c] < bd) {
-          bd = dist[tid][c];
+      float bd = INFINITY;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float xc = part[0][tid][c] + part[1][tid][c] + part[2][tid][c] + part[3][tid][c];
+        const float cc = part[0][tid][4 + c] + part[1][tid][4 + c] + part[2][tid][4 + c] + part[3][tid][4 + c];
+        const float dc = cw[c] > 0.0f ? cc - 2.0f * xc : INFINITY;
+        if (c == 0 || dc < bd) {  // first minimum, like argmin
+          bd = dc;
           best = c;
         }
-      changed = (tid < nvalid) && best != lab[tid];
+      }
+      const int changed = wave_sum_i((tid < nvalid) && best != lab[tid]);
       lab[tid] = best;
+      if (tid == 0) red_i[0] = changed;
     }
-    changed = wave_sum_i(changed);
-    if (l == 0) red_i[wv] = changed;
     __syncthreads();
     const int total = red_i[0];
     centroids(false);
     if (total == 0) break;
   }
 
-  // representatives: plain means of K and V over each cluster's valid tokens
+  // representatives: plain means of K and V over each cluster's valid tokens (both tiles in LDS)
+  wait_vmem();
+  __syncthreads();
   {
     const int c = tid >> 6, e = 2 * (tid & 63);
     float k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
     int n = 0;
+#pragma unroll 4
     for (int t = 0; t < nvalid; ++t) {
-      if (lab[t] != c) continue;
-      ++n;
-      const unsigned kw = *reinterpret_cast<const unsigned*>(kt + tile_off(t, e / 8) + (e % 8) * 2);
-      const unsigned vw = *reinterpret_cast<const unsigned*>(v + ((size_t)(j * BK + t) * H + h) * HD + e);
-      k0 += __uint_as_float(kw << 16);
-      k1 += __uint_as_float(kw & 0xffff0000u);
-      v0 += __uint_as_float(vw << 16);
-      v1 += __uint_as_float(vw & 0xffff0000u);
+      const int off = tile_off(t, e / 8) + (e % 8) * 2;
+      const unsigned kw = *reinterpret_cast<const unsigned*>(kt + off);
+      const unsigned vw = *reinterpret_cast<const unsigned*>(vt + off);
+      const float m = lab[t] == c ? 1.0f : 0.0f;
+      n += lab[t] == c;
+      k0 = fmaf(m, __uint_as_float(kw << 16), k0);
+      k1 = fmaf(m, __uint_as_float(kw & 0xffff0000u), k1);
+      v0 = fmaf(m, __uint_as_float(vw << 16), v0);
+      v1 = fmaf(m, __uint_as_float(vw & 0xffff0000u), v1);
     }
     const float inv = 1.0f / fmaxf((float)n, 1.0f);
     const size_t o = ((size_t)h * (NB + 1) * 4 + (size_t)j * 4 + c) * HD + e;
@@ -321,13 +358,14 @@ __global__ __launch_bounds__(256) void kmeans_kernel(const bf16_t* __restrict__ 
     v4[o + 1] = f2bf(v1 * inv);
     if ((tid & 63) == 0) lc4[(size_t)h * (NB + 1) * 4 + (size_t)j * 4 + c] = n > 0 ? log2f((float)n) : -INFINITY;
   }
-  if (MEANS && tid < 128) {  // block means, same arithmetic as means_kernel
-    const bf16_t* src = tid < 64 ? k : v;
+  if (MEANS && tid < 128) {  // block means: the same sequential fp32 sum and division as means_kernel
+    const char* src = tid < 64 ? kt : vt;
     bf16_t* dst = tid < 64 ? km : vm;
     const int e = 2 * (tid & 63);
     float a = 0.f, b = 0.f;
+#pragma unroll 4
     for (int r = 0; r < nvalid; ++r) {
-      const unsigned w = *reinterpret_cast<const unsigned*>(src + ((size_t)(j * BK + r) * H + h) * HD + e);
+      const unsigned w = *reinterpret_cast<const unsigned*>(src + tile_off(r, e / 8) + (e % 8) * 2);
       a += __uint_as_float(w << 16);
       b += __uint_as_float(w & 0xffff0000u);
     }
@@ -361,6 +399,7 @@ extern "C" int es_representatives(const void* q, const void* k, const void* v, v
   const float scale = 1.0f / sqrtf((float)HD);
   hipLaunchKernelGGL(gram_kernel, dim3(w.splits, H), dim3(256), 0, stream, (const bf16_t*)q, w.gram, L, H,
                      w.rows_per_split, w.splits);
+  hipLaunchKernelGGL(gram_reduce_kernel, dim3(HD * HD / 256, H), dim3(256), 0, stream, w.gram, w.splits);
   hipLaunchKernelGGL(chol_kernel, dim3(H), dim3(256), 0, stream, w.gram, w.metric_t, w.splits,
                      scale * scale / (float)L);
   hipLaunchKernelGGL(probe_kernel, dim3(NPROBE, H), dim3(64), 0, stream, (const bf16_t*)q, w.probes, L, H, nb,
