@@ -166,7 +166,7 @@ def main():
                    "mean_mean_columns_per_tile": round(float(ps.mean_counts.double().mean()), 2),
                    "mean_refined_blocks_per_tile": round(float(ps.refine_counts.double().mean()), 2),
                    "executed_tflop_per_layer": round(fl_layer / 1e12, 3)},
-        "roofline": {"kernel": "attn_kernel<FIXED,COMP,MASS> (es_sparse_attention)", "bound": "mfma",
+        "roofline": {"kernel": "attn_kernel<FIXED,COMP,*> (es_sparse_attention, both CFG branches)", "bound": "mfma",
                      "achieved": round(achieved, 2), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
                      "frac": round(achieved * 1e12 / PEAK_BF16, 4), "traffic": None,
                      "avg_launch_ms": round(kern_ms, 3), "launches": len(events),
