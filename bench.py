@@ -23,6 +23,9 @@ import time
 import torch
 
 PEAK_BF16 = 2.5e15
+# HBM-side bytes per es_sparse_attention launch at this workload: rocprofv3 FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0
+# (scale factors from a copy of known size), profiles/echosparse_sparse_attention_wan14b_traffic.md
+TRAFFIC_BYTES = 4.67e10
 
 
 def parse():
@@ -168,7 +171,7 @@ def main():
                    "executed_tflop_per_layer": round(fl_layer / 1e12, 3)},
         "roofline": {"kernel": "attn_kernel<FIXED,COMP,*> (es_sparse_attention, both CFG branches)", "bound": "mfma",
                      "achieved": round(achieved, 2), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved * 1e12 / PEAK_BF16, 4), "traffic": None,
+                     "frac": round(achieved * 1e12 / PEAK_BF16, 4), "traffic": TRAFFIC_BYTES,
                      "avg_launch_ms": round(kern_ms, 3), "launches": len(events),
                      "flop_per_launch": fl_branch},
     }
