@@ -1,0 +1,286 @@
+"""numpy restatement of the VSA / VSA2 path -- TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+Tokens are [B, H, L, D] with L = NB * 64 and blk_cnt [NB] valid tokens per block (valid-first); selections are
+bool block masks [B, H, NB, NB] or CSR (ptr [B, H, NB + 1], idx). Floating-point work is float64 unless a function
+restates a kernel's float32 / bf16 arithmetic order on purpose (then it says so and is compared bit for bit).
+
+Functions and what pins each one (tests/test_cpu_vsa_oracle.py):
+  token_valid, pool        pool restates pool.cu's float32 order (rows of a group in order, then the groups; times
+                           the reciprocal count, bf16 round): pinned against float64 means within fp32 rounding and
+                           by padding never being read (NaN padding keeps outputs finite)
+  block_scores             rnd(rnd(qc . kc) / sqrt(D)) from given means (reference tests/vsa_reference.py:148-151):
+                           float64 dot, so it pins the GPU value up to one bf16 step of the dot's rounding
+  row_topk_mask            known-answer vector of reference tests/test_vsa.py:67-73 (ties, -0 == +0, K bounds)
+                           and brute force over Python's stable sort
+  global_topk_mask         exact count per (b, h), brute-force flat order (reference tests/vsa_reference.py:77-87)
+  psp_scores               rows sum to 1 under valid_groups with every group valid (reference
+                           tests/test_vsa2.py:169-170), paper = valid_groups / G for full blocks, and a brute-force
+                           per-element loop on a tiny case
+  fine_attention           full mask == dense softmax attention (torch scaled_dot_product_attention, float64), empty
+                           rows -> O = 0 / lse = -inf, permutation of the kv blocks leaves O unchanged
+  fine_backward            analytic gradients, pinned against torch.autograd on the float64 forward
+  fuse_fwd / fuse_bwd      torch.autograd of the fusion formula (reference csrc/vsa/fuse.cu:3-9)
+  vsa_output               the full operator for a frozen mask (reference tests/vsa_reference.py:110-135) in torch
+                           float64 with autograd; pinned by the fine / coarse pieces above and by the identity that
+                           the empty mask leaves only the coarse branch (reference tests/test_vsa.py:76-84)
+  plan_reference           the split planner's contract (reference tests/test_vsa2_split.py:60-87), pinned by hand
+                           cases and by every edge being covered exactly once
+  merge_fwd                LSE merge of normalized partials equals the unsplit softmax (closed form)
+"""
+import math
+
+import numpy as np
+
+from .bf16 import round_bf16
+
+BLOCK = 64
+
+
+def token_valid(blk_cnt, L):
+    """bool [L]: position p is valid iff p % 64 < blk_cnt[p // 64] (reference tests/vsa_reference.py:27-29)."""
+    pos = np.arange(L)
+    return (pos % BLOCK) < np.asarray(blk_cnt, np.int64)[pos // BLOCK]
+
+
+def pool(x, blk_cnt, R):
+    """(group means [B, H, NB * G, D], block means [B, H, NB, D]) as bf16 values in float32, restating
+    csrc/vsa/router/pool.cu:16-51: per column, float32 sums of a group's valid rows in order, the group sums added in
+    order, times 1 / count; empty groups give 0."""
+    x = np.asarray(x, np.float32)
+    B, H, L, D = x.shape
+    NB, G = L // BLOCK, BLOCK // R
+    cnt = np.asarray(blk_cnt, np.int64)
+    grp = np.zeros((B, H, NB * G, D), np.float32)
+    blk = np.zeros((B, H, NB, D), np.float32)
+    for b in range(NB):
+        tot = np.zeros((B, H, D), np.float32)
+        for g in range(G):
+            r0, r1 = g * R, min(g * R + R, int(cnt[b]))
+            s = np.zeros((B, H, D), np.float32)
+            for r in range(r0, r1):
+                s = (s + x[:, :, b * BLOCK + r]).astype(np.float32)
+            inv = np.float32(1.0) / np.float32(r1 - r0) if r1 > r0 else np.float32(0.0)
+            grp[:, :, b * G + g] = round_bf16(s * inv)
+            tot = (tot + s).astype(np.float32)
+        blk[:, :, b] = round_bf16(tot * (np.float32(1.0) / np.float32(cnt[b])))
+    return grp, blk
+
+
+def block_scores(qc, kc):
+    """rnd(rnd(qc . kc) / sqrt(D)) with rnd = bf16, float64 dot (reference tests/vsa_reference.py:148-151)."""
+    qc, kc = np.asarray(qc, np.float64), np.asarray(kc, np.float64)
+    D = qc.shape[-1]
+    s = round_bf16(np.einsum("...id,...jd->...ij", qc, kc).astype(np.float32))
+    return round_bf16((s * np.float32(1.0 / math.sqrt(D))).astype(np.float32))
+
+
+def _desc_order(values):
+    """Indices sorting a 1-D float array by value descending, ties by smaller index (-0 == +0)."""
+    v = np.asarray(values, np.float64) + 0.0
+    return np.lexsort((np.arange(v.size), -v))
+
+
+def row_topk_mask(scores, K):
+    """Exactly min(K, NB) blocks per row, score desc, ties to the smaller index (reference
+    tests/vsa_reference.py:160-165)."""
+    s = np.asarray(scores, np.float64)
+    k = max(0, min(int(K), s.shape[-1]))
+    flat = s.reshape(-1, s.shape[-1])
+    mask = np.zeros(flat.shape, bool)
+    for r in range(flat.shape[0]):
+        mask[r, _desc_order(flat[r])[:k]] = True
+    return mask.reshape(s.shape)
+
+
+def global_topk_mask(scores, budget):
+    """Exactly min(budget, NB^2) entries per (b, h), score desc then flat index asc (reference
+    tests/vsa_reference.py:77-87)."""
+    s = np.asarray(scores, np.float64)
+    B, H, NB, _ = s.shape
+    k = max(0, min(int(budget), NB * NB))
+    flat = s.reshape(B * H, NB * NB)
+    mask = np.zeros(flat.shape, bool)
+    for r in range(flat.shape[0]):
+        mask[r, _desc_order(flat[r])[:k]] = True
+    return mask.reshape(s.shape)
+
+
+def group_valid(blk_cnt, R):
+    """bool [NB * G]: a pooled group is valid iff it holds >= 1 valid token."""
+    cnt = np.asarray(blk_cnt, np.int64)
+    G = BLOCK // R
+    g = np.arange(cnt.size * G)
+    return (g % G) * R < cnt[g // G]
+
+
+def psp_scores(qr, kr, blk_cnt, R, row_norm):
+    """VSA2 PSP block scores [B, H, NB, NB] from given pooled rows qr / kr [B, H, >= NB * G, D] (float64):
+    A = softmax over all valid pooled keys of qr . kr / sqrt(D), zero rows for invalid pooled queries, summed over
+    (query group in i, key group in j), times 1 / G^2 (row_norm 1, "paper") or 1 / #valid groups of i (row_norm 0)
+    (reference csrc/vsa/router/router.cu:1-15, tests/vsa_reference.py:56-74)."""
+    cnt = np.asarray(blk_cnt, np.int64)
+    NB, G = cnt.size, BLOCK // R
+    Lr = NB * G
+    q = np.asarray(qr, np.float64)[:, :, :Lr]
+    k = np.asarray(kr, np.float64)[:, :, :Lr]
+    D = q.shape[-1]
+    gv = group_valid(cnt, R)
+    s = np.einsum("bhid,bhjd->bhij", q, k) / math.sqrt(D)
+    s = np.where(gv[None, None, None, :], s, -np.inf)
+    s = s - s.max(-1, keepdims=True)
+    a = np.exp(s)
+    a = a / a.sum(-1, keepdims=True) * gv[None, None, :, None]
+    B, H = q.shape[:2]
+    S = a.reshape(B, H, NB, G, NB, G).sum((3, 5))
+    if row_norm == 1:
+        return S / (G * G)
+    return S / ((cnt + R - 1) // R)[None, None, :, None]
+
+
+def csr_from_mask(mask):
+    """(ptr [B, H, NB + 1] int32 absolute, idx int32) of a bool mask [B, H, NB, NB], rows ascending."""
+    m = np.asarray(mask, bool)
+    B, H, N, _ = m.shape
+    rows = m.reshape(-1, N)
+    ends = np.cumsum(rows.sum(1))
+    starts = ends - rows.sum(1)
+    ptr = np.concatenate([starts.reshape(B * H, N), ends.reshape(B * H, N)[:, -1:]], 1).reshape(B, H, N + 1)
+    idx = np.nonzero(rows)[1]
+    return ptr.astype(np.int32), idx.astype(np.int32)
+
+
+def mask_from_csr(ptr, idx, nb):
+    ptr, idx = np.asarray(ptr, np.int64), np.asarray(idx, np.int64)
+    B, H = ptr.shape[:2]
+    m = np.zeros((B, H, nb, nb), bool)
+    for b in range(B):
+        for h in range(H):
+            for i in range(nb):
+                m[b, h, i, idx[ptr[b, h, i]:ptr[b, h, i + 1]]] = True
+    return m
+
+
+def fine_attention(q, k, v, blk_cnt, mask):
+    """(O [B, H, L, D], lse [B, H, L] natural) of attention restricted to the selected blocks with invalid keys
+    masked; rows with nothing to attend and padding rows give O = 0, lse = -inf (reference
+    tests/vsa_reference.py:90-107, csrc/vsa/generic/attn_fwd.cu:16-24). float64."""
+    q, k, v = (np.asarray(x, np.float64) for x in (q, k, v))
+    B, H, L, D = q.shape
+    valid = token_valid(blk_cnt, L)
+    blk = np.arange(L) // BLOCK
+    allowed = np.asarray(mask, bool)[:, :, blk][:, :, :, blk] & valid[None, None, None, :]
+    s = np.einsum("bhid,bhjd->bhij", q, k) / math.sqrt(D)
+    s = np.where(allowed, s, -np.inf)
+    has = allowed.any(-1) & valid[None, None, :]
+    m = np.where(has, s.max(-1), 0.0)
+    p = np.where(allowed, np.exp(s - m[..., None]), 0.0)
+    l = p.sum(-1)
+    o = np.einsum("bhij,bhjd->bhid", p / np.where(has, l, 1.0)[..., None], v) * has[..., None]
+    lse = np.where(has, m + np.log(np.where(has, l, 1.0)), -np.inf)
+    return o, lse
+
+
+def fine_backward(q, k, v, blk_cnt, mask, dout):
+    """(dq, dk, dv) of fine_attention for upstream dO, float64 closed form: P = softmax, dV = P^T dO,
+    dP = dO V^T, dS = P (dP - rowsum(dO * O)), dQ = dS K / sqrt(D), dK = dS^T Q / sqrt(D); padding rows of dO are
+    ignored (their P is 0)."""
+    q, k, v, dout = (np.asarray(x, np.float64) for x in (q, k, v, dout))
+    B, H, L, D = q.shape
+    o, lse = fine_attention(q, k, v, blk_cnt, mask)
+    valid = token_valid(blk_cnt, L)
+    blk = np.arange(L) // BLOCK
+    allowed = np.asarray(mask, bool)[:, :, blk][:, :, :, blk] & valid[None, None, None, :] & valid[None, None, :, None]
+    s = np.einsum("bhid,bhjd->bhij", q, k) / math.sqrt(D)
+    p = np.where(allowed, np.exp(s - np.where(np.isfinite(lse), lse, 0.0)[..., None]), 0.0)
+    delta = (dout * o).sum(-1)
+    dv = np.einsum("bhij,bhid->bhjd", p, dout)
+    dp = np.einsum("bhid,bhjd->bhij", dout, v)
+    ds = p * (dp - delta[..., None])
+    dq = np.einsum("bhij,bhjd->bhid", ds, k) / math.sqrt(D)
+    dk = np.einsum("bhij,bhid->bhjd", ds, q) / math.sqrt(D)
+    keep = valid[None, None, :, None]
+    return dq * keep, dk * keep, dv * keep
+
+
+def vsa_output(q, k, v, gate, blk_cnt, mask, gate_act="tanh", pooled=None):
+    """The full operator for a frozen mask as a torch float64 graph (autograd gives the gradients):
+    O = (O_fine + act(gate) * O_coarse[blk]) on valid rows, 0 elsewhere, O_coarse = softmax(qc kc^T / sqrt(D)) vc
+    over the block means (reference tests/vsa_reference.py:110-135, csrc/vsa/fuse.cu:3). q / k / v / gate are torch
+    float64 tensors; `pooled` optionally overrides (qc, kc, vc) values (e.g. the bf16-rounded means the kernels
+    use) while keeping the mean's gradient path (straight-through)."""
+    import torch
+    B, H, L, D = q.shape
+    NB = L // BLOCK
+    valid = torch.as_tensor(token_valid(blk_cnt, L))
+    cnt = torch.as_tensor(np.asarray(blk_cnt, np.float64))
+    z = valid[None, None, :, None].to(q.dtype)
+
+    def mean(x):
+        return (x * z).reshape(B, H, NB, BLOCK, D).sum(3) / cnt[None, None, :, None]
+
+    qc, kc, vc = mean(q), mean(k), mean(v)
+    if pooled is not None:
+        qc, kc, vc = (m + (torch.as_tensor(np.asarray(p, np.float64)) - m).detach() for m, p in zip((qc, kc, vc), pooled))
+    oc = torch.softmax(qc @ kc.transpose(-1, -2) / math.sqrt(D), -1) @ vc
+    blk = torch.arange(L) // BLOCK
+    allowed = torch.as_tensor(np.asarray(mask, bool))[:, :, blk][:, :, :, blk] & valid[None, None, None, :]
+    s = (q @ k.transpose(-1, -2)) / math.sqrt(D)
+    s = s.masked_fill(~allowed, float("-inf"))
+    has = allowed.any(-1, keepdim=True)
+    p = torch.softmax(torch.where(has, s, torch.zeros_like(s)), -1) * has
+    of = p @ v
+    if gate is None:
+        a = torch.ones_like(of[..., :1])
+    else:
+        a = torch.tanh(gate) if gate_act == "tanh" else gate
+        if gate.dim() == 3:
+            a = a[..., None]
+    return (of + a * oc[:, :, blk]) * z
+
+
+def plan_reference(ptr, chunk, max_slots, min_len=0, rel_mean=0.0, tail_frac=0.0, resident=1, budget=-1):
+    """The split-KV planner's contract in plain Python: (tasks, merges, info[8]) (reference
+    tests/test_vsa2_split.py:60-87, csrc/vsa/split.cu:1-19)."""
+    p = np.asarray(ptr, np.int64)
+    B, H, n1 = p.shape
+    nb = n1 - 1
+    rows_ptr = p.reshape(B * H, n1)
+    W = int(rows_ptr[-1, -1] - rows_ptr[0, 0])
+    gthr = max(chunk + 1, min_len)
+    if tail_frac > 0:
+        gthr = max(gthr, math.ceil(tail_frac * W / resident))
+    cap = 2 ** 31 - 1 if budget < 0 else budget
+    rows = []
+    for bh in range(B * H):
+        hp = rows_ptr[bh]
+        thr = gthr if rel_mean <= 0 else max(gthr, math.ceil(rel_mean * int(hp[nb] - hp[0]) / nb))
+        for i in range(nb):
+            n = int(hp[i + 1] - hp[i])
+            rows.append((bh * nb + i, int(hp[i]), n, n >= thr))
+    E = sum(1 for r in rows if r[3])
+    ok = E <= cap
+    split, direct, merges, used = [], [], [], 0
+    for r, beg, n, elig in rows:
+        c = -(-n // chunk) if elig else 0
+        if ok and c and used + c <= max_slots:
+            merges.append([r, used, c, 0])
+            split += [[r, beg + j * n // c, beg + (j + 1) * n // c, used + j] for j in range(c)]
+        else:
+            direct.append([r, beg, beg + n, -1])
+        used += c
+    t_split = sum(m[2] for m in merges)
+    info = [len(split) + len(direct), len(merges), t_split, len(rows), E, int(ok), gthr, W]
+    return split + direct, merges, info
+
+
+def merge_fwd(part_o, part_lse2):
+    """(o, lse natural) of normalized partials with log2 LSEs: weights 2^(lse_i - M) (reference
+    csrc/vsa/split.cu:16-19)."""
+    po, pl = np.asarray(part_o, np.float64), np.asarray(part_lse2, np.float64)
+    M = pl.max(0)
+    w = np.exp2(pl - np.where(np.isfinite(M), M, 0.0))
+    w = np.where(np.isfinite(pl), w, 0.0)
+    s = w.sum(0)
+    o = (w[..., None] * po).sum(0) / np.where(s > 0, s, 1.0)[..., None]
+    lse = np.where(s > 0, (M + np.log2(np.where(s > 0, s, 1.0))) * math.log(2.0), -np.inf)
+    return o, lse

@@ -1,4 +1,5 @@
-"""ctypes binding of the C ABI in include/echosparse_hip.h (libechosparse_hip.so, built in-tree by build_lib).
+"""ctypes binding of the C ABI in include/echosparse_hip.h and include/vsa_hip.h (libechosparse_hip.so, built
+in-tree by build_lib).
 
 There is no fallback: if the library is missing or fails to load, every kernel call raises. Arguments are torch
 tensors (device pointers taken with data_ptr) or Python scalars; each call is enqueued on the current HIP stream
@@ -14,6 +15,7 @@ LIB_PATH = os.environ.get("ECHOSPARSE_HIP_LIB") or os.path.join(os.path.dirname(
                                                                 "libechosparse_hip.so")
 
 P, I, F, Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+LL, DB = ctypes.c_longlong, ctypes.c_double
 
 # name -> argument types (the trailing hipStream_t is added below); mirrors include/echosparse_hip.h
 SIGNATURES = {
@@ -29,9 +31,30 @@ SIGNATURES = {
     "es_pack_plan": [P, P, I, I, I, I],
     "es_rebuild_plan": [P, P, I, P, P, P, P, P, I, P, P, I, I, I],
     "es_representatives": [P, P, P, P, P, P, P, P, P, Z, I, I, I, I],
+    # include/vsa_hip.h
+    "vsa_pool": [P, P, P, P, P, P, P, P, P, P, I, I, I, I],
+    "vsa_fuse_fwd": [P, P, P, P, P, I, I, I, I, I, I],
+    "vsa_fuse_bwd": [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I],
+    "vsa_finalize": [P, P, I, P, P, I, I, I],
+    "vsa_attn_fwd": [P, P, P, P, P, P, P, P, I, I, I],
+    "vsa_attn_fwd_tasks": [P, P, P, P, P, P, P, I, P, P, P, P, I, I, I],
+    "vsa_attn_bwd_kv": [P, P, P, P, P, P, P, P, P, P, P, I, P, P, I, I, I, I],
+    "vsa_attn_bwd_kv_tasks": [P, P, P, P, P, P, P, P, P, P, I, P, P, I, P, P, P, P, I, I, I],
+    "vsa_attn_bwd_q": [P, P, P, P, P, P, P, P, P, P, I, P, P, I, I, I],
+    "vsa_attn_bwd_q_tasks": [P, P, P, P, P, P, P, P, P, P, I, P, I, P, P, I, I, I],
+    "vsa_block_scores": [P, P, P, I, I, I, I, I],
+    "vsa_route_rows": [P, P, I, I, I, I, I, I, P, P, P, P, P, Z],
+    "vsa_row_topk": [P, I, I, I, I, P, P, P, P, P, Z],
+    "vsa_router_lse": [P, P, P, P, I, I, I, I],
+    "vsa_router_scores": [P, P, P, P, P, I, I, I, I, I, I],
+    "vsa_global_topk": [P, I, I, I, LL, P, P, P, P, P, Z],
+    "vsa_csr_transpose": [P, P, I, I, I, P, P, P, Z],
+    "vsa_split_plan": [P, I, I, I, I, I, DB, DB, I, I, P, P, P],
+    "vsa_split_merge_fwd": [P, P, P, P, I, P, P, P, I, I, I, I],
+    "vsa_split_merge_sum": [P, P, P, I, P, I, P, P, P, I, I, I],
 }
 NO_STREAM = {"es_representatives_workspace": ([I, I, I], Z), "es_last_error_string": ([], ctypes.c_char_p),
-             "es_abi_version": ([], I)}
+             "es_abi_version": ([], I), "vsa_topk_workspace": ([I, I], Z)}
 
 _lib = None
 
@@ -65,6 +88,10 @@ def ptr(x):
 def call(name, *args):
     """Call an entry point on torch's current stream; raise RuntimeError with the library's message on failure."""
     so = lib()
+    for a in args:
+        # a host tensor's address handed to a kernel faults the GPU: refuse it before the launch
+        if isinstance(a, torch.Tensor) and not a.is_cuda:
+            raise RuntimeError(f"{name}: every tensor argument must live on the GPU (got a {a.device} tensor)")
     conv = [ptr(a) if isinstance(a, torch.Tensor) or a is None else a for a in args]
     stream = torch.cuda.current_stream().cuda_stream
     status = getattr(so, name)(*conv, ctypes.c_void_p(stream))
@@ -75,3 +102,7 @@ def call(name, *args):
 
 def workspace_bytes(L, H, D):
     return int(lib().es_representatives_workspace(L, H, D))
+
+
+def topk_workspace_bytes(bh_count, NB):
+    return int(lib().vsa_topk_workspace(bh_count, NB))

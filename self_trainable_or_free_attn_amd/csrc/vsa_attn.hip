@@ -1,0 +1,801 @@
+// VSA fine block-sparse attention over a CSR block selection (gfx950, bf16 MFMA 32x32x16).
+//
+// Tokens are [BH, L, D] bf16 (D = 128), L = NB * 64 in 64-token blocks; blk_cnt[NB] gives each block's valid
+// tokens (valid-first). Query block i of head bh attends to the kv blocks row_ptr / col_idx list for row
+// (bh, i), with key columns >= blk_cnt[kv] masked; query rows >= blk_cnt[i] and rows with an empty list get
+// O = 0 and lse = -inf. lse is the natural-log row sum. Semantics: reference csrc/vsa/generic/attn_fwd.cu:16-24,
+// tests/vsa_reference.py:90-107.
+//
+// Forward: one workgroup per (query block, head), 4 waves = 2 row groups of 32 queries x 2 key halves of each
+// 64-key chunk. Every chunk is staged once in LDS (double-buffered direct global->LDS loads, swizzled 256-byte
+// rows) and each wave runs its own online softmax over its 32-key halves (S^T = K Q^T so that exp(S^T) is directly
+// the B operand of O^T += V^T P^T); the two key-half states of a row group are merged once at the end through
+// LDS. The running max is only moved when a row's new maximum exceeds it by more than 8 (log2 units), which
+// keeps the O rescale off the common path without changing the result beyond rounding.
+// Task mode (split-KV, reference attn_fwd.cu:216-237): the grid walks (row, beg, end, slot) tasks; slot >= 0
+// writes an fp32 normalized partial O and its log2 lse to part_o / part_lse, slot < 0 the final O / lse.
+#include "../../include/vsa_hip.h"
+#include "common.h"
+
+namespace es {
+
+namespace {
+
+constexpr float LN2 = 0.6931471805599453f;
+constexpr float RESCALE_SLACK = 8.0f;
+
+struct VsaFwdArgs {
+  const bf16_t *q, *k, *v;
+  bf16_t* out;
+  float* lse;
+  const int *row_ptr, *col_idx, *blk_cnt;
+  const int4* tasks;
+  const int* info;  // device task count (task mode)
+  float *part_o, *part_lse;
+  int L, NB, BH, per_xcd;
+  float scale;  // log2(e) / sqrt(D)
+};
+
+template <bool TASKS>
+__global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
+  __shared__ __attribute__((aligned(16))) char kv_s[2][2][BK * 256];
+
+  int qb, bh, beg, end, slot = -1;
+  if (TASKS) {
+    if ((int)blockIdx.x >= sload(a.info)) return;
+    const int4 tk = a.tasks[blockIdx.x];
+    bh = tk.x / a.NB;
+    qb = tk.x - bh * a.NB;
+    beg = tk.y;
+    end = tk.z;
+    slot = tk.w;
+  } else {
+    // XCD-aware order: dispatch slot w runs on XCD w % 8; each XCD walks a contiguous run of query blocks of a head
+    const int w = blockIdx.x, xcd = w & 7, s = w >> 3;
+    bh = s / a.per_xcd;
+    qb = xcd * a.per_xcd + s % a.per_xcd;
+    if (bh >= a.BH || qb >= a.NB) return;
+    const int* rp = a.row_ptr + (size_t)bh * (a.NB + 1) + qb;
+    beg = sload(rp);
+    end = sload(rp + 1);
+  }
+  beg = __builtin_amdgcn_readfirstlane(beg);
+  end = __builtin_amdgcn_readfirstlane(end);
+  const int nc = end - beg;
+
+  const int tid = threadIdx.x, l = tid & 63, hi = l >> 5, lq = l & 31;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rg = wv & 1, kh = wv >> 1;
+  const int qrow = 32 * rg + lq;  // row inside the query block
+  const int qcnt = sload(a.blk_cnt + qb);
+  const bool qvalid = qrow < qcnt;
+  const size_t head = (size_t)bh * a.L;
+
+  const unsigned head_bytes = (unsigned)((size_t)a.L * HD * 2);
+  const rsrc_t rk = make_rsrc(a.k + head * HD, head_bytes);
+  const rsrc_t rv = make_rsrc(a.v + head * HD, head_bytes);
+  // this lane's four load rows R = 16 wv + 4 i + l / 16 of a chunk and its swizzled 16-byte chunk in them
+  unsigned ld_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int P = (wv * 4 + i) * 64 + l, R = P >> 4;
+    ld_off[i] = (unsigned)R * 256 + (unsigned)(((P & 15) ^ swz(R)) * 16);
+  }
+  auto issue = [&](int b, int sb) {
+    const unsigned soff = (unsigned)b * (BK * 256);
+    char* kd = kv_s[sb][0] + wv * 4096;
+    char* vd = kv_s[sb][1] + wv * 4096;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      buf2lds16(rk, kd + i * 1024, ld_off[i], soff);
+      buf2lds16(rv, vd + i * 1024, ld_off[i], soff);
+    }
+  };
+
+  bf16x8 qreg[8];
+  {
+    const bf16_t* qp = a.q + (head + (size_t)qb * BK + qrow) * HD;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qreg[ks] = *reinterpret_cast<const bf16x8*>(qp + 16 * ks + 8 * hi);
+  }
+  int koff[8];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) koff[ks] = kh * 8192 + tile_off(lq, 2 * ks + hi);
+  int voff[2][4];
+  {
+    const int g1 = (l >> 4) & 1, sub = (l & 1) * 8, rowA = 4 * hi + ((l & 15) >> 2);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      voff[0][db] = tile_off(rowA, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
+      voff[1][db] = tile_off(rowA + 8, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
+    }
+  }
+
+  f32x16 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) o[db] = f32x16{};
+  float lsum = 0.0f, mref = -INFINITY;
+  const float scale = a.scale;
+
+  int bcur = nc > 0 ? sload(a.col_idx + beg) : 0;
+  int ccur = nc > 0 ? sload(a.blk_cnt + bcur) : 0;
+  int bnext = nc > 1 ? sload(a.col_idx + beg + 1) : 0;
+  if (nc > 0) issue(bcur, 0);
+  wait_vmem();
+  __syncthreads();
+
+  for (int j = 0; j < nc; ++j) {
+    const int sb = j & 1;
+    int cnext = 0, bnn = 0;
+    if (j + 1 < nc) {
+      issue(bnext, sb ^ 1);
+      cnext = sload(a.blk_cnt + bnext);
+      if (j + 2 < nc) bnn = sload(a.col_idx + beg + j + 2);
+    }
+    const char* kb = kv_s[sb][0];
+    const char* vb = kv_s[sb][1] + kh * 8192;
+    f32x16 s = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) s = mfma32(lds_read16(kb, koff[ks]), qreg[ks], s);
+    float p[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = s[r] * scale;
+    if (ccur < BK) {  // key columns past the block's valid tokens
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (32 * kh + 8 * (r / 4) + 4 * hi + (r % 4) >= ccur) p[r] = -INFINITY;
+    }
+    float mx = p[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, p[r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    if (__builtin_amdgcn_ballot_w64(mx > mref + RESCALE_SLACK) != 0) {
+      const float mnew = fmaxf(mref, mx);
+      const float alpha = mref == -INFINITY ? 0.0f : exp2f_fast(mref - mnew);
+      lsum *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      mref = mnew;
+    }
+    const float msub = mref == -INFINITY ? 0.0f : mref;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = exp2f_fast(p[r] - msub);
+    const bf16x8 pa = pack8(&p[0]), pb = pack8(&p[8]);
+    lsum += sum8_bf16(pb, sum8_bf16(pa, 0.0f));
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      o[db] = mfma32(cat_tr(lds_read_tr(vb, voff[0][db]), lds_read_tr(vb, voff[1][db])), pa, o[db]);
+      o[db] = mfma32(cat_tr(lds_read_tr(vb + 4096, voff[0][db]), lds_read_tr(vb + 4096, voff[1][db])), pb, o[db]);
+    }
+    wait_vmem();
+    __syncthreads();
+    bcur = bnext;
+    ccur = cnext;
+    bnext = bnn;
+  }
+
+  // merge the two key halves of each row group: kh = 1 waves hand (m, l, O) to the kh = 0 waves through LDS
+  float* xo = reinterpret_cast<float*>(&kv_s[0][0][0]) + rg * (64 * 64);        // [64 regs][64 lanes]
+  float* xm = reinterpret_cast<float*>(&kv_s[1][0][0]) + rg * 128;              // [m | l][64 lanes]
+  const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+  if (kh == 1) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xo[(db * 16 + r) * 64 + l] = o[db][r];
+    xm[l] = mref;
+    xm[64 + l] = ltot;
+  }
+  __syncthreads();
+  if (kh == 1) return;
+  const float m1 = xm[l], l1 = xm[64 + l];
+  const float M = fmaxf(mref, m1);
+  const float a0 = mref == -INFINITY ? 0.0f : exp2f_fast(mref - M);
+  const float a1 = m1 == -INFINITY ? 0.0f : exp2f_fast(m1 - M);
+  const float lt = a0 * ltot + a1 * l1;
+  const bool live = qvalid && lt > 0.0f;
+  const float inv = live ? 1.0f / lt : 0.0f;
+  const size_t tok = head + (size_t)qb * BK + qrow;
+  const float lse2 = live ? M + log2f(lt) : -INFINITY;
+  if (!TASKS || slot < 0) {
+    bf16_t* orow = a.out + tok * HD;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ushort4 v4;
+        v4.x = f2bf((a0 * o[db][4 * i + 0] + a1 * xo[(db * 16 + 4 * i + 0) * 64 + l]) * inv);
+        v4.y = f2bf((a0 * o[db][4 * i + 1] + a1 * xo[(db * 16 + 4 * i + 1) * 64 + l]) * inv);
+        v4.z = f2bf((a0 * o[db][4 * i + 2] + a1 * xo[(db * 16 + 4 * i + 2) * 64 + l]) * inv);
+        v4.w = f2bf((a0 * o[db][4 * i + 3] + a1 * xo[(db * 16 + 4 * i + 3) * 64 + l]) * inv);
+        *reinterpret_cast<ushort4*>(orow + 32 * db + 8 * i + 4 * hi) = v4;
+      }
+    if (hi == 0) a.lse[tok] = live ? lse2 * LN2 : -INFINITY;
+  } else {
+    float* prow = a.part_o + ((size_t)slot * BK + qrow) * HD;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float4 v4;
+        v4.x = (a0 * o[db][4 * i + 0] + a1 * xo[(db * 16 + 4 * i + 0) * 64 + l]) * inv;
+        v4.y = (a0 * o[db][4 * i + 1] + a1 * xo[(db * 16 + 4 * i + 1) * 64 + l]) * inv;
+        v4.z = (a0 * o[db][4 * i + 2] + a1 * xo[(db * 16 + 4 * i + 2) * 64 + l]) * inv;
+        v4.w = (a0 * o[db][4 * i + 3] + a1 * xo[(db * 16 + 4 * i + 3) * 64 + l]) * inv;
+        *reinterpret_cast<float4*>(prow + 32 * db + 8 * i + 4 * hi) = v4;
+      }
+    if (hi == 0) a.part_lse[(size_t)slot * BK + qrow] = lse2;
+  }
+}
+
+
+// ------------------------------------------------------------------------------------------------ backward
+// Per selected pair (query block i, kv block j), with P = exp(S / sqrt(D) - lse) and dS = P (dP - delta) / sqrt(D)
+// (reference csrc/vsa/generic/attn_bwd.cu:1-34; rows with lse = -inf and key columns >= blk_cnt get P = 0):
+//   KV owner (dK, dV; k2q lists): one workgroup per (kv block, head), 4 waves = 2 key halves x 2 query halves of
+//     each staged query block. S = Q K^T and dP = dO V^T come out with keys on lanes, so P and dS are directly the
+//     B operands of dV^T += dO^T P and dK^T += Q^T dS (dO^T / Q^T through transposed LDS reads). K and V stay in
+//     registers; Q, dO, lse and delta of each listed query block stream through LDS. 4 products per pair.
+//   Q owner (dQ; q2k lists): the forward's layout. S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T with K^T through
+//     transposed LDS reads. 3 products per pair; dQ is deterministic (no atomics).
+// The two partial accumulators of a workgroup (query halves, or key halves) are summed once at the end in LDS.
+struct VsaBwdArgs {
+  const bf16_t *q, *k, *v, *dout;
+  const float *lse, *delta;
+  const int *row_ptr, *col_idx, *blk_cnt;
+  const int4* tasks;
+  const int* info;
+  const float *add_a, *add_b;  // per-block gradients distributed as add / cnt (KV owner: dK, dV; Q owner: dQ)
+  int add_nb;
+  bf16_t *out_a, *out_b;       // bf16 outputs
+  float *out_a32, *out_b32;    // fp32 outputs (KV owner) / accumulator dq_acc += dQ (Q owner)
+  float *part_a, *part_b;      // split partials [slot, 64, D]
+  int L, NB, BH, per_xcd;
+  float scale_log2, scale;
+};
+
+// decode the workgroup's (owner block, head, list range, slot); false = nothing to do
+template <bool TASKS>
+__device__ __forceinline__ bool owner_of(const VsaBwdArgs& a, int& blk, int& bh, int& beg, int& end, int& slot) {
+  slot = -1;
+  if (TASKS) {
+    if ((int)blockIdx.x >= sload(a.info)) return false;
+    const int4 tk = a.tasks[blockIdx.x];
+    bh = tk.x / a.NB;
+    blk = tk.x - bh * a.NB;
+    beg = tk.y;
+    end = tk.z;
+    slot = tk.w;
+  } else {
+    const int w = blockIdx.x, xcd = w & 7, s = w >> 3;
+    bh = s / a.per_xcd;
+    blk = xcd * a.per_xcd + s % a.per_xcd;
+    if (bh >= a.BH || blk >= a.NB) return false;
+    const int* rp = a.row_ptr + (size_t)bh * (a.NB + 1) + blk;
+    beg = sload(rp);
+    end = sload(rp + 1);
+  }
+  beg = __builtin_amdgcn_readfirstlane(beg);
+  end = __builtin_amdgcn_readfirstlane(end);
+  return true;
+}
+
+// lse (natural) -> log2 domain, +inf for rows that must get P = 0
+__device__ __forceinline__ float lse_to_log2(float lse) { return lse == -INFINITY ? INFINITY : lse * LOG2E; }
+
+template <bool TASKS>
+__global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
+  // V of the owned block stays in LDS (the B operand of dP = dO V^T); K stays in registers (the B operand of
+  // S = Q K^T); Q, dO, lse and delta of the listed query blocks are double-buffered. The dK / dV accumulators
+  // (128 registers) need the full register file: one wave per SIMD.
+  __shared__ __attribute__((aligned(16))) char qd_s[2][2][BK * 256];  // [buffer][Q | dO]
+  __shared__ __attribute__((aligned(16))) char v_s[BK * 256];
+  __shared__ __attribute__((aligned(16))) float st_s[2][2][BK];       // [buffer][lse2 (+inf: P = 0) | delta]
+  int kb, bh, beg, end, slot;
+  if (!owner_of<TASKS>(a, kb, bh, beg, end, slot)) return;
+  const int nc = end - beg;
+  const int tid = threadIdx.x, l = tid & 63, hi = l >> 5, lq = l & 31;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kh = wv & 1, qh = wv >> 1;
+  const int key = 32 * kh + lq;
+  const int kcnt = sload(a.blk_cnt + kb);
+  const bool kvalid = key < kcnt;
+  const size_t head = (size_t)bh * a.L;
+
+  const unsigned head_bytes = (unsigned)((size_t)a.L * HD * 2);
+  const rsrc_t rq = make_rsrc(a.q + head * HD, head_bytes);
+  const rsrc_t rd = make_rsrc(a.dout + head * HD, head_bytes);
+  unsigned ld_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int P = (wv * 4 + i) * 64 + l, R = P >> 4;
+    ld_off[i] = (unsigned)R * 256 + (unsigned)(((P & 15) ^ swz(R)) * 16);
+  }
+  {
+    const rsrc_t rv = make_rsrc(a.v + head * HD, head_bytes);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) buf2lds16(rv, v_s + wv * 4096 + i * 1024, ld_off[i], (unsigned)kb * (BK * 256));
+  }
+  bf16x8 kreg[8];
+  {
+    const size_t off = (head + (size_t)kb * BK + key) * HD + 8 * hi;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) kreg[ks] = *reinterpret_cast<const bf16x8*>(a.k + off + 16 * ks);
+  }
+  // stage query block i (Q, dO); wave 0 returns lane l's lse2 / delta of row i * 64 + l
+  auto issue = [&](int i, int sb, float& ls, float& dl) {
+    const unsigned soff = (unsigned)i * (BK * 256);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      buf2lds16(rq, qd_s[sb][0] + wv * 4096 + r * 1024, ld_off[r], soff);
+      buf2lds16(rd, qd_s[sb][1] + wv * 4096 + r * 1024, ld_off[r], soff);
+    }
+    if (wv == 0) {
+      const size_t t = head + (size_t)i * BK + l;
+      ls = lse_to_log2(a.lse[t]);
+      dl = a.delta[t];
+    }
+  };
+  int aoff[8], boff[8];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    aoff[ks] = qh * 8192 + tile_off(lq, 2 * ks + hi);
+    boff[ks] = kh * 8192 + tile_off(lq, 2 * ks + hi);
+  }
+  int toff[2][4];
+  {
+    const int g1 = (l >> 4) & 1, sub = (l & 1) * 8, rowA = 4 * hi + ((l & 15) >> 2);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      toff[0][db] = qh * 8192 + tile_off(rowA, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
+      toff[1][db] = qh * 8192 + tile_off(rowA + 8, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
+    }
+  }
+  f32x16 dk[4], dv[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) dk[db] = dv[db] = f32x16{};
+
+  float ls = 0.0f, dl = 0.0f;
+  int inext = nc > 1 ? sload(a.col_idx + beg + 1) : 0;
+  if (nc > 0) {
+    issue(sload(a.col_idx + beg), 0, ls, dl);
+    wait_vmem();
+    if (wv == 0) {
+      st_s[0][0][l] = ls;
+      st_s[0][1][l] = dl;
+    }
+  }
+  wait_vmem();
+  __syncthreads();
+  // masked key columns: every row's lse2 becomes +inf for this lane, so P = 2^(s - inf) = 0 without a branch
+  const float kmask = kvalid ? 0.0f : INFINITY;
+  for (int j = 0; j < nc; ++j) {
+    const int sb = j & 1;
+    int inn = 0;
+    if (j + 1 < nc) {
+      issue(inext, sb ^ 1, ls, dl);
+      if (j + 2 < nc) inn = sload(a.col_idx + beg + j + 2);
+    }
+    const char* qt = qd_s[sb][0];
+    const char* dt = qd_s[sb][1];
+    f32x16 s = {}, dp = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) s = mfma32(lds_read16(qt, aoff[ks]), kreg[ks], s);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) dp = mfma32(lds_read16(dt, aoff[ks]), lds_read16(v_s, boff[ks]), dp);
+    float p[16], ds[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 l4 = *reinterpret_cast<const f32x4*>(&st_s[sb][0][32 * qh + 8 * g + 4 * hi]);
+      const f32x4 d4 = *reinterpret_cast<const f32x4*>(&st_s[sb][1][32 * qh + 8 * g + 4 * hi]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * g + e;
+        p[r] = exp2f_fast(fmaf(s[r], a.scale_log2, -(l4[e] + kmask)));
+        ds[r] = p[r] * (dp[r] - d4[e]) * a.scale;
+      }
+    }
+    const bf16x8 pa = pack8(&p[0]), pb = pack8(&p[8]);
+    const bf16x8 sa = pack8(&ds[0]), sb8 = pack8(&ds[8]);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      dv[db] = mfma32(cat_tr(lds_read_tr(dt, toff[0][db]), lds_read_tr(dt, toff[1][db])), pa, dv[db]);
+      dv[db] = mfma32(cat_tr(lds_read_tr(dt + 4096, toff[0][db]), lds_read_tr(dt + 4096, toff[1][db])), pb, dv[db]);
+      dk[db] = mfma32(cat_tr(lds_read_tr(qt, toff[0][db]), lds_read_tr(qt, toff[1][db])), sa, dk[db]);
+      dk[db] = mfma32(cat_tr(lds_read_tr(qt + 4096, toff[0][db]), lds_read_tr(qt + 4096, toff[1][db])), sb8, dk[db]);
+    }
+    wait_vmem();
+    if (j + 1 < nc && wv == 0) {
+      st_s[sb ^ 1][0][l] = ls;
+      st_s[sb ^ 1][1][l] = dl;
+    }
+    __syncthreads();
+    inext = inn;
+  }
+
+  // sum the query-half partials: qh = 1 waves hand theirs to the qh = 0 waves of the same key half
+  float* xk = reinterpret_cast<float*>(&qd_s[0][0][0]) + kh * (2 * 64 * 64);
+  float* xv = xk + 64 * 64;
+  if (qh == 1) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        xk[(db * 16 + r) * 64 + l] = dk[db][r];
+        xv[(db * 16 + r) * 64 + l] = dv[db][r];
+      }
+  }
+  __syncthreads();
+  if (qh == 1) return;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      dk[db][r] += xk[(db * 16 + r) * 64 + l];
+      dv[db][r] += xv[(db * 16 + r) * 64 + l];
+    }
+  const size_t tok = head + (size_t)kb * BK + key;
+  if (TASKS && slot >= 0) {
+    float* pk = a.part_a + ((size_t)slot * BK + key) * HD;
+    float* pv = a.part_b + ((size_t)slot * BK + key) * HD;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = 32 * db + 8 * i + 4 * hi;
+        *reinterpret_cast<float4*>(pk + c) = make_float4(dk[db][4 * i], dk[db][4 * i + 1], dk[db][4 * i + 2], dk[db][4 * i + 3]);
+        *reinterpret_cast<float4*>(pv + c) = make_float4(dv[db][4 * i], dv[db][4 * i + 1], dv[db][4 * i + 2], dv[db][4 * i + 3]);
+      }
+    return;
+  }
+  // valid keys: dK / dV + add / cnt; padding keys: 0
+  const float inv = kvalid ? 1.0f / (float)kcnt : 0.0f;
+  const float keep = kvalid ? 1.0f : 0.0f;
+  const float* adk = a.add_a + ((size_t)bh * a.add_nb + kb) * HD;
+  const float* adv = a.add_b + ((size_t)bh * a.add_nb + kb) * HD;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = 32 * db + 8 * i + 4 * hi;
+      f32x4 xk4, xv4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xk4[e] = dk[db][4 * i + e] * keep;
+        xv4[e] = dv[db][4 * i + e] * keep;
+      }
+      if (a.add_a != nullptr) xk4 += *reinterpret_cast<const f32x4*>(adk + c) * inv;
+      if (a.add_b != nullptr) xv4 += *reinterpret_cast<const f32x4*>(adv + c) * inv;
+      if (a.out_a32 != nullptr) {
+        *reinterpret_cast<f32x4*>(a.out_a32 + tok * HD + c) = xk4;
+        *reinterpret_cast<f32x4*>(a.out_b32 + tok * HD + c) = xv4;
+      } else {
+        ushort4 k4, v4;
+        k4.x = f2bf(xk4[0]); k4.y = f2bf(xk4[1]); k4.z = f2bf(xk4[2]); k4.w = f2bf(xk4[3]);
+        v4.x = f2bf(xv4[0]); v4.y = f2bf(xv4[1]); v4.z = f2bf(xv4[2]); v4.w = f2bf(xv4[3]);
+        *reinterpret_cast<ushort4*>(a.out_a + tok * HD + c) = k4;
+        *reinterpret_cast<ushort4*>(a.out_b + tok * HD + c) = v4;
+      }
+    }
+}
+
+template <bool TASKS>
+__global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
+  __shared__ __attribute__((aligned(16))) char kv_s[2][2][BK * 256];
+  int qb, bh, beg, end, slot;
+  if (!owner_of<TASKS>(a, qb, bh, beg, end, slot)) return;
+  const int nc = end - beg;
+  const int tid = threadIdx.x, l = tid & 63, hi = l >> 5, lq = l & 31;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rg = wv & 1, kh = wv >> 1;
+  const int qrow = 32 * rg + lq;
+  const int qcnt = sload(a.blk_cnt + qb);
+  const bool qvalid = qrow < qcnt;
+  const size_t head = (size_t)bh * a.L;
+  const size_t tok = head + (size_t)qb * BK + qrow;
+
+  bf16x8 qreg[8], dreg[8];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    qreg[ks] = *reinterpret_cast<const bf16x8*>(a.q + tok * HD + 16 * ks + 8 * hi);
+    dreg[ks] = *reinterpret_cast<const bf16x8*>(a.dout + tok * HD + 16 * ks + 8 * hi);
+  }
+  const float ls = qvalid ? lse_to_log2(a.lse[tok]) : INFINITY;
+  const float dl = a.delta[tok];
+
+  const unsigned head_bytes = (unsigned)((size_t)a.L * HD * 2);
+  const rsrc_t rk = make_rsrc(a.k + head * HD, head_bytes);
+  const rsrc_t rv = make_rsrc(a.v + head * HD, head_bytes);
+  unsigned ld_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int P = (wv * 4 + i) * 64 + l, R = P >> 4;
+    ld_off[i] = (unsigned)R * 256 + (unsigned)(((P & 15) ^ swz(R)) * 16);
+  }
+  auto issue = [&](int b, int sb) {
+    const unsigned soff = (unsigned)b * (BK * 256);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      buf2lds16(rk, kv_s[sb][0] + wv * 4096 + i * 1024, ld_off[i], soff);
+      buf2lds16(rv, kv_s[sb][1] + wv * 4096 + i * 1024, ld_off[i], soff);
+    }
+  };
+  int koff[8];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) koff[ks] = kh * 8192 + tile_off(lq, 2 * ks + hi);
+  int toff[2][4];
+  {
+    const int g1 = (l >> 4) & 1, sub = (l & 1) * 8, rowA = 4 * hi + ((l & 15) >> 2);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      toff[0][db] = kh * 8192 + tile_off(rowA, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
+      toff[1][db] = kh * 8192 + tile_off(rowA + 8, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
+    }
+  }
+  f32x16 dq[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) dq[db] = f32x16{};
+
+  int bcur = nc > 0 ? sload(a.col_idx + beg) : 0;
+  int ccur = nc > 0 ? sload(a.blk_cnt + bcur) : 0;
+  int bnext = nc > 1 ? sload(a.col_idx + beg + 1) : 0;
+  if (nc > 0) issue(bcur, 0);
+  wait_vmem();
+  __syncthreads();
+  for (int j = 0; j < nc; ++j) {
+    const int sb = j & 1;
+    int cnext = 0, bnn = 0;
+    if (j + 1 < nc) {
+      issue(bnext, sb ^ 1);
+      cnext = sload(a.blk_cnt + bnext);
+      if (j + 2 < nc) bnn = sload(a.col_idx + beg + j + 2);
+    }
+    const char* kt = kv_s[sb][0];
+    const char* vt = kv_s[sb][1];
+    f32x16 s = {}, dp = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) s = mfma32(lds_read16(kt, koff[ks]), qreg[ks], s);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) dp = mfma32(lds_read16(vt, koff[ks]), dreg[ks], dp);
+    float ds[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float kill = 32 * kh + 8 * (r / 4) + 4 * hi + (r % 4) < ccur ? 0.0f : INFINITY;
+      const float p = exp2f_fast(fmaf(s[r], a.scale_log2, -(ls + kill)));
+      ds[r] = p * (dp[r] - dl) * a.scale;
+    }
+    const bf16x8 sa = pack8(&ds[0]), sb8 = pack8(&ds[8]);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      dq[db] = mfma32(cat_tr(lds_read_tr(kt, toff[0][db]), lds_read_tr(kt, toff[1][db])), sa, dq[db]);
+      dq[db] = mfma32(cat_tr(lds_read_tr(kt + 4096, toff[0][db]), lds_read_tr(kt + 4096, toff[1][db])), sb8, dq[db]);
+    }
+    wait_vmem();
+    __syncthreads();
+    bcur = bnext;
+    ccur = cnext;
+    bnext = bnn;
+  }
+
+  float* xq = reinterpret_cast<float*>(&kv_s[0][0][0]) + rg * (64 * 64);
+  if (kh == 1) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xq[(db * 16 + r) * 64 + l] = dq[db][r];
+  }
+  __syncthreads();
+  if (kh == 1) return;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[db][r] += xq[(db * 16 + r) * 64 + l];
+  if (TASKS && slot >= 0) {
+    float* pq = a.part_a + ((size_t)slot * BK + qrow) * HD;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<float4*>(pq + 32 * db + 8 * i + 4 * hi) =
+            make_float4(dq[db][4 * i], dq[db][4 * i + 1], dq[db][4 * i + 2], dq[db][4 * i + 3]);
+    return;
+  }
+  const float inv = qvalid ? 1.0f / (float)qcnt : 0.0f;
+  const float keep = qvalid ? 1.0f : 0.0f;
+  const float* adq = a.add_a + ((size_t)bh * a.add_nb + qb) * HD;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = 32 * db + 8 * i + 4 * hi;
+      f32x4 x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = dq[db][4 * i + e] * keep;
+      if (a.out_a32 != nullptr) {  // dq_acc += dQ (padding rows keep their value)
+        f32x4* dst = reinterpret_cast<f32x4*>(a.out_a32 + tok * HD + c);
+        *dst = *dst + x;
+      } else {
+        if (a.add_a != nullptr) x += *reinterpret_cast<const f32x4*>(adq + c) * inv;
+        ushort4 q4;
+        q4.x = f2bf(x[0]); q4.y = f2bf(x[1]); q4.z = f2bf(x[2]); q4.w = f2bf(x[3]);
+        *reinterpret_cast<ushort4*>(a.out_a + tok * HD + c) = q4;
+      }
+    }
+}
+
+}  // namespace
+
+}  // namespace es
+
+using namespace es;
+
+static int vsa_check_qkv(const void* q, const void* k, const void* v, int BH, int L, int D) {
+  ES_REQUIRE(q && k && v, ES_ERR_INVALID, "VSA: null q / k / v");
+  ES_REQUIRE(BH > 0 && L > 0 && L % BK == 0, ES_ERR_INVALID, "VSA: tokens must be [BH, L = NB * 64, D]");
+  ES_REQUIRE(D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 128");
+  ES_REQUIRE((size_t)L * HD * 2 < (1ull << 31), ES_ERR_UNSUPPORTED, "VSA: one head's tokens exceed 2 GiB");
+  return ES_OK;
+}
+
+static VsaFwdArgs fwd_args(const void* q, const void* k, const void* v, const int* blk_cnt, int BH, int L) {
+  VsaFwdArgs a = {};
+  a.q = (const bf16_t*)q;
+  a.k = (const bf16_t*)k;
+  a.v = (const bf16_t*)v;
+  a.blk_cnt = blk_cnt;
+  a.L = L;
+  a.NB = L / BK;
+  a.BH = BH;
+  a.scale = LOG2E / sqrtf((float)HD);
+  return a;
+}
+
+extern "C" int vsa_attn_fwd(const void* q, const void* k, const void* v, const int* row_ptr, const int* col_idx,
+                            const int* blk_cnt, void* out, float* lse, int BH, int L, int D, hipStream_t stream) {
+  if (int st = vsa_check_qkv(q, k, v, BH, L, D)) return st;
+  ES_REQUIRE(row_ptr && blk_cnt && out && lse, ES_ERR_INVALID, "VSA: null tensor pointer");
+  VsaFwdArgs a = fwd_args(q, k, v, blk_cnt, BH, L);
+  a.row_ptr = row_ptr;
+  a.col_idx = col_idx;
+  a.out = (bf16_t*)out;
+  a.lse = lse;
+  a.per_xcd = (a.NB + 7) / 8;
+  const long long grid = 8LL * BH * a.per_xcd;
+  ES_REQUIRE(grid < (1LL << 31), ES_ERR_UNSUPPORTED, "VSA: grid too large");
+  hipLaunchKernelGGL(vsa_fwd_kernel<false>, dim3((unsigned)grid), dim3(256), 0, stream, a);
+  return check_launch("vsa_attn_fwd");
+}
+
+extern "C" int vsa_attn_fwd_tasks(const void* q, const void* k, const void* v, const int* col_idx,
+                                  const int* blk_cnt, const int* tasks, const int* info, int max_tasks, void* out,
+                                  float* lse, float* part_o, float* part_lse, int BH, int L, int D,
+                                  hipStream_t stream) {
+  if (int st = vsa_check_qkv(q, k, v, BH, L, D)) return st;
+  // part_o / part_lse may be null when the plan has no split slots (no task then writes a partial)
+  ES_REQUIRE(blk_cnt && tasks && info && out && lse, ES_ERR_INVALID, "VSA: null tensor pointer");
+  ES_REQUIRE(max_tasks >= 0, ES_ERR_INVALID, "VSA: negative task capacity");
+  if (max_tasks == 0) return ES_OK;
+  VsaFwdArgs a = fwd_args(q, k, v, blk_cnt, BH, L);
+  a.col_idx = col_idx;
+  a.tasks = (const int4*)tasks;
+  a.info = info;
+  a.out = (bf16_t*)out;
+  a.lse = lse;
+  a.part_o = part_o;
+  a.part_lse = part_lse;
+  hipLaunchKernelGGL(vsa_fwd_kernel<true>, dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
+  return check_launch("vsa_attn_fwd_tasks");
+}
+
+
+static VsaBwdArgs bwd_args(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                           const float* delta, const int* blk_cnt, int BH, int L) {
+  VsaBwdArgs a = {};
+  a.q = (const bf16_t*)q;
+  a.k = (const bf16_t*)k;
+  a.v = (const bf16_t*)v;
+  a.dout = (const bf16_t*)dout;
+  a.lse = lse;
+  a.delta = delta;
+  a.blk_cnt = blk_cnt;
+  a.L = L;
+  a.NB = L / BK;
+  a.BH = BH;
+  a.per_xcd = (a.NB + 7) / 8;
+  a.scale = 1.0f / sqrtf((float)HD);
+  a.scale_log2 = LOG2E / sqrtf((float)HD);
+  return a;
+}
+
+extern "C" int vsa_attn_bwd_kv(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                               const float* delta, const int* k2q_ptr, const int* k2q_idx, const int* blk_cnt,
+                               const float* add_dk, const float* add_dv, int add_nb, void* dk, void* dv,
+                               int out_fp32, int BH, int L, int D, hipStream_t stream) {
+  if (int st = vsa_check_qkv(q, k, v, BH, L, D)) return st;
+  ES_REQUIRE(dout && lse && delta && k2q_ptr && blk_cnt && dk && dv, ES_ERR_INVALID, "VSA: null tensor pointer");
+  ES_REQUIRE((add_dk == nullptr && add_dv == nullptr) || add_nb >= L / BK, ES_ERR_INVALID,
+             "VSA: per-block gradient has fewer rows than blocks");
+  VsaBwdArgs a = bwd_args(q, k, v, dout, lse, delta, blk_cnt, BH, L);
+  a.row_ptr = k2q_ptr;
+  a.col_idx = k2q_idx;
+  a.add_a = add_dk;
+  a.add_b = add_dv;
+  a.add_nb = add_nb;
+  if (out_fp32) {
+    a.out_a32 = (float*)dk;
+    a.out_b32 = (float*)dv;
+  } else {
+    a.out_a = (bf16_t*)dk;
+    a.out_b = (bf16_t*)dv;
+  }
+  const long long grid = 8LL * BH * a.per_xcd;
+  ES_REQUIRE(grid < (1LL << 31), ES_ERR_UNSUPPORTED, "VSA: grid too large");
+  hipLaunchKernelGGL(vsa_bwd_kv_kernel<false>, dim3((unsigned)grid), dim3(256), 0, stream, a);
+  return check_launch("vsa_attn_bwd_kv");
+}
+
+extern "C" int vsa_attn_bwd_kv_tasks(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                                     const float* delta, const int* k2q_idx, const int* blk_cnt, const int* tasks,
+                                     const int* info, int max_tasks, const float* add_dk, const float* add_dv,
+                                     int add_nb, void* dk, void* dv, float* part_dk, float* part_dv, int BH, int L,
+                                     int D, hipStream_t stream) {
+  if (int st = vsa_check_qkv(q, k, v, BH, L, D)) return st;
+  ES_REQUIRE(dout && lse && delta && blk_cnt && tasks && info && dk && dv, ES_ERR_INVALID, "VSA: null tensor pointer");
+  ES_REQUIRE(max_tasks >= 0, ES_ERR_INVALID, "VSA: negative task capacity");
+  if (max_tasks == 0) return ES_OK;
+  VsaBwdArgs a = bwd_args(q, k, v, dout, lse, delta, blk_cnt, BH, L);
+  a.col_idx = k2q_idx;
+  a.tasks = (const int4*)tasks;
+  a.info = info;
+  a.add_a = add_dk;
+  a.add_b = add_dv;
+  a.add_nb = add_nb;
+  a.out_a = (bf16_t*)dk;
+  a.out_b = (bf16_t*)dv;
+  a.part_a = part_dk;
+  a.part_b = part_dv;
+  hipLaunchKernelGGL(vsa_bwd_kv_kernel<true>, dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
+  return check_launch("vsa_attn_bwd_kv_tasks");
+}
+
+extern "C" int vsa_attn_bwd_q(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                              const float* delta, const int* q2k_ptr, const int* q2k_idx, const int* blk_cnt,
+                              const float* add_dq, int add_nb, void* dq, float* dq_acc, int BH, int L, int D,
+                              hipStream_t stream) {
+  if (int st = vsa_check_qkv(q, k, v, BH, L, D)) return st;
+  ES_REQUIRE(dout && lse && delta && q2k_ptr && blk_cnt && (dq || dq_acc), ES_ERR_INVALID, "VSA: null tensor pointer");
+  ES_REQUIRE(add_dq == nullptr || add_nb >= L / BK, ES_ERR_INVALID, "VSA: per-block gradient has fewer rows than blocks");
+  VsaBwdArgs a = bwd_args(q, k, v, dout, lse, delta, blk_cnt, BH, L);
+  a.row_ptr = q2k_ptr;
+  a.col_idx = q2k_idx;
+  a.add_a = add_dq;
+  a.add_nb = add_nb;
+  a.out_a = (bf16_t*)dq;
+  a.out_a32 = dq_acc;
+  const long long grid = 8LL * BH * a.per_xcd;
+  ES_REQUIRE(grid < (1LL << 31), ES_ERR_UNSUPPORTED, "VSA: grid too large");
+  hipLaunchKernelGGL(vsa_bwd_q_kernel<false>, dim3((unsigned)grid), dim3(256), 0, stream, a);
+  return check_launch("vsa_attn_bwd_q");
+}
+
+extern "C" int vsa_attn_bwd_q_tasks(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                                    const float* delta, const int* q2k_idx, const int* blk_cnt, const int* tasks,
+                                    const int* info, int max_tasks, const float* add_dq, int add_nb, void* dq,
+                                    float* part_dq, int BH, int L, int D, hipStream_t stream) {
+  if (int st = vsa_check_qkv(q, k, v, BH, L, D)) return st;
+  ES_REQUIRE(dout && lse && delta && blk_cnt && tasks && info && dq, ES_ERR_INVALID, "VSA: null tensor pointer");
+  ES_REQUIRE(max_tasks >= 0, ES_ERR_INVALID, "VSA: negative task capacity");
+  if (max_tasks == 0) return ES_OK;
+  VsaBwdArgs a = bwd_args(q, k, v, dout, lse, delta, blk_cnt, BH, L);
+  a.col_idx = q2k_idx;
+  a.tasks = (const int4*)tasks;
+  a.info = info;
+  a.add_a = add_dq;
+  a.add_nb = add_nb;
+  a.out_a = (bf16_t*)dq;
+  a.part_a = part_dq;
+  hipLaunchKernelGGL(vsa_bwd_q_kernel<true>, dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
+  return check_launch("vsa_attn_bwd_q_tasks");
+}

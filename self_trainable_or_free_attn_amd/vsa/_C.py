@@ -1,0 +1,392 @@
+"""The VSA native op set (the reference's pybind module ``echosparse.vsa._C``, csrc/vsa/vsa2_api.cpp:904-941) over the
+MI355X C ABI in include/vsa_hip.h.
+
+Every op keeps the reference's name, argument order and return values; outputs are fresh torch tensors allocated here
+(the C ABI itself never allocates), workspaces are torch uint8 tensors, and every launch goes to torch's current
+stream. Shape / dtype problems raise RuntimeError with the reference's wording; there is no CPU fallback.
+
+Differences that are not visible in results: dQ is always computed without atomics (a Q-owner pass), so ``dq_word``
+only selects nothing; ``attn_bwd(..., dq_acc)`` builds the q->kv lists it needs by transposing the kv->q lists on
+the device; ``route_rows`` never materialises the [NB, NB] scores, so ``max_score_bytes`` only bounds the (b, h)
+chunking of ``route``.
+"""
+import math
+
+import torch
+
+from .. import _lib
+
+BLOCK = 64
+_FWD_VARIANT = [0]
+
+
+def _check(cond, msg):
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _tokens(x, name):
+    _check(isinstance(x, torch.Tensor) and x.is_cuda, f"{name} must be a CUDA tensor")
+    _check(x.dim() == 4 and x.is_contiguous(), f"{name} must be contiguous [B, H, L, D]")
+    _check(x.dtype == torch.bfloat16, f"{name} must be bf16 (this build computes in bf16)")
+    _check(x.shape[3] == 128, f"{name}: head dim must be 128 (this build)")
+    _check(x.shape[2] % BLOCK == 0, f"{name}: L must be a multiple of 64")
+
+
+def _i32(x, name):
+    _check(isinstance(x, torch.Tensor) and x.is_cuda and x.dtype == torch.int32 and x.is_contiguous(),
+           f"{name} must be a contiguous int32 CUDA tensor")
+
+
+def _f32(x, name):
+    _check(isinstance(x, torch.Tensor) and x.is_cuda and x.dtype == torch.float32 and x.is_contiguous(),
+           f"{name} must be a contiguous fp32 CUDA tensor")
+
+
+def _ceil64(n):
+    return (n + 63) // 64 * 64
+
+
+def has_tk():
+    """The ThunderKittens SM90 kernels do not exist on this build."""
+    return False
+
+
+def device_limits():
+    """(multiprocessor count, shared memory per block) of the current device, for split planning."""
+    p = torch.cuda.get_device_properties(torch.cuda.current_device())
+    return [p.multi_processor_count, 160 * 1024]
+
+
+def set_fwd_variant(v):
+    """Kept for API parity: one forward kernel serves every shape here."""
+    _FWD_VARIANT[0] = int(v)
+
+
+def get_fwd_variant():
+    return _FWD_VARIANT[0]
+
+
+# ------------------------------------------------------------------ pooling / fusion
+def pool_fwd(q, k, v, blk_cnt, R):
+    """(qr, kr, qc, kc, vc): router group means and whole-block means (reference vsa2_api.cpp:73-97)."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _tokens(t, n)
+    _i32(blk_cnt, "blk_cnt")
+    _check(R in (4, 8, 16, 32), "VSA2: router pool size R must be 4, 8, 16 or 32")
+    B, H, L, D = q.shape
+    NB = L // BLOCK
+    _check(blk_cnt.numel() == NB, "blk_cnt must have L/64 entries")
+    G = BLOCK // R
+    qr = torch.zeros(B, H, _ceil64(NB * G), D, device=q.device, dtype=q.dtype)
+    kr = torch.zeros_like(qr)
+    qc = torch.zeros(B, H, _ceil64(NB), D, device=q.device, dtype=q.dtype)
+    kc, vc = torch.zeros_like(qc), torch.zeros_like(qc)
+    _lib.call("vsa_pool", q, k, v, blk_cnt, qr, kr, None, qc, kc, vc, B * H, L, D, int(R))
+    return qr, kr, qc, kc, vc
+
+
+def fuse_fwd(of, oc, gate, blk_cnt, gate_act):
+    """O = O_f + act(gate) * O_c[blk] on valid rows (reference fuse.cu:3)."""
+    _tokens(of, "of")
+    B, H, L, D = of.shape
+    mode = 0
+    if gate is not None:
+        _check(gate.is_contiguous() and gate.dtype == of.dtype, "gate must be contiguous in the token dtype")
+        if gate.dim() == 3 and tuple(gate.shape) == (B, H, L):
+            mode = 1
+        elif tuple(gate.shape) == tuple(of.shape):
+            mode = 2
+        else:
+            raise RuntimeError("gate must be [B, H, L] or [B, H, L, D]")
+    o = torch.empty_like(of)
+    _lib.call("vsa_fuse_fwd", of, oc, gate, o, blk_cnt, B * H, L, D, oc.shape[2], mode, int(gate_act))
+    return o
+
+
+def fuse_bwd(dout, of, oc, gate, blk_cnt, gate_act, write_dout_f=True):
+    """(dout_f, delta_f, dout_c, delta_c, dgate) (reference fuse.cu:4-8)."""
+    _tokens(dout, "dout")
+    B, H, L, D = dout.shape
+    mode = 0 if gate is None else (1 if gate.dim() == 3 else 2)
+    dout_f = torch.empty_like(dout) if write_dout_f else None
+    delta_f = torch.empty(B, H, L, device=dout.device, dtype=torch.float32)
+    dout_c = torch.zeros(B, H, oc.shape[2], D, device=dout.device, dtype=dout.dtype)
+    delta_c = torch.zeros(B, H, oc.shape[2], device=dout.device, dtype=torch.float32)
+    dgate = torch.empty_like(gate) if gate is not None else None
+    _lib.call("vsa_fuse_bwd", dout, of, oc, gate, dout_f, delta_f, dout_c, delta_c, dgate, blk_cnt, B * H, L, D,
+              oc.shape[2], mode, int(gate_act))
+    return dout_f, delta_f, dout_c, delta_c, dgate
+
+
+def finalize(acc, add, blk_cnt, like):
+    """valid ? acc + add[blk] / cnt : 0 in like's dtype (reference fuse.cu:9)."""
+    B, H, L, D = like.shape
+    out = torch.empty(like.shape, dtype=like.dtype, device=blk_cnt.device)
+    add_nb = add.shape[2] if add is not None else 0
+    _lib.call("vsa_finalize", acc, add, add_nb, out, blk_cnt, B * H, L, D)
+    return out
+
+
+# ------------------------------------------------------------------ routers
+def _workspace(bh_count, NB, device):
+    return torch.empty(max(1, _lib.topk_workspace_bytes(bh_count, NB)), device=device, dtype=torch.uint8)
+
+
+def _block_args(qc, kc, nb):
+    _check(qc.dim() == 4 and qc.shape == kc.shape, "qc/kc must be [B, H, NBc_pad, D] (pool_fwd)")
+    _check(qc.shape[3] == 128, "qc: head dim must be 128 (this build)")
+    _check(nb >= 1 and qc.shape[2] == _ceil64(nb), "qc must hold ceil(nb/64)*64 pooled rows")
+
+
+def block_scores(qc, kc, nb, bh0=0, bh_count=0):
+    """Whole-block scores [bh_count, nb, nb] in the token dtype (reference vsa2_api.cpp:244-260)."""
+    _block_args(qc, kc, nb)
+    BH = qc.shape[0] * qc.shape[1]
+    if bh_count <= 0:
+        bh_count = BH - bh0
+    _check(bh0 >= 0 and bh_count <= 65535 and bh0 + bh_count <= BH, "bad (b,h) range")
+    scores = torch.empty(bh_count, nb, nb, device=qc.device, dtype=qc.dtype)
+    _lib.call("vsa_block_scores", qc, kc, scores, int(nb), qc.shape[2], int(bh0), int(bh_count), qc.shape[3])
+    return scores
+
+
+def _csr(B, H, NB, nnz, device):
+    i32 = dict(device=device, dtype=torch.int32)
+    return (torch.empty(B, H, NB + 1, **i32), torch.empty(max(nnz, 0), **i32), torch.empty(B, H, NB + 1, **i32),
+            torch.empty(max(nnz, 0), **i32))
+
+
+def row_topk_into(scores, topk, bh0, q2k_ptr, q2k_idx, k2q_ptr, k2q_idx):
+    """Per-row top-K of given scores into rows bh0.. of the CSR outputs (reference vsa2_api.cpp:262-282)."""
+    _check(scores.dim() == 3 and scores.shape[1] == scores.shape[2], "scores must be [BH, NB, NB]")
+    for t, n in ((q2k_ptr, "q2k_ptr"), (q2k_idx, "q2k_idx"), (k2q_ptr, "k2q_ptr"), (k2q_idx, "k2q_idx")):
+        _i32(t, n)
+    bhc, NB = scores.shape[0], scores.shape[1]
+    _check(bhc <= 65535, "too many (b,h) per top-k chunk")
+    K = max(0, min(int(topk), NB))
+    ws = _workspace(bhc, NB, scores.device)
+    _lib.call("vsa_row_topk", scores.contiguous(), NB, int(bh0), bhc, K, q2k_ptr, q2k_idx, k2q_ptr, k2q_idx, ws,
+              ws.numel())
+
+
+def route_rows(qc, kc, nb, topk, max_score_bytes=2 << 30):
+    """Original-VSA router: (q2k_ptr, q2k_idx, k2q_ptr, k2q_idx), K = min(topk, nb) per row (reference
+    vsa2_api.cpp:284-315)."""
+    _block_args(qc, kc, nb)
+    B, H = qc.shape[:2]
+    NB, BH = int(nb), B * H
+    K = max(0, min(int(topk), NB))
+    _check(BH * NB * K < 2 ** 31, "VSA: total selected blocks exceed int32 CSR range")
+    out = _csr(B, H, NB, BH * NB * K, qc.device)
+    chunk = min(BH, 65535)
+    ws = _workspace(chunk, NB, qc.device)
+    for bh0 in range(0, BH, chunk):
+        cnt = min(chunk, BH - bh0)
+        _lib.call("vsa_route_rows", qc, kc, NB, qc.shape[2], bh0, cnt, K, qc.shape[3], *out, ws, ws.numel())
+    return list(out)
+
+
+def router_lse(qr, kr, blk_cnt, R):
+    """lse2 [B, H, Lr_pad] of every pooled query row (reference vsa2_api.cpp:122-135)."""
+    B, H, Lr_pad, D = qr.shape
+    lse2 = torch.empty(B, H, Lr_pad, device=qr.device, dtype=torch.float32)
+    _lib.call("vsa_router_lse", qr, kr, blk_cnt, lse2, blk_cnt.numel(), int(R), B * H, D)
+    return lse2
+
+
+def router_scores(qr, kr, lse2, blk_cnt, R, row_norm, bh0=0, bh_count=0):
+    """PSP block scores [bh_count, NB, NB] fp32 (reference vsa2_api.cpp:137-155)."""
+    B, H, _, D = qr.shape
+    NB = blk_cnt.numel()
+    if bh_count <= 0:
+        bh_count = B * H - bh0
+    scores = torch.empty(bh_count, NB, NB, device=qr.device, dtype=torch.float32)
+    _lib.call("vsa_router_scores", qr, kr, lse2, blk_cnt, scores, NB, int(R), int(row_norm), int(bh0), int(bh_count), D)
+    return scores
+
+
+def global_topk_into(scores, budget, bh0, q2k_ptr, q2k_idx, k2q_ptr, k2q_idx):
+    """Exact global top-k of fp32 scores into rows bh0.. of the CSR outputs (reference vsa2_api.cpp:157-178)."""
+    _check(scores.dtype == torch.float32 and scores.dim() == 3 and scores.shape[1] == scores.shape[2],
+           "scores must be fp32 [BH, NB, NB]")
+    bhc, NB = scores.shape[0], scores.shape[1]
+    _check(bhc <= 65535, "too many (b,h) per top-k chunk")
+    ws = _workspace(bhc, NB, scores.device)
+    _lib.call("vsa_global_topk", scores.contiguous(), NB, int(bh0), bhc, int(budget), q2k_ptr, q2k_idx, k2q_ptr,
+              k2q_idx, ws, ws.numel())
+
+
+def route(qr, kr, blk_cnt, R, budget, row_norm, max_score_bytes=2 << 30):
+    """VSA2 router: lse pass, then scores + exact global top-k in (b, h) chunks bounded by max_score_bytes
+    (reference vsa2_api.cpp:183-219)."""
+    _i32(blk_cnt, "blk_cnt")
+    B, H = qr.shape[:2]
+    NB, BH = blk_cnt.numel(), B * H
+    nn = NB * NB
+    keff = max(0, min(int(budget), nn))
+    _check(BH * keff < 2 ** 31, "VSA2: total selected blocks exceed int32 CSR range")
+    out = _csr(B, H, NB, BH * keff, qr.device)
+    lse2 = router_lse(qr, kr, blk_cnt, R)
+    chunk = int(max(1, min(BH, int(max_score_bytes) // max(nn * 4, 1), 65535)))
+    ws = _workspace(chunk, NB, qr.device)
+    scores = torch.empty(chunk, NB, NB, device=qr.device, dtype=torch.float32)
+    for bh0 in range(0, BH, chunk):
+        cnt = min(chunk, BH - bh0)
+        s = scores[:cnt]
+        _lib.call("vsa_router_scores", qr, kr, lse2, blk_cnt, s, NB, int(R), int(row_norm), bh0, cnt, qr.shape[3])
+        _lib.call("vsa_global_topk", s, NB, bh0, cnt, int(budget), *out, ws, ws.numel())
+    return list(out)
+
+
+def csr_transpose(ptr, idx):
+    """(ptr_T, idx_T): the column lists (ascending) of a CSR selection, same absolute offsets per (b, h)."""
+    B, H, n1 = ptr.shape
+    NB, BH = n1 - 1, B * H
+    out_ptr = torch.empty_like(ptr)
+    out_idx = torch.empty_like(idx)
+    chunk = min(BH, 65535)
+    ws = _workspace(chunk, NB, ptr.device)
+    for bh0 in range(0, BH, chunk):
+        cnt = min(chunk, BH - bh0)
+        _lib.call("vsa_csr_transpose", ptr, idx, NB, bh0, cnt, out_ptr, out_idx, ws, ws.numel())
+    return out_ptr, out_idx
+
+
+# ------------------------------------------------------------------ attention
+def _attn_args(q, k, v, blk_cnt):
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _tokens(t, n)
+    _i32(blk_cnt, "blk_cnt")
+    _check(q.shape == k.shape and q.shape == v.shape, "q/k/v must share [B,H,L,D] (MHA self-attention)")
+    _check(blk_cnt.numel() == q.shape[2] // BLOCK, "metadata shape mismatch")
+
+
+def attn_fwd(q, k, v, row_ptr, col_idx, blk_cnt, use_tk=False):
+    """(o, lse): fine attention over the q2k CSR (reference vsa2_api.cpp:318-348)."""
+    _attn_args(q, k, v, blk_cnt)
+    _i32(row_ptr, "row_ptr")
+    _i32(col_idx, "col_idx")
+    B, H, L, D = q.shape
+    _check(row_ptr.numel() == B * H * (L // BLOCK + 1), "metadata shape mismatch")
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
+    _lib.call("vsa_attn_fwd", q, k, v, row_ptr, col_idx, blk_cnt, o, lse, B * H, L, D)
+    return o, lse
+
+
+def attn_bwd(q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, dq_acc=None, add_dk=None, add_dv=None,
+             out_fp32=False, dq_word=False):
+    """(dk, dv) over the k2q CSR, + add / cnt; with dq_acc, also dq_acc += dQ (reference vsa2_api.cpp:353-416)."""
+    _attn_args(q, k, v, blk_cnt)
+    B, H, L, D = q.shape
+    if dq_acc is not None:
+        _check(dq_acc.dtype == torch.float32 and dq_acc.shape == q.shape, "dq_acc must be fp32 like q")
+    f = dict(device=q.device, dtype=torch.float32) if out_fp32 else dict(device=q.device, dtype=q.dtype)
+    dk, dv = torch.empty(q.shape, **f), torch.empty(q.shape, **f)
+    add_nb = add_dk.shape[2] if add_dk is not None else (add_dv.shape[2] if add_dv is not None else 0)
+    _lib.call("vsa_attn_bwd_kv", q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, add_dk, add_dv, add_nb, dk, dv,
+              1 if out_fp32 else 0, B * H, L, D)
+    if dq_acc is not None:
+        q2k_ptr, q2k_idx = csr_transpose(row_ptr, col_idx)
+        _lib.call("vsa_attn_bwd_q", q, k, v, dout, lse, delta, q2k_ptr, q2k_idx, blk_cnt, None, 0, None, dq_acc,
+                  B * H, L, D)
+    return dk, dv
+
+
+def attn_bwd_q(q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, add_dq=None):
+    """dQ over the q2k CSR without atomics, + add_dq / cnt (reference vsa2_api.cpp:419-457)."""
+    _attn_args(q, k, v, blk_cnt)
+    B, H, L, D = q.shape
+    dq = torch.empty_like(q)
+    _lib.call("vsa_attn_bwd_q", q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, add_dq,
+              add_dq.shape[2] if add_dq is not None else 0, dq, None, B * H, L, D)
+    return dq
+
+
+# ------------------------------------------------------------------ split-KV
+def split_plan(ptr, chunk, max_slots, min_len=0, rel_mean=0.0, tail_frac=0.0, resident=1, budget=-1):
+    """(tasks [NR + max_slots, 4], merges [max(1, min(NR, max_slots // 2)), 4], info [8]) on the device
+    (reference vsa2_api.cpp:464-508)."""
+    _i32(ptr, "ptr")
+    _check(ptr.dim() == 3 and ptr.shape[2] >= 2, "ptr must be [B, H, NB+1]")
+    _check(1 <= chunk <= (1 << 30), "split chunk must be in [1, 2^30]")
+    _check(0 <= max_slots < (1 << 30), "bad max_slots")
+    _check(rel_mean >= 0.0 and tail_frac >= 0.0 and resident >= 1, "bad split policy")
+    B, H, n1 = ptr.shape
+    NR = B * H * (n1 - 1)
+    i32 = dict(device=ptr.device, dtype=torch.int32)
+    tasks = torch.empty(NR + int(max_slots), 4, **i32)
+    merges = torch.empty(max(1, min(NR, int(max_slots) // 2)), 4, **i32)
+    info = torch.empty(8, **i32)
+    _lib.call("vsa_split_plan", ptr, B * H, n1 - 1, int(chunk), int(max_slots), int(min_len), float(rel_mean),
+              float(tail_frac), int(resident), int(budget), tasks, merges, info)
+    return tasks, merges, info
+
+
+def attn_fwd_tasks(q, k, v, col_idx, blk_cnt, tasks, info, part_o, part_lse):
+    """(o, lse) of direct tasks; split chunks fill part_o / part_lse (reference vsa2_api.cpp:524-555)."""
+    _attn_args(q, k, v, blk_cnt)
+    B, H, L, D = q.shape
+    _check(part_lse.numel() == part_o.numel() // D, "part_lse must be [slots, 64]")
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
+    _lib.call("vsa_attn_fwd_tasks", q, k, v, col_idx, blk_cnt, tasks, info, tasks.shape[0], o, lse,
+              part_o if part_o.numel() else None, part_lse if part_lse.numel() else None, B * H, L, D)
+    return o, lse
+
+
+def split_merge_fwd(part_o, part_lse, merges, info, blk_cnt, o, lse, mask_rows=True):
+    """Ordered LSE merge of split rows into o / lse in place (reference vsa2_api.cpp:557-583)."""
+    if part_o.numel() == 0:
+        return
+    B, H, L, D = o.shape
+    _lib.call("vsa_split_merge_fwd", part_o, part_lse, merges, info, merges.shape[0], blk_cnt, o, lse, B * H, L, D,
+              1 if mask_rows else 0)
+
+
+def split_merge_sum(part, merges, info, add, blk_cnt, out):
+    """Split rows of out = sum of partials + add / cnt, in place (reference vsa2_api.cpp:586-620)."""
+    if part.numel() == 0:
+        return
+    B, H, L, D = out.shape
+    f32 = out.dtype == torch.float32
+    _lib.call("vsa_split_merge_sum", part, merges, info, merges.shape[0], add, add.shape[2] if add is not None else 0,
+              blk_cnt, None if f32 else out, out if f32 else None, B * H, L, D)
+
+
+def attn_bwd_tasks(q, k, v, dout, lse, delta, col_idx, blk_cnt, tasks, info, dq_acc, add_dk, add_dv, part_dk,
+                   part_dv, dq_word=False):
+    """(dk, dv) of direct k2q tasks; split chunks fill part_dk / part_dv (reference vsa2_api.cpp:624-685).
+    dq_acc (optional) needs the q->kv lists: pass the plan's list with ``csr_transpose`` results through
+    attn_bwd_q instead; here it raises, like an atomic dQ that this build does not have."""
+    _check(dq_acc is None, "attn_bwd_tasks: dQ comes from attn_bwd_q_tasks on this build (no atomics)")
+    _attn_args(q, k, v, blk_cnt)
+    B, H, L, D = q.shape
+    dk, dv = torch.empty_like(q), torch.empty_like(q)
+    add_nb = add_dk.shape[2] if add_dk is not None else (add_dv.shape[2] if add_dv is not None else 0)
+    _lib.call("vsa_attn_bwd_kv_tasks", q, k, v, dout, lse, delta, col_idx, blk_cnt, tasks, info, tasks.shape[0],
+              add_dk, add_dv, add_nb, dk, dv, part_dk if part_dk.numel() else None,
+              part_dv if part_dv.numel() else None, B * H, L, D)
+    return dk, dv
+
+
+def attn_bwd_q_tasks(q, k, v, dout, lse, delta, col_idx, blk_cnt, tasks, info, add_dq, part_dq):
+    """dQ of direct q2k tasks; split chunks fill part_dq (reference vsa2_api.cpp:687-730)."""
+    _attn_args(q, k, v, blk_cnt)
+    B, H, L, D = q.shape
+    dq = torch.empty_like(q)
+    _lib.call("vsa_attn_bwd_q_tasks", q, k, v, dout, lse, delta, col_idx, blk_cnt, tasks, info, tasks.shape[0],
+              add_dq, add_dq.shape[2] if add_dq is not None else 0, dq, part_dq if part_dq.numel() else None,
+              B * H, L, D)
+    return dq
+
+
+def attn_bwd_q_acc(q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, dq_acc):
+    """dq_acc += dQ over the q2k CSR (fp32, valid rows); the deterministic stand-in for an atomic dQ accumulator."""
+    _attn_args(q, k, v, blk_cnt)
+    _f32(dq_acc, "dq_acc")
+    B, H, L, D = q.shape
+    _lib.call("vsa_attn_bwd_q", q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, None, 0, None, dq_acc, B * H,
+              L, D)
+    return dq_acc

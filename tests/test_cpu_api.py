@@ -86,10 +86,16 @@ def test_budget_matches_reference_rule():
     assert EchoSparseAttention(density=1.0)._budget(65) == (65, 0)
 
 
+HEADERS = ("echosparse_hip.h", "vsa_hip.h")
+
+
+def header_text():
+    text = "".join(open(os.path.join(ROOT, "include", h)).read() for h in HEADERS)
+    return re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+
+
 def declared_entry_points():
-    text = open(os.path.join(ROOT, "include", "echosparse_hip.h")).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(es_[a-z0-9_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b((?:es|vsa)_[a-z0-9_]+)\s*\(", header_text())))
 
 
 def library():
@@ -101,7 +107,7 @@ def library():
 
 def test_library_exports_every_declared_entry_point():
     names = declared_entry_points()
-    assert len(names) >= 14 and "es_sparse_attention" in names
+    assert len(names) >= 35 and "es_sparse_attention" in names and "vsa_attn_bwd_kv" in names
     so = library()
     missing = [n for n in names if not hasattr(so, n)]
     assert not missing, missing
@@ -113,9 +119,7 @@ def test_ctypes_signatures_cover_the_header():
     """Every stream-taking entry point of the header has an argument list in the binding, with the header's
     argument count (the binding appends the stream)."""
     from self_trainable_or_free_attn_amd import _lib
-    text = open(os.path.join(ROOT, "include", "echosparse_hip.h")).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    for name, args in re.findall(r"\b(es_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+    for name, args in re.findall(r"\b((?:es|vsa)_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", header_text()):
         n = len([a for a in args.split(",") if a.strip() and a.strip() != "void"])
         if "hipStream_t" in args:
             assert name in _lib.SIGNATURES, name
@@ -134,3 +138,12 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert st == 2 and b"head dimension must be 128" in so.es_last_error_string()
     st = so.es_block_means(None, p, p, p, ctypes.c_int(64), ctypes.c_int(1), ctypes.c_int(128), ctypes.c_void_p(0))
     assert st == 1 and b"null" in so.es_last_error_string()
+
+
+def test_host_tensors_are_refused_before_any_launch():
+    """A host tensor's address given to a kernel would fault the GPU: the binding refuses it first."""
+    import torch
+    from self_trainable_or_free_attn_amd import _lib
+    x = torch.zeros(4)
+    with pytest.raises(RuntimeError, match="must live on the GPU"):
+        _lib.call("vsa_finalize", None, None, 0, x, x, 1, 64, 128)
