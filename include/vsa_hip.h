@@ -129,10 +129,12 @@ int vsa_router_scores(const void* qr, const void* kr, const float* lse2, const i
                       int R, int row_norm, int bh0, int bh_count, int D, hipStream_t stream);
 
 /* Exact global top-k of fp32 scores [bh_count, NB, NB]: k = min(budget, NB^2) entries per (b, h), score desc then
- * flat index asc, into the CSR of rows bh0 .. (offsets b * k). NB <= 4096.
+ * flat index asc, into the CSR of rows bh0 .. (offsets b * k), and (bits_out != NULL) the selection bitmap rows
+ * bits_out [BH, NB, ceil(NB / 32)] of those (b, h). NB <= 4096.
  * Replaces csrc/vsa/vsa2_api.cpp:157-178 global_topk_into (topk.cu:69-578). */
 int vsa_global_topk(const float* scores, int NB, int bh0, int bh_count, long long budget, int* q2k_ptr, int* q2k_idx,
-                    int* k2q_ptr, int* k2q_idx, void* workspace, size_t workspace_bytes, hipStream_t stream);
+                    int* k2q_ptr, int* k2q_idx, unsigned* bits_out, void* workspace, size_t workspace_bytes,
+                    hipStream_t stream);
 
 /* Transposed CSR (column lists, ascending) of rows bh0 .. with the same absolute base per (b, h). No reference
  * counterpart as an entry point: the reference builds k2q only inside its routers (topk.cu:405-459); this serves
@@ -160,6 +162,55 @@ int vsa_split_merge_fwd(const float* part_o, const float* part_lse, const int* m
 int vsa_split_merge_sum(const float* part, const int* merges, const int* info, int max_merges, const float* add,
                         int add_nb, const int* blk_cnt, void* out, float* out_f32, int BH, int L, int D,
                         hipStream_t stream);
+
+/* ---------------------------------------------------------------- VSA2 three-tier representatives */
+
+/* Representative tables: k_mid / v_mid [BH, ceil64(NB * RM), D] = means of the RM contiguous 64 / RM-token groups
+ * of every block (row blk * RM + g), k_tail / v_tail [BH, ceil64(NB), D] = block means, lc_mid [NB * RM] and
+ * lc_tail [NB] = log2 of the valid tokens (-inf: empty group); padding rows are not written. Replaces
+ * experiments/vsa2_representative/csrc/rep/rep_api.cpp rep_build (rep_pool.cu:23-57). */
+int vsa_rep_build(const void* k, const void* v, const int* blk_cnt, void* k_mid, void* v_mid, float* lc_mid,
+                  void* k_tail, void* v_tail, float* lc_tail, int BH, int L, int D, int RM, hipStream_t stream);
+
+/* Three-tier forward: one softmax over the tier-A tokens (q2k CSR), the tier-B representatives (bits_ab & ~bits_a)
+ * and the tier-C means (~bits_ab), each representative column with + log2(count); O bf16, lse natural. phases:
+ * 1 | 2 | 4 selects the tiers. NB <= 2048. Replaces rep_api.cpp rep_attn_fwd (rep_attn_fwd.cu:37). */
+int vsa_rep_attn_fwd(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
+                     const float* lc_mid, const void* k_tail, const void* v_tail, const float* lc_tail,
+                     const int* q2k_ptr, const int* q2k_idx, const unsigned* bits_a, const unsigned* bits_ab,
+                     const int* blk_cnt, void* out, float* lse, int BH, int L, int D, int RM, int phases,
+                     hipStream_t stream);
+
+/* dQ of the three-tier attention (deterministic, no atomics), + dq_acc (fp32, optional) + add_dq / blk_cnt
+ * (optional); padding rows 0. Replaces the dQ part of rep_api.cpp rep_attn_bwd_q (rep_attn_bwd.cu:141). */
+int vsa_rep_attn_bwd_q(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
+                       const float* lc_mid, const void* k_tail, const void* v_tail, const float* lc_tail,
+                       const void* dout, const float* lse, const float* delta, const int* q2k_ptr,
+                       const int* q2k_idx, const unsigned* bits_a, const unsigned* bits_ab, const int* blk_cnt,
+                       const float* add_dq, int add_nb, const float* dq_acc, void* dq, int BH, int L, int D, int RM,
+                       int phases, hipStream_t stream);
+
+/* dK / dV of one representative table (tier 2: the mid table over tier B, tier 4: the tail table over tier C),
+ * accumulated into dk_tab / dv_tab (fp32, the table's row layout) by a KV-owner pass: no atomics, deterministic.
+ * Replaces the representative dK / dV atomics of rep_api.cpp rep_attn_bwd_q (rep_attn_bwd.cu:141). */
+int vsa_rep_bwd_tables(const void* q, const void* dout, const void* k_tab, const void* v_tab, const float* lc,
+                       const float* lse, const float* delta, const unsigned* bits_a, const unsigned* bits_ab,
+                       float* dk_tab, float* dv_tab, int BH, int L, int D, int RM, int tier, hipStream_t stream);
+
+/* dK, dV (bf16) = acc (fp32 tier-A token gradients, optional) + dk_mid[group] / c_group + dk_tail[blk] / c_blk on
+ * valid rows, 0 on padding. Replaces rep_api.cpp rep_unpool (rep_pool.cu:59-88). */
+int vsa_rep_unpool(const float* acc_k, const float* acc_v, const float* dk_mid, const float* dv_mid,
+                   const float* dk_tail, const float* dv_tail, const int* blk_cnt, void* dk, void* dv, int BH, int L,
+                   int D, int RM, hipStream_t stream);
+
+/* out [BH, L] = rowsum(x * y) on valid rows, 0 on padding. Replaces rep_api.cpp row_dot (rep_pool.cu:90-112). */
+int vsa_row_dot(const void* x, const void* y, const int* blk_cnt, float* out, int BH, int L, int D,
+                hipStream_t stream);
+
+/* Tier-B CSR lists: the A|B lists without the tier-A columns, b_ptr = ab_ptr - a_ptr. Replaces
+ * rep_pool.cu:114-140 tier_b_lists. */
+int vsa_tier_b_lists(const int* ab_ptr, const int* ab_idx, const int* a_ptr, const unsigned* bits_a, int* b_ptr,
+                     int* b_idx, int BH, int NB, hipStream_t stream);
 
 #ifdef __cplusplus
 }

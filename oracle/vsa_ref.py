@@ -284,3 +284,67 @@ def merge_fwd(part_o, part_lse2):
     o = (w[..., None] * po).sum(0) / np.where(s > 0, s, 1.0)[..., None]
     lse = np.where(s > 0, (M + np.log2(np.where(s > 0, s, 1.0))) * math.log(2.0), -np.inf)
     return o, lse
+
+
+# --------------------------------------------------------------------------- VSA2 three-tier representatives
+def rep_tables(k, v, blk_cnt, RM):
+    """(k_mid, v_mid [B, H, NB * RM, D], k_tail, v_tail [B, H, NB, D], lc_mid [NB * RM], lc_tail [NB]): the pooled
+    group / block means of the kernels' float32 order (see `pool`, groups of 64 / RM tokens) and log2 counts, -inf
+    for an empty group (reference experiments/vsa2_representative/vsa2_rep/reference.py:23-50)."""
+    km, kt = pool(k, blk_cnt, BLOCK // RM)
+    vm, vt = pool(v, blk_cnt, BLOCK // RM)
+    cnt = np.asarray(blk_cnt, np.int64)
+    gs = BLOCK // RM
+    n = np.clip(cnt[:, None] - np.arange(RM)[None, :] * gs, 0, gs).reshape(-1)
+    with np.errstate(divide="ignore"):
+        lc_mid = np.where(n > 0, np.log2(np.maximum(n, 1)), -np.inf)
+        lc_tail = np.log2(cnt.astype(np.float64))
+    return km, vm, kt, vt, lc_mid, lc_tail
+
+
+def rep_fine_torch(q, k, v, blk_cnt, mask_a, mask_ab, RM, phases=7, tables=None):
+    """Three-tier attention as a torch float64 graph: one softmax over tier-A tokens (mask_a), tier-B representatives
+    (mask_ab & ~mask_a; means of 64 / RM-token groups with + ln c) and tier-C block means (~mask_ab, + ln cnt); O = 0
+    and lse = -inf on padding rows and rows with no column (reference vsa2_rep/reference.py:53-96). The means are
+    functions of k / v (so autograd reaches the tokens); `tables` = (k_mid, v_mid, k_tail, v_tail) overrides their
+    values (e.g. the bf16 tables the kernels use) straight-through. Returns (O, lse natural)."""
+    import torch
+    B, H, L, D = q.shape
+    NB, gs = L // BLOCK, BLOCK // RM
+    cnt = np.asarray(blk_cnt, np.int64)
+    valid = torch.as_tensor(token_valid(cnt, L))
+    z = valid[None, None, :, None].to(q.dtype)
+    ng = torch.as_tensor(np.clip(cnt[:, None] - np.arange(RM)[None, :] * gs, 0, gs).reshape(-1), dtype=q.dtype)
+
+    def means(x):
+        xs = (x * z).reshape(B, H, NB, RM, gs, D).sum(4).reshape(B, H, NB * RM, D)
+        mid = xs / ng.clamp(min=1)[None, None, :, None]
+        tail = xs.reshape(B, H, NB, RM, D).sum(3) / torch.as_tensor(cnt, dtype=q.dtype)[None, None, :, None]
+        return mid, tail
+
+    km, kt = means(k)
+    vm, vt = means(v)
+    if tables is not None:
+        over = [torch.as_tensor(np.asarray(t, np.float64)) for t in tables]
+        km, vm, kt, vt = (m + (o - m).detach() for m, o in zip((km, vm, kt, vt), over))
+    a = np.asarray(mask_a, bool) & bool(phases & 1)
+    ab = np.asarray(mask_ab, bool)
+    tb = (ab & ~np.asarray(mask_a, bool)) & bool(phases & 2)
+    tc = (~ab) & bool(phases & 4)
+    blk = np.arange(L) // BLOCK
+    vis_a = a[:, :, blk][:, :, :, blk] & token_valid(cnt, L)[None, None, None, :]
+    vis_b = np.repeat(tb, RM, axis=3)[:, :, blk] & (ng.numpy() > 0)[None, None, None, :]
+    vis_c = tc[:, :, blk]
+    vis = torch.as_tensor(np.concatenate([vis_a, vis_b, vis_c], axis=3))
+    with np.errstate(divide="ignore"):
+        bias = torch.as_tensor(np.concatenate([np.zeros(L), np.log(np.maximum(ng.numpy(), 1)), np.log(cnt)]))
+    Kc = torch.cat([k, km, kt], 2)
+    Vc = torch.cat([v, vm, vt], 2)
+    s = (q @ Kc.transpose(-1, -2)) / math.sqrt(D) + bias
+    s = s.masked_fill(~vis, float("-inf"))
+    has = vis.any(-1, keepdim=True) & valid[None, None, :, None]
+    s_safe = torch.where(has, s, torch.zeros_like(s))
+    p = torch.softmax(s_safe, -1) * has
+    o = p @ Vc
+    lse = torch.where(has[..., 0], torch.logsumexp(s_safe, -1), torch.full_like(s[..., 0], float("-inf")))
+    return o, lse

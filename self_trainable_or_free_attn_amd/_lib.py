@@ -47,11 +47,18 @@ SIGNATURES = {
     "vsa_row_topk": [P, I, I, I, I, P, P, P, P, P, Z],
     "vsa_router_lse": [P, P, P, P, I, I, I, I],
     "vsa_router_scores": [P, P, P, P, P, I, I, I, I, I, I],
-    "vsa_global_topk": [P, I, I, I, LL, P, P, P, P, P, Z],
+    "vsa_global_topk": [P, I, I, I, LL, P, P, P, P, P, P, Z],
     "vsa_csr_transpose": [P, P, I, I, I, P, P, P, Z],
     "vsa_split_plan": [P, I, I, I, I, I, DB, DB, I, I, P, P, P],
     "vsa_split_merge_fwd": [P, P, P, P, I, P, P, P, I, I, I, I],
     "vsa_split_merge_sum": [P, P, P, I, P, I, P, P, P, I, I, I],
+    "vsa_rep_build": [P, P, P, P, P, P, P, P, P, I, I, I, I],
+    "vsa_rep_attn_fwd": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I],
+    "vsa_rep_attn_bwd_q": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I, I, I, I, I],
+    "vsa_rep_bwd_tables": [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I],
+    "vsa_rep_unpool": [P, P, P, P, P, P, P, P, P, I, I, I, I],
+    "vsa_row_dot": [P, P, P, P, I, I, I],
+    "vsa_tier_b_lists": [P, P, P, P, P, P, I, I],
 }
 NO_STREAM = {"es_representatives_workspace": ([I, I, I], Z), "es_last_error_string": ([], ctypes.c_char_p),
              "es_abi_version": ([], I), "vsa_topk_workspace": ([I, I], Z)}

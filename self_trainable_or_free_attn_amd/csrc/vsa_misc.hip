@@ -64,8 +64,8 @@ constexpr int POOL_BLOCKS = 4;  // 64-token blocks per workgroup
 __global__ __launch_bounds__(192) void pool_kernel(PoolArgs a) {
   const int sub = threadIdx.x / 48, t = threadIdx.x % 48;
   const int blk = blockIdx.x * POOL_BLOCKS + sub;
-  if (blk >= a.NB) return;
   const int which = t / 16, c8 = (t % 16) * 8;
+  if (blk >= a.NB || a.src[which] == nullptr) return;  // a null source: that tensor is not pooled
   const size_t bh = blockIdx.y;
   const int n = a.blk_cnt[blk];
   const bf16_t* src = a.src[which] + (bh * a.L + (size_t)blk * BK) * HD + c8;
@@ -242,6 +242,18 @@ __global__ __launch_bounds__(256) void finalize_kernel(const float* __restrict__
   }
 }
 
+// log2 of the valid tokens of every representative group (RM per block) and of every block; -inf when empty
+__global__ void rep_counts_kernel(const int* __restrict__ blk_cnt, float* __restrict__ lc_mid,
+                                  float* __restrict__ lc_tail, int NB, int RM) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= NB * RM) return;
+  const int blk = e / RM, g = e - blk * RM, gs = BK / RM;
+  const int cnt = blk_cnt[blk];
+  const int n = min(max(cnt - g * gs, 0), gs);
+  lc_mid[e] = n > 0 ? log2f((float)n) : -INFINITY;
+  if (g == 0) lc_tail[blk] = cnt > 0 ? log2f((float)cnt) : -INFINITY;
+}
+
 }  // namespace
 
 }  // namespace es
@@ -308,4 +320,24 @@ extern "C" int vsa_finalize(const float* acc, const float* add, int add_nb, void
   hipLaunchKernelGGL(finalize_kernel, dim3((NB + 3) / 4, BH), dim3(256), 0, stream, acc, add, (bf16_t*)out, blk_cnt,
                      NB, L, add_nb);
   return check_launch("vsa_finalize");
+}
+
+extern "C" int vsa_rep_build(const void* k, const void* v, const int* blk_cnt, void* k_mid, void* v_mid,
+                             float* lc_mid, void* k_tail, void* v_tail, float* lc_tail, int BH, int L, int D, int RM,
+                             hipStream_t stream) {
+  if (int st = check_tokens(BH, L, D)) return st;
+  ES_REQUIRE(k && v && blk_cnt && k_mid && v_mid && lc_mid && k_tail && v_tail && lc_tail, ES_ERR_INVALID,
+             "VSA2-rep: null tensor pointer");
+  ES_REQUIRE(RM == 1 || RM == 2 || RM == 4 || RM == 8 || RM == 16, ES_ERR_INVALID,
+             "RepTiers.mid_reps must be one of (1, 2, 4, 8, 16)");
+  const int NB = L / BK, R = BK / RM;
+  // the mid table is the pooled groups of R = 64 / RM tokens, the tail table the block means
+  PoolArgs a{{nullptr, (const bf16_t*)k, (const bf16_t*)v},
+             {nullptr, (bf16_t*)k_mid, (bf16_t*)v_mid},
+             {nullptr, (bf16_t*)k_tail, (bf16_t*)v_tail},
+             blk_cnt, NB, L, R, RM, (NB * RM + 63) / 64 * 64, (NB + 63) / 64 * 64};
+  hipLaunchKernelGGL(pool_kernel, dim3((NB + POOL_BLOCKS - 1) / POOL_BLOCKS, BH), dim3(192), 0, stream, a);
+  hipLaunchKernelGGL(rep_counts_kernel, dim3((NB * RM + 255) / 256), dim3(256), 0, stream, blk_cnt, lc_mid, lc_tail,
+                     NB, RM);
+  return check_launch("vsa_rep_build");
 }

@@ -1,0 +1,794 @@
+// VSA2 three-tier representative attention (gfx950): tier A = the selected 64-token blocks, tier B = RM
+// representatives (contiguous 64 / RM-token group means) of the next-ranked blocks, tier C = the block mean of every
+// other block. A representative of c tokens is one softmax column with + log2(c) on its logit (reference
+// experiments/vsa2_representative/csrc/rep/rep_kernels.h:1-40, vsa2_rep/reference.py:53-96).
+//
+// Tables (built by vsa_rep_build): k_mid / v_mid [BH, ceil64(NB * RM), D] (row blk * RM + g), k_tail / v_tail
+// [BH, ceil64(NB), D] (row blk), lc_mid [NB * RM] and lc_tail [NB] log2 counts (-inf: empty group), shared by
+// every head. Tier membership of pair (query block i, kv block j) comes from the bitmaps bits_a / bits_ab
+// [BH, NB, W], W = ceil(NB / 32): A = a, B = ab & ~a, C = ~ab.
+//
+//   rep_fwd_kernel      one workgroup per (query block, head), the VSA fine forward's layout (2 row groups x 2 key
+//                       halves, chunks staged in LDS) over one column stream: tier-A blocks of the CSR list, then
+//                       64-row chunks of tier-B representatives, then 64-row chunks of tier-C means; the B and C
+//                       block lists are compacted from the bitmaps into LDS at the start (wave ballots).
+//   rep_bwd_q_kernel    dQ over the same stream (S^T, dP^T, dQ^T += K^T dS^T), deterministic.
+//   rep_bwd_tab_kernel  dK / dV of the representative tables, KV-owner: a workgroup owns 64 table rows and walks
+//                       every query block that has one of its pairs in the tier (pairs outside get P = 0), so the
+//                       shared rows need no atomics. Tier-A token dK / dV come from the fine KV-owner kernel.
+//   rep_unpool_kernel   dX = acc + dk_mid[group] / c_group + dk_tail[blk] / c_blk on valid rows (the adjoint of the
+//                       means), tier_b_lists_kernel (A|B lists minus tier A), row_dot_kernel (delta).
+#include "../../include/vsa_hip.h"
+#include "common.h"
+
+namespace es {
+
+namespace {
+
+constexpr float LN2_F = 0.6931471805599453f;
+constexpr float SLACK = 8.0f;
+constexpr int REP_MAX_NB = 2048;
+enum { PH_A = 1, PH_B = 2, PH_C = 4 };
+
+struct RepArgs {
+  const bf16_t *q, *k, *v, *dout;
+  const bf16_t *k_mid, *v_mid, *k_tail, *v_tail;
+  const float *lc_mid, *lc_tail;
+  const float *lse, *delta;
+  bf16_t* out;
+  float* lse_out;
+  const int *row_ptr, *col_idx, *blk_cnt;
+  const unsigned *bits_a, *bits_ab;
+  const float* add_dq;
+  int add_nb;
+  float* dq_acc;
+  int L, NB, RM, W, BH, per_xcd, phases, mid_rows, tail_rows;
+  float scale_log2, scale;
+};
+
+// The column stream of one (query block, head): chunk kinds A (one 64-token block each), B (64 representative
+// rows), C (64 block means). Built once per workgroup; every lane can then name the 4 rows it stages per chunk.
+struct Stream {
+  int nA, nBrows, nC;  // tier-A blocks, tier-B representative rows, tier-C blocks
+  int cA, cB, cC;      // chunks of each kind
+  int beg;             // tier-A list start
+};
+
+__device__ __forceinline__ unsigned row_word(const unsigned* bits, size_t row, int W, int w) {
+  return bits[row * W + w];
+}
+
+// compact tier B (ab & ~a) and tier C (~ab) blocks of bitmap row `row` into LDS lists (wave 0)
+__device__ void build_lists(const RepArgs& a, size_t row, unsigned short* blist, unsigned short* clist, int* counts) {
+  const int l = threadIdx.x & 63;
+  int nb_run = 0, nc_run = 0;
+  for (int w0 = 0; w0 < a.W; w0 += 64) {
+    const int w = w0 + l;
+    unsigned bm = 0, cm = 0;
+    if (w < a.W) {
+      const unsigned av = row_word(a.bits_a, row, a.W, w), abv = row_word(a.bits_ab, row, a.W, w);
+      const int lo = w * 32;
+      const unsigned valid = a.NB - lo >= 32 ? 0xffffffffu : ((1u << (a.NB - lo)) - 1u);
+      bm = (a.phases & PH_B) ? (abv & ~av & valid) : 0u;
+      cm = (a.phases & PH_C) ? (~abv & valid) : 0u;
+    }
+    int pb = __popc(bm), pc = __popc(cm), ib = pb, ic = pc;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int yb = __shfl_up(ib, d, 64), yc = __shfl_up(ic, d, 64);
+      if (l >= d) {
+        ib += yb;
+        ic += yc;
+      }
+    }
+    int ob = nb_run + ib - pb, oc = nc_run + ic - pc;
+    while (bm) {
+      const int b = __ffs(bm) - 1;
+      blist[ob++] = (unsigned short)(w * 32 + b);
+      bm &= bm - 1;
+    }
+    while (cm) {
+      const int b = __ffs(cm) - 1;
+      clist[oc++] = (unsigned short)(w * 32 + b);
+      cm &= cm - 1;
+    }
+    nb_run += __shfl(ib, 63, 64);
+    nc_run += __shfl(ic, 63, 64);
+  }
+  if (l == 0) {
+    counts[0] = nb_run;
+    counts[1] = nc_run;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ forward / dQ
+template <bool BWD>
+__global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
+  __shared__ __attribute__((aligned(16))) char kv_s[2][2][BK * 256];
+  __shared__ __attribute__((aligned(16))) float bias_s[2][BK];
+  __shared__ unsigned short blist[REP_MAX_NB], clist[REP_MAX_NB];
+  __shared__ int counts[2];
+
+  const int w = blockIdx.x, xcd = w & 7, sidx = w >> 3;
+  const int bh = sidx / a.per_xcd;
+  const int qb = xcd * a.per_xcd + sidx % a.per_xcd;
+  if (bh >= a.BH || qb >= a.NB) return;
+  const int tid = threadIdx.x, l = tid & 63, hi = l >> 5, lq = l & 31;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rg = wv & 1, kh = wv >> 1;
+  const int qrow = 32 * rg + lq;
+  const int qcnt = sload(a.blk_cnt + qb);
+  const bool qvalid = qrow < qcnt;
+  const size_t head = (size_t)bh * a.L;
+  const size_t tok = head + (size_t)qb * BK + qrow;
+  const size_t brow = (size_t)bh * a.NB + qb;
+
+  if (wv == 0) build_lists(a, brow, blist, clist, counts);
+  Stream st;
+  st.beg = sload(a.row_ptr + (size_t)bh * (a.NB + 1) + qb);
+  st.nA = (a.phases & PH_A) ? sload(a.row_ptr + (size_t)bh * (a.NB + 1) + qb + 1) - st.beg : 0;
+  st.beg = __builtin_amdgcn_readfirstlane(st.beg);
+  st.nA = __builtin_amdgcn_readfirstlane(st.nA);
+  __syncthreads();
+  st.nBrows = __builtin_amdgcn_readfirstlane(counts[0] * a.RM);
+  st.nC = __builtin_amdgcn_readfirstlane(counts[1]);
+  st.cA = st.nA;
+  st.cB = (st.nBrows + BK - 1) / BK;
+  st.cC = (st.nC + BK - 1) / BK;
+  const int nc = st.cA + st.cB + st.cC;
+
+  const unsigned head_bytes = (unsigned)((size_t)a.L * HD * 2);
+  const rsrc_t rk = make_rsrc(a.k + head * HD, head_bytes);
+  const rsrc_t rv = make_rsrc(a.v + head * HD, head_bytes);
+  const rsrc_t rkm = make_rsrc(a.k_mid + (size_t)bh * a.mid_rows * HD, (unsigned)((size_t)a.mid_rows * HD * 2));
+  const rsrc_t rvm = make_rsrc(a.v_mid + (size_t)bh * a.mid_rows * HD, (unsigned)((size_t)a.mid_rows * HD * 2));
+  const rsrc_t rkt = make_rsrc(a.k_tail + (size_t)bh * a.tail_rows * HD, (unsigned)((size_t)a.tail_rows * HD * 2));
+  const rsrc_t rvt = make_rsrc(a.v_tail + (size_t)bh * a.tail_rows * HD, (unsigned)((size_t)a.tail_rows * HD * 2));
+  unsigned chb[4];
+  int lrow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int P = (wv * 4 + i) * 64 + l, R = P >> 4;
+    lrow[i] = R;
+    chb[i] = (unsigned)(((P & 15) ^ swz(R)) * 16);
+  }
+  // stage chunk cj into buffer sb; returns (wave 0) the bias of chunk column l
+  auto issue = [&](int cj, int sb) -> float {
+    char* kd = kv_s[sb][0] + wv * 4096;
+    char* vd = kv_s[sb][1] + wv * 4096;
+    if (cj < st.cA) {
+      const int b = __builtin_amdgcn_readfirstlane(a.col_idx[st.beg + cj]);
+      const unsigned soff = (unsigned)b * (BK * 256);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        buf2lds16(rk, kd + i * 1024, (unsigned)lrow[i] * 256 + chb[i], soff);
+        buf2lds16(rv, vd + i * 1024, (unsigned)lrow[i] * 256 + chb[i], soff);
+      }
+      return l < sload(a.blk_cnt + b) ? 0.0f : -INFINITY;
+    }
+    const bool tb = cj < st.cA + st.cB;
+    const int p0 = (cj - (tb ? st.cA : st.cA + st.cB)) * BK;
+    const int n = tb ? st.nBrows : st.nC;
+    auto table_row = [&](int p) -> int {
+      if (p >= n) return -1;
+      return tb ? (int)blist[p / a.RM] * a.RM + p % a.RM : (int)clist[p];
+    };
+    const rsrc_t r1 = tb ? rkm : rkt, r2 = tb ? rvm : rvt;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = table_row(p0 + lrow[i]);
+      const unsigned off = row < 0 ? 0x80000000u : (unsigned)row * 256 + chb[i];
+      buf2lds16(r1, kd + i * 1024, off, 0);
+      buf2lds16(r2, vd + i * 1024, off, 0);
+    }
+    const int row = table_row(p0 + l);
+    return row < 0 ? -INFINITY : (tb ? a.lc_mid[row] : a.lc_tail[row]);
+  };
+
+  bf16x8 qreg[8], dreg[8];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    qreg[ks] = *reinterpret_cast<const bf16x8*>(a.q + tok * HD + 16 * ks + 8 * hi);
+    if (BWD) dreg[ks] = *reinterpret_cast<const bf16x8*>(a.dout + tok * HD + 16 * ks + 8 * hi);
+  }
+  float ls = 0.0f, dl = 0.0f;
+  if (BWD) {
+    const float lv = a.lse[tok];
+    ls = (qvalid && lv != -INFINITY) ? lv * LOG2E : INFINITY;
+    dl = a.delta[tok];
+  }
+  int koff[8];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) koff[ks] = kh * 8192 + tile_off(lq, 2 * ks + hi);
+  int toff[2][4];
+  {
+    const int g1 = (l >> 4) & 1, sub = (l & 1) * 8, rowA = 4 * hi + ((l & 15) >> 2);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      toff[0][db] = kh * 8192 + tile_off(rowA, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
+      toff[1][db] = kh * 8192 + tile_off(rowA + 8, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
+    }
+  }
+  f32x16 acc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
+  float lsum = 0.0f, mref = -INFINITY;
+
+  if (nc > 0) {
+    const float b0 = issue(0, 0);
+    if (wv == 0) bias_s[0][l] = b0;
+  }
+  wait_vmem();
+  __syncthreads();
+  for (int j = 0; j < nc; ++j) {
+    const int sb = j & 1;
+    float bn = 0.0f;
+    if (j + 1 < nc) bn = issue(j + 1, sb ^ 1);
+    const char* kt = kv_s[sb][0];
+    const char* vt = kv_s[sb][1];
+    f32x16 s = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) s = mfma32(lds_read16(kt, koff[ks]), qreg[ks], s);
+    float x[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bias_s[sb][32 * kh + 8 * g + 4 * hi]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[4 * g + e] = fmaf(s[4 * g + e], a.scale_log2, b4[e]);
+    }
+    if (!BWD) {
+      float mx = x[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, x[r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      if (__builtin_amdgcn_ballot_w64(mx > mref + SLACK) != 0) {
+        const float mnew = fmaxf(mref, mx);
+        const float alpha = mref == -INFINITY ? 0.0f : exp2f_fast(mref - mnew);
+        lsum *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+        mref = mnew;
+      }
+      const float msub = mref == -INFINITY ? 0.0f : mref;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] = exp2f_fast(x[r] - msub);
+      const bf16x8 pa = pack8(&x[0]), pb = pack8(&x[8]);
+      lsum += sum8_bf16(pb, sum8_bf16(pa, 0.0f));
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        acc[db] = mfma32(cat_tr(lds_read_tr(vt, toff[0][db]), lds_read_tr(vt, toff[1][db])), pa, acc[db]);
+        acc[db] = mfma32(cat_tr(lds_read_tr(vt + 4096, toff[0][db]), lds_read_tr(vt + 4096, toff[1][db])), pb, acc[db]);
+      }
+    } else {
+      f32x16 dp = {};
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) dp = mfma32(lds_read16(vt, koff[ks]), dreg[ks], dp);
+      float ds[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ds[r] = exp2f_fast(x[r] - ls) * (dp[r] - dl) * a.scale;
+      const bf16x8 sa = pack8(&ds[0]), sb8 = pack8(&ds[8]);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        acc[db] = mfma32(cat_tr(lds_read_tr(kt, toff[0][db]), lds_read_tr(kt, toff[1][db])), sa, acc[db]);
+        acc[db] = mfma32(cat_tr(lds_read_tr(kt + 4096, toff[0][db]), lds_read_tr(kt + 4096, toff[1][db])), sb8,
+                         acc[db]);
+      }
+    }
+    if (j + 1 < nc && wv == 0) bias_s[sb ^ 1][l] = bn;
+    wait_vmem();
+    __syncthreads();
+  }
+
+  // combine the two key halves of each row group through LDS
+  float* xo = reinterpret_cast<float*>(&kv_s[0][0][0]) + rg * (64 * 64);
+  float* xm = reinterpret_cast<float*>(&kv_s[1][0][0]) + rg * 128;
+  const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+  if (kh == 1) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xo[(db * 16 + r) * 64 + l] = acc[db][r];
+    xm[l] = mref;
+    xm[64 + l] = ltot;
+  }
+  __syncthreads();
+  if (kh == 1) return;
+  float a0 = 1.0f, a1 = 1.0f, inv = 1.0f, lse2 = 0.0f;
+  bool live = qvalid;
+  if (!BWD) {
+    const float m1 = xm[l], l1 = xm[64 + l];
+    const float M = fmaxf(mref, m1);
+    a0 = mref == -INFINITY ? 0.0f : exp2f_fast(mref - M);
+    a1 = m1 == -INFINITY ? 0.0f : exp2f_fast(m1 - M);
+    const float lt = a0 * ltot + a1 * l1;
+    live = qvalid && lt > 0.0f;
+    inv = live ? 1.0f / lt : 0.0f;
+    lse2 = live ? M + log2f(lt) : -INFINITY;
+  } else {
+    inv = qvalid ? 1.0f : 0.0f;
+  }
+  const float inv_cnt = qvalid ? 1.0f / (float)qcnt : 0.0f;
+  const float* adq = a.add_dq ? a.add_dq + ((size_t)bh * a.add_nb + qb) * HD : nullptr;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = 32 * db + 8 * i + 4 * hi;
+      f32x4 x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = (a0 * acc[db][4 * i + e] + a1 * xo[(db * 16 + 4 * i + e) * 64 + l]) * inv;
+      if (BWD && a.dq_acc != nullptr) {
+        if (qvalid) x += *reinterpret_cast<const f32x4*>(a.dq_acc + tok * HD + c);
+      }
+      if (BWD && adq != nullptr) x += *reinterpret_cast<const f32x4*>(adq + c) * inv_cnt;
+      ushort4 u;
+      u.x = f2bf(x[0]); u.y = f2bf(x[1]); u.z = f2bf(x[2]); u.w = f2bf(x[3]);
+      *reinterpret_cast<ushort4*>(a.out + tok * HD + c) = u;
+    }
+  if (!BWD && hi == 0) a.lse_out[tok] = live ? lse2 * LN2_F : -INFINITY;
+}
+
+// ------------------------------------------------------------------------------------------------ table dK / dV
+struct TabArgs {
+  const bf16_t *q, *dout;
+  const bf16_t *k_tab, *v_tab;  // [BH, rows_pad, D]
+  const float* lc;              // [rows]
+  const float *lse, *delta;
+  const unsigned *bits_a, *bits_ab;
+  float *dk_tab, *dv_tab;       // [BH, rows_pad, D] fp32, accumulated
+  int L, NB, RM, W, rows, rows_pad, tier;  // tier: PH_B or PH_C
+  float scale_log2, scale;
+};
+
+// 64-bit mask of the tier blocks of query-block row i among the workgroup's blocks fb .. fb + nblk - 1
+__device__ __forceinline__ unsigned long long tier_mask(const TabArgs& a, size_t row, int fb, int nblk) {
+  const int w0 = fb >> 5;
+  auto word = [&](int w) -> unsigned long long {
+    if (w >= a.W) return 0ull;
+    const unsigned abv = sload(a.bits_ab + row * a.W + w);
+    unsigned m = a.tier == PH_B ? (abv & ~sload(a.bits_a + row * a.W + w)) : ~abv;
+    const int lo = w * 32;
+    if (a.NB - lo < 32) m &= (1u << (a.NB - lo)) - 1u;
+    return m;
+  };
+  unsigned long long m = word(w0) | (nblk > 32 - (fb & 31) ? word(w0 + 1) << 32 : 0ull);
+  m >>= (fb & 31);
+  return nblk >= 64 ? m : (m & ((1ull << nblk) - 1ull));
+}
+
+// grid (rows_pad / 64, BH), 256 threads; the fine KV-owner layout (2 key halves x 2 query halves), V in LDS
+__global__ __launch_bounds__(256, 1) void rep_bwd_tab_kernel(TabArgs a) {
+  __shared__ __attribute__((aligned(16))) char qd_s[2][2][BK * 256];
+  __shared__ __attribute__((aligned(16))) char v_s[BK * 256];
+  __shared__ __attribute__((aligned(16))) float st_s[2][2][BK];
+  const int grp = blockIdx.x, bh = blockIdx.y;
+  const int tid = threadIdx.x, l = tid & 63, hi = l >> 5, lq = l & 31;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kh = wv & 1, qh = wv >> 1;
+  const int key = 32 * kh + lq;
+  const int trow = grp * BK + key;  // table row of this lane's key
+  const int per_blk = a.tier == PH_B ? a.RM : 1;
+  const int fb = grp * BK / per_blk, nblk = BK / per_blk;
+  const int lblk = key / per_blk;   // block of this key within the workgroup's blocks
+  const float kbias = trow < a.rows ? a.lc[trow] : -INFINITY;
+  const size_t head = (size_t)bh * a.L;
+
+  const unsigned head_bytes = (unsigned)((size_t)a.L * HD * 2);
+  const rsrc_t rq = make_rsrc(a.q + head * HD, head_bytes);
+  const rsrc_t rd = make_rsrc(a.dout + head * HD, head_bytes);
+  unsigned ld_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int P = (wv * 4 + i) * 64 + l, R = P >> 4;
+    ld_off[i] = (unsigned)R * 256 + (unsigned)(((P & 15) ^ swz(R)) * 16);
+  }
+  {
+    const rsrc_t rv = make_rsrc(a.v_tab + (size_t)bh * a.rows_pad * HD, (unsigned)((size_t)a.rows_pad * HD * 2));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) buf2lds16(rv, v_s + wv * 4096 + i * 1024, ld_off[i], (unsigned)grp * (BK * 256));
+  }
+  bf16x8 kreg[8];
+  {
+    const bf16_t* kp = a.k_tab + ((size_t)bh * a.rows_pad + trow) * HD + 8 * hi;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) kreg[ks] = *reinterpret_cast<const bf16x8*>(kp + 16 * ks);
+  }
+  auto issue = [&](int i, int sb, float& ls, float& dl) {
+    const unsigned soff = (unsigned)i * (BK * 256);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      buf2lds16(rq, qd_s[sb][0] + wv * 4096 + r * 1024, ld_off[r], soff);
+      buf2lds16(rd, qd_s[sb][1] + wv * 4096 + r * 1024, ld_off[r], soff);
+    }
+    if (wv == 0) {
+      const size_t t = head + (size_t)i * BK + l;
+      const float lv = a.lse[t];
+      ls = lv == -INFINITY ? INFINITY : lv * LOG2E;
+      dl = a.delta[t];
+    }
+  };
+  // the next query block at or after i with at least one tier pair among this workgroup's blocks
+  auto next_active = [&](int i, unsigned long long& m) -> int {
+    for (; i < a.NB; ++i) {
+      m = tier_mask(a, (size_t)bh * a.NB + i, fb, nblk);
+      if (m != 0ull) return i;
+    }
+    return a.NB;
+  };
+  int aoff[8], boff[8];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    aoff[ks] = qh * 8192 + tile_off(lq, 2 * ks + hi);
+    boff[ks] = kh * 8192 + tile_off(lq, 2 * ks + hi);
+  }
+  int toff[2][4];
+  {
+    const int g1 = (l >> 4) & 1, sub = (l & 1) * 8, rowA = 4 * hi + ((l & 15) >> 2);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      toff[0][db] = qh * 8192 + tile_off(rowA, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
+      toff[1][db] = qh * 8192 + tile_off(rowA + 8, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
+    }
+  }
+  f32x16 dk[4], dv[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) dk[db] = dv[db] = f32x16{};
+
+  float ls = 0.0f, dl = 0.0f;
+  unsigned long long mcur = 0, mnext = 0;
+  int icur = next_active(0, mcur);
+  int inext = icur < a.NB ? next_active(icur + 1, mnext) : a.NB;
+  if (icur < a.NB) {
+    issue(icur, 0, ls, dl);
+    wait_vmem();
+    if (wv == 0) {
+      st_s[0][0][l] = ls;
+      st_s[0][1][l] = dl;
+    }
+  }
+  wait_vmem();
+  __syncthreads();
+  for (int j = 0; icur < a.NB; ++j) {
+    const int sb = j & 1;
+    unsigned long long mnn = 0;
+    int inn = a.NB;
+    if (inext < a.NB) {
+      issue(inext, sb ^ 1, ls, dl);
+      inn = next_active(inext + 1, mnn);
+    }
+    // this lane's key: bias log2(c) when its block's pair with query block icur is in the tier, else -inf
+    const float kb = ((mcur >> lblk) & 1ull) ? kbias : -INFINITY;
+    const char* qt = qd_s[sb][0];
+    const char* dt = qd_s[sb][1];
+    f32x16 s = {}, dp = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) s = mfma32(lds_read16(qt, aoff[ks]), kreg[ks], s);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) dp = mfma32(lds_read16(dt, aoff[ks]), lds_read16(v_s, boff[ks]), dp);
+    float p[16], ds[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 l4 = *reinterpret_cast<const f32x4*>(&st_s[sb][0][32 * qh + 8 * g + 4 * hi]);
+      const f32x4 d4 = *reinterpret_cast<const f32x4*>(&st_s[sb][1][32 * qh + 8 * g + 4 * hi]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * g + e;
+        p[r] = exp2f_fast(fmaf(s[r], a.scale_log2, kb) - l4[e]);
+        ds[r] = p[r] * (dp[r] - d4[e]) * a.scale;
+      }
+    }
+    const bf16x8 pa = pack8(&p[0]), pb = pack8(&p[8]);
+    const bf16x8 sa = pack8(&ds[0]), sb8 = pack8(&ds[8]);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      dv[db] = mfma32(cat_tr(lds_read_tr(dt, toff[0][db]), lds_read_tr(dt, toff[1][db])), pa, dv[db]);
+      dv[db] = mfma32(cat_tr(lds_read_tr(dt + 4096, toff[0][db]), lds_read_tr(dt + 4096, toff[1][db])), pb, dv[db]);
+      dk[db] = mfma32(cat_tr(lds_read_tr(qt, toff[0][db]), lds_read_tr(qt, toff[1][db])), sa, dk[db]);
+      dk[db] = mfma32(cat_tr(lds_read_tr(qt + 4096, toff[0][db]), lds_read_tr(qt + 4096, toff[1][db])), sb8, dk[db]);
+    }
+    wait_vmem();
+    if (inext < a.NB && wv == 0) {
+      st_s[sb ^ 1][0][l] = ls;
+      st_s[sb ^ 1][1][l] = dl;
+    }
+    __syncthreads();
+    icur = inext;
+    mcur = mnext;
+    inext = inn;
+    mnext = mnn;
+  }
+
+  float* xk = reinterpret_cast<float*>(&qd_s[0][0][0]) + kh * (2 * 64 * 64);
+  float* xv = xk + 64 * 64;
+  if (qh == 1) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        xk[(db * 16 + r) * 64 + l] = dk[db][r];
+        xv[(db * 16 + r) * 64 + l] = dv[db][r];
+      }
+  }
+  __syncthreads();
+  if (qh == 1) return;
+  float* gk = a.dk_tab + ((size_t)bh * a.rows_pad + trow) * HD;
+  float* gv = a.dv_tab + ((size_t)bh * a.rows_pad + trow) * HD;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = 32 * db + 8 * i + 4 * hi;
+      f32x4 xk4, xv4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xk4[e] = dk[db][4 * i + e] + xk[(db * 16 + 4 * i + e) * 64 + l];
+        xv4[e] = dv[db][4 * i + e] + xv[(db * 16 + 4 * i + e) * 64 + l];
+      }
+      *reinterpret_cast<f32x4*>(gk + c) = *reinterpret_cast<const f32x4*>(gk + c) + xk4;
+      *reinterpret_cast<f32x4*>(gv + c) = *reinterpret_cast<const f32x4*>(gv + c) + xv4;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ small passes
+// grid (cdiv(NB, 4), BH), 256 threads: one wave per block, lane -> (row slot, 8 columns)
+__global__ __launch_bounds__(256) void rep_unpool_kernel(const float* __restrict__ acc_k, const float* __restrict__ acc_v,
+                                                         const float* __restrict__ dk_mid, const float* __restrict__ dv_mid,
+                                                         const float* __restrict__ dk_tail,
+                                                         const float* __restrict__ dv_tail, bf16_t* __restrict__ dk,
+                                                         bf16_t* __restrict__ dv, const int* __restrict__ blk_cnt,
+                                                         int L, int NB, int RM, int mid_rows, int tail_rows) {
+  const int blk = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (blk >= NB) return;
+  const int l = threadIdx.x & 63, s = l >> 4, c8 = (l & 15) * 8;
+  const size_t bh = blockIdx.y;
+  const int cnt = blk_cnt[blk], gs = BK / RM;
+  const float invc = 1.0f / (float)cnt;
+  const size_t tail = (bh * tail_rows + blk) * HD + c8;
+  for (int r = s; r < BK; r += 4) {
+    const size_t tok = (bh * L + (size_t)blk * BK + r) * HD + c8;
+    const int g = r / gs;
+    const int n = min(max(cnt - g * gs, 0), gs);
+    const size_t mid = (bh * mid_rows + (size_t)blk * RM + g) * HD + c8;
+    float xk[8], xv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      xk[e] = 0.0f;
+      xv[e] = 0.0f;
+    }
+    if (r < cnt) {
+      const float invg = 1.0f / (float)n;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xk[e] = (acc_k ? acc_k[tok + e] : 0.0f) + dk_mid[mid + e] * invg + dk_tail[tail + e] * invc;
+        xv[e] = (acc_v ? acc_v[tok + e] : 0.0f) + dv_mid[mid + e] * invg + dv_tail[tail + e] * invc;
+      }
+    }
+    uint4 uk, uv;
+    uk.x = (unsigned)f2bf(xk[0]) | ((unsigned)f2bf(xk[1]) << 16);
+    uk.y = (unsigned)f2bf(xk[2]) | ((unsigned)f2bf(xk[3]) << 16);
+    uk.z = (unsigned)f2bf(xk[4]) | ((unsigned)f2bf(xk[5]) << 16);
+    uk.w = (unsigned)f2bf(xk[6]) | ((unsigned)f2bf(xk[7]) << 16);
+    uv.x = (unsigned)f2bf(xv[0]) | ((unsigned)f2bf(xv[1]) << 16);
+    uv.y = (unsigned)f2bf(xv[2]) | ((unsigned)f2bf(xv[3]) << 16);
+    uv.z = (unsigned)f2bf(xv[4]) | ((unsigned)f2bf(xv[5]) << 16);
+    uv.w = (unsigned)f2bf(xv[6]) | ((unsigned)f2bf(xv[7]) << 16);
+    *reinterpret_cast<uint4*>(dk + tok) = uk;
+    *reinterpret_cast<uint4*>(dv + tok) = uv;
+  }
+}
+
+// delta[row] = <dO, O> on valid rows, 0 on padding; one wave per block, 16 lanes per token row
+__global__ __launch_bounds__(256) void row_dot_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ y,
+                                                      float* __restrict__ out, const int* __restrict__ blk_cnt, int L,
+                                                      int NB) {
+  const int blk = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (blk >= NB) return;
+  const int l = threadIdx.x & 63, s = l >> 4, c8 = (l & 15) * 8;
+  const size_t bh = blockIdx.y;
+  const int cnt = blk_cnt[blk];
+  for (int r = s; r < BK; r += 4) {
+    const size_t t = bh * L + (size_t)blk * BK + r;
+    float acc = 0.0f;
+    if (r < cnt) {
+      const uint4 ux = *reinterpret_cast<const uint4*>(x + t * HD + c8);
+      const uint4 uy = *reinterpret_cast<const uint4*>(y + t * HD + c8);
+      const unsigned wx[4] = {ux.x, ux.y, ux.z, ux.w}, wy[4] = {uy.x, uy.y, uy.z, uy.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        acc += __uint_as_float(wx[i] << 16) * __uint_as_float(wy[i] << 16) +
+               __uint_as_float(wx[i] & 0xffff0000u) * __uint_as_float(wy[i] & 0xffff0000u);
+    }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) acc += __shfl_xor(acc, m, 16);
+    if ((l & 15) == 0) out[t] = acc;
+  }
+}
+
+// tier-B lists: row i of the A|B lists without its tier-A columns (one wave per row); ptr_B = ptr_AB - ptr_A
+__global__ __launch_bounds__(256) void tier_b_lists_kernel(const int* __restrict__ ab_ptr, const int* __restrict__ ab_idx,
+                                                           const int* __restrict__ a_ptr,
+                                                           const unsigned* __restrict__ bits_a, int* __restrict__ b_ptr,
+                                                           int* __restrict__ b_idx, int NB, int W) {
+  const int bh = blockIdx.y, row = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+  if (row >= NB) return;
+  const size_t r = (size_t)bh * (NB + 1) + row;
+  const int s0 = ab_ptr[r], s1 = ab_ptr[r + 1];
+  const int o0 = s0 - a_ptr[r];
+  if (l == 0) {
+    b_ptr[r] = o0;
+    if (row == NB - 1) b_ptr[r + 1] = s1 - a_ptr[r + 1];
+  }
+  const unsigned* bits = bits_a + ((size_t)bh * NB + row) * W;
+  int out = o0;
+  for (int e0 = s0; e0 < s1; e0 += 64) {
+    const int e = e0 + l;
+    int col = 0;
+    bool keep = false;
+    if (e < s1) {
+      col = ab_idx[e];
+      keep = ((bits[col >> 5] >> (col & 31)) & 1u) == 0u;
+    }
+    const unsigned long long m = __builtin_amdgcn_ballot_w64(keep);
+    if (keep) b_idx[out + __popcll(m & ((1ull << l) - 1ull))] = col;
+    out += __popcll(m);
+  }
+}
+
+}  // namespace
+
+}  // namespace es
+
+using namespace es;
+
+static int rep_check(int BH, int L, int D, int RM) {
+  ES_REQUIRE(BH > 0 && BH <= 65535 && L > 0 && L % BK == 0, ES_ERR_INVALID, "VSA2-rep: tokens must be [BH, L = NB * 64, D]");
+  ES_REQUIRE(D == HD, ES_ERR_UNSUPPORTED, "VSA2-rep: head dim must be 128");
+  ES_REQUIRE(L / BK <= REP_MAX_NB, ES_ERR_UNSUPPORTED, "VSA2-rep: NB <= 2048 blocks");
+  ES_REQUIRE(RM == 1 || RM == 2 || RM == 4 || RM == 8 || RM == 16, ES_ERR_INVALID,
+             "RepTiers.mid_reps must be one of (1, 2, 4, 8, 16)");
+  ES_REQUIRE((size_t)L * HD * 2 < (1ull << 31), ES_ERR_UNSUPPORTED, "VSA2-rep: one head's tokens exceed 2 GiB");
+  return ES_OK;
+}
+
+static RepArgs rep_args(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
+                        const float* lc_mid, const void* k_tail, const void* v_tail, const float* lc_tail,
+                        const int* q2k_ptr, const int* q2k_idx, const unsigned* bits_a, const unsigned* bits_ab,
+                        const int* blk_cnt, int BH, int L, int RM, int phases) {
+  RepArgs a = {};
+  a.q = (const bf16_t*)q;
+  a.k = (const bf16_t*)k;
+  a.v = (const bf16_t*)v;
+  a.k_mid = (const bf16_t*)k_mid;
+  a.v_mid = (const bf16_t*)v_mid;
+  a.lc_mid = lc_mid;
+  a.k_tail = (const bf16_t*)k_tail;
+  a.v_tail = (const bf16_t*)v_tail;
+  a.lc_tail = lc_tail;
+  a.row_ptr = q2k_ptr;
+  a.col_idx = q2k_idx;
+  a.bits_a = bits_a;
+  a.bits_ab = bits_ab;
+  a.blk_cnt = blk_cnt;
+  a.L = L;
+  a.NB = L / BK;
+  a.RM = RM;
+  a.W = (a.NB + 31) / 32;
+  a.BH = BH;
+  a.per_xcd = (a.NB + 7) / 8;
+  a.phases = phases;
+  a.mid_rows = (a.NB * RM + 63) / 64 * 64;
+  a.tail_rows = (a.NB + 63) / 64 * 64;
+  a.scale_log2 = LOG2E / sqrtf((float)HD);
+  a.scale = 1.0f / sqrtf((float)HD);
+  return a;
+}
+
+extern "C" int vsa_rep_attn_fwd(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
+                                const float* lc_mid, const void* k_tail, const void* v_tail, const float* lc_tail,
+                                const int* q2k_ptr, const int* q2k_idx, const unsigned* bits_a,
+                                const unsigned* bits_ab, const int* blk_cnt, void* out, float* lse, int BH, int L,
+                                int D, int RM, int phases, hipStream_t stream) {
+  if (int st = rep_check(BH, L, D, RM)) return st;
+  ES_REQUIRE(q && k && v && k_mid && v_mid && lc_mid && k_tail && v_tail && lc_tail && q2k_ptr && bits_a && bits_ab &&
+                 blk_cnt && out && lse,
+             ES_ERR_INVALID, "VSA2-rep: null tensor pointer");
+  ES_REQUIRE(phases >= 0 && phases <= 7, ES_ERR_INVALID, "VSA2-rep: phases must be a mask of 1 | 2 | 4");
+  RepArgs a = rep_args(q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, q2k_ptr, q2k_idx, bits_a, bits_ab,
+                       blk_cnt, BH, L, RM, phases);
+  a.out = (bf16_t*)out;
+  a.lse_out = lse;
+  hipLaunchKernelGGL(rep_q_kernel<false>, dim3(8 * BH * a.per_xcd), dim3(256), 0, stream, a);
+  return check_launch("vsa_rep_attn_fwd");
+}
+
+extern "C" int vsa_rep_attn_bwd_q(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
+                                  const float* lc_mid, const void* k_tail, const void* v_tail, const float* lc_tail,
+                                  const void* dout, const float* lse, const float* delta, const int* q2k_ptr,
+                                  const int* q2k_idx, const unsigned* bits_a, const unsigned* bits_ab,
+                                  const int* blk_cnt, const float* add_dq, int add_nb, const float* dq_acc, void* dq,
+                                  int BH, int L, int D, int RM, int phases, hipStream_t stream) {
+  if (int st = rep_check(BH, L, D, RM)) return st;
+  ES_REQUIRE(q && k && v && k_mid && v_mid && lc_mid && k_tail && v_tail && lc_tail && dout && lse && delta &&
+                 q2k_ptr && bits_a && bits_ab && blk_cnt && dq,
+             ES_ERR_INVALID, "VSA2-rep: null tensor pointer");
+  ES_REQUIRE(add_dq == nullptr || add_nb >= L / BK, ES_ERR_INVALID, "VSA2-rep: add_dq has fewer rows than blocks");
+  RepArgs a = rep_args(q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, q2k_ptr, q2k_idx, bits_a, bits_ab,
+                       blk_cnt, BH, L, RM, phases);
+  a.dout = (const bf16_t*)dout;
+  a.lse = lse;
+  a.delta = delta;
+  a.add_dq = add_dq;
+  a.add_nb = add_nb;
+  a.dq_acc = (float*)dq_acc;
+  a.out = (bf16_t*)dq;
+  hipLaunchKernelGGL(rep_q_kernel<true>, dim3(8 * BH * a.per_xcd), dim3(256), 0, stream, a);
+  return check_launch("vsa_rep_attn_bwd_q");
+}
+
+extern "C" int vsa_rep_bwd_tables(const void* q, const void* dout, const void* k_tab, const void* v_tab,
+                                  const float* lc, const float* lse, const float* delta, const unsigned* bits_a,
+                                  const unsigned* bits_ab, float* dk_tab, float* dv_tab, int BH, int L, int D, int RM,
+                                  int tier, hipStream_t stream) {
+  if (int st = rep_check(BH, L, D, RM)) return st;
+  ES_REQUIRE(q && dout && k_tab && v_tab && lc && lse && delta && bits_a && bits_ab && dk_tab && dv_tab,
+             ES_ERR_INVALID, "VSA2-rep: null tensor pointer");
+  ES_REQUIRE(tier == 2 || tier == 4, ES_ERR_INVALID, "VSA2-rep: tier must be 2 (B, mid table) or 4 (C, tail table)");
+  TabArgs a = {};
+  a.q = (const bf16_t*)q;
+  a.dout = (const bf16_t*)dout;
+  a.k_tab = (const bf16_t*)k_tab;
+  a.v_tab = (const bf16_t*)v_tab;
+  a.lc = lc;
+  a.lse = lse;
+  a.delta = delta;
+  a.bits_a = bits_a;
+  a.bits_ab = bits_ab;
+  a.dk_tab = dk_tab;
+  a.dv_tab = dv_tab;
+  a.L = L;
+  a.NB = L / BK;
+  a.RM = RM;
+  a.W = (a.NB + 31) / 32;
+  a.tier = tier;
+  a.rows = tier == 2 ? a.NB * RM : a.NB;
+  a.rows_pad = (a.rows + 63) / 64 * 64;
+  a.scale_log2 = LOG2E / sqrtf((float)HD);
+  a.scale = 1.0f / sqrtf((float)HD);
+  hipLaunchKernelGGL(rep_bwd_tab_kernel, dim3(a.rows_pad / 64, BH), dim3(256), 0, stream, a);
+  return check_launch("vsa_rep_bwd_tables");
+}
+
+extern "C" int vsa_rep_unpool(const float* acc_k, const float* acc_v, const float* dk_mid, const float* dv_mid,
+                              const float* dk_tail, const float* dv_tail, const int* blk_cnt, void* dk, void* dv,
+                              int BH, int L, int D, int RM, hipStream_t stream) {
+  if (int st = rep_check(BH, L, D, RM)) return st;
+  ES_REQUIRE(dk_mid && dv_mid && dk_tail && dv_tail && blk_cnt && dk && dv, ES_ERR_INVALID,
+             "VSA2-rep: null tensor pointer");
+  const int NB = L / BK;
+  hipLaunchKernelGGL(rep_unpool_kernel, dim3((NB + 3) / 4, BH), dim3(256), 0, stream, acc_k, acc_v, dk_mid, dv_mid,
+                     dk_tail, dv_tail, (bf16_t*)dk, (bf16_t*)dv, blk_cnt, L, NB, RM, (NB * RM + 63) / 64 * 64,
+                     (NB + 63) / 64 * 64);
+  return check_launch("vsa_rep_unpool");
+}
+
+extern "C" int vsa_row_dot(const void* x, const void* y, const int* blk_cnt, float* out, int BH, int L, int D,
+                           hipStream_t stream) {
+  ES_REQUIRE(x && y && blk_cnt && out, ES_ERR_INVALID, "VSA: null tensor pointer");
+  ES_REQUIRE(BH > 0 && BH <= 65535 && L > 0 && L % BK == 0, ES_ERR_INVALID, "VSA: tokens must be [BH, L = NB * 64, D]");
+  ES_REQUIRE(D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 128");
+  const int NB = L / BK;
+  hipLaunchKernelGGL(row_dot_kernel, dim3((NB + 3) / 4, BH), dim3(256), 0, stream, (const bf16_t*)x, (const bf16_t*)y,
+                     out, blk_cnt, L, NB);
+  return check_launch("vsa_row_dot");
+}
+
+extern "C" int vsa_tier_b_lists(const int* ab_ptr, const int* ab_idx, const int* a_ptr, const unsigned* bits_a,
+                                int* b_ptr, int* b_idx, int BH, int NB, hipStream_t stream) {
+  ES_REQUIRE(ab_ptr && a_ptr && bits_a && b_ptr, ES_ERR_INVALID, "VSA2-rep: null tensor pointer");
+  ES_REQUIRE(BH > 0 && BH <= 65535 && NB > 0, ES_ERR_INVALID, "VSA2-rep: bad shape");
+  hipLaunchKernelGGL(tier_b_lists_kernel, dim3((NB + 3) / 4, BH), dim3(256), 0, stream, ab_ptr, ab_idx, a_ptr, bits_a,
+                     b_ptr, b_idx, NB, (NB + 31) / 32);
+  return check_launch("vsa_tier_b_lists");
+}

@@ -427,6 +427,16 @@ __global__ void fill_base_kernel(long long* base, const TopkState* st, long long
   else base[i] = (long long)(bh0 + i) * (st ? st[i].keff : keff);
 }
 
+// the selection bitmap rows of (b, h) bh0 + b into bits_out [BH, NB, W] (the workspace pads rows to ceil32(NB))
+__global__ void export_bits_kernel(const unsigned* __restrict__ selbits, unsigned* __restrict__ bits_out, int NB, int W,
+                                   int bh0, int bh_count) {
+  const long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (long long)bh_count * NB * W) return;
+  const int bhl = (int)(e / ((long long)NB * W));
+  const long long rem = e - (long long)bhl * NB * W;
+  bits_out[(size_t)(bh0 + bhl) * NB * W + rem] = selbits[((size_t)bhl * ((NB + 31) & ~31)) * W + rem];
+}
+
 // selection bits of given CSR rows (one wave per row): bit j of row i set for every listed j
 __global__ __launch_bounds__(256) void csr_bits_kernel(const int* __restrict__ ptr, const int* __restrict__ idx,
                                                        unsigned* __restrict__ selbits, int NB, int W, int bh0) {
@@ -722,8 +732,8 @@ extern "C" int vsa_row_topk(const void* scores, int NB, int bh0, int bh_count, i
 }
 
 extern "C" int vsa_global_topk(const float* scores, int NB, int bh0, int bh_count, long long budget, int* q2k_ptr,
-                               int* q2k_idx, int* k2q_ptr, int* k2q_idx, void* workspace, size_t workspace_bytes,
-                               hipStream_t stream) {
+                               int* q2k_idx, int* k2q_ptr, int* k2q_idx, unsigned* bits_out, void* workspace,
+                               size_t workspace_bytes, hipStream_t stream) {
   ES_REQUIRE(scores && q2k_ptr && k2q_ptr && workspace, ES_ERR_INVALID, "VSA: null tensor pointer");
   ES_REQUIRE(NB >= 1 && NB <= 46340 && bh0 >= 0 && bh_count >= 1 && bh_count <= 65535, ES_ERR_INVALID,
              "VSA: bad top-k shape");
@@ -755,6 +765,9 @@ extern "C" int vsa_global_topk(const float* scores, int NB, int bh0, int bh_coun
   hipLaunchKernelGGL(fill_base_kernel, dim3((bh_count + 255) / 256), dim3(256), 0, stream, c.base, c.st, 0LL,
                      (const int*)nullptr, NB, bh0, bh_count);
   invert(c, k2q_ptr, k2q_idx, NB, bh0, bh_count, stream);
+  if (bits_out != nullptr)
+    hipLaunchKernelGGL(export_bits_kernel, dim3((bh_count * NB * W + 255) / 256), dim3(256), 0, stream, c.selbits,
+                       bits_out, NB, W, bh0, bh_count);
   return check_launch("vsa_global_topk");
 }
 

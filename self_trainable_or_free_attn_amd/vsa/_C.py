@@ -214,7 +214,7 @@ def global_topk_into(scores, budget, bh0, q2k_ptr, q2k_idx, k2q_ptr, k2q_idx):
     _check(bhc <= 65535, "too many (b,h) per top-k chunk")
     ws = _workspace(bhc, NB, scores.device)
     _lib.call("vsa_global_topk", scores.contiguous(), NB, int(bh0), bhc, int(budget), q2k_ptr, q2k_idx, k2q_ptr,
-              k2q_idx, ws, ws.numel())
+              k2q_idx, None, ws, ws.numel())
 
 
 def route(qr, kr, blk_cnt, R, budget, row_norm, max_score_bytes=2 << 30):
@@ -235,7 +235,7 @@ def route(qr, kr, blk_cnt, R, budget, row_norm, max_score_bytes=2 << 30):
         cnt = min(chunk, BH - bh0)
         s = scores[:cnt]
         _lib.call("vsa_router_scores", qr, kr, lse2, blk_cnt, s, NB, int(R), int(row_norm), bh0, cnt, qr.shape[3])
-        _lib.call("vsa_global_topk", s, NB, bh0, cnt, int(budget), *out, ws, ws.numel())
+        _lib.call("vsa_global_topk", s, NB, bh0, cnt, int(budget), *out, None, ws, ws.numel())
     return list(out)
 
 
@@ -390,3 +390,118 @@ def attn_bwd_q_acc(q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, dq_acc)
     _lib.call("vsa_attn_bwd_q", q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, None, 0, None, dq_acc, B * H,
               L, D)
     return dq_acc
+
+
+# ------------------------------------------------------------------ VSA2 three-tier representatives
+def rep_build(k, v, blk_cnt, mid_reps):
+    """(k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail): group means of the mid_reps contiguous groups of every block
+    [B, H, ceil64(NB * RM), D], block means [B, H, ceil64(NB), D], log2 counts [NB * RM] / [NB] (reference
+    experiments/vsa2_representative/csrc/rep/rep_api.cpp rep_build)."""
+    _tokens(k, "k")
+    _tokens(v, "v")
+    B, H, L, D = k.shape
+    NB, RM = L // BLOCK, int(mid_reps)
+    k_mid = torch.zeros(B, H, _ceil64(NB * RM), D, device=k.device, dtype=k.dtype)
+    v_mid = torch.zeros_like(k_mid)
+    k_tail = torch.zeros(B, H, _ceil64(NB), D, device=k.device, dtype=k.dtype)
+    v_tail = torch.zeros_like(k_tail)
+    lc_mid = torch.empty(NB * RM, device=k.device, dtype=torch.float32)
+    lc_tail = torch.empty(NB, device=k.device, dtype=torch.float32)
+    _lib.call("vsa_rep_build", k, v, blk_cnt, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, B * H, L, D, RM)
+    return [k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail]
+
+
+def route_tiers(qr, kr, blk_cnt, R, budget_a, budget_ab, row_norm, max_score_bytes=2 << 30):
+    """VSA2's router at two budgets over one score matrix: (q2k_ptr, q2k_idx, k2q_ptr, k2q_idx) of tier A, the
+    bitmaps bits_a / bits_ab [B, H, NB, ceil(NB / 32)] and the tier-B lists (b_ptr, b_idx) (reference rep_api.cpp
+    route_tiers)."""
+    _i32(blk_cnt, "blk_cnt")
+    _check(0 <= budget_a <= budget_ab, "need 0 <= budget_a <= budget_ab")
+    B, H = qr.shape[:2]
+    NB, BH = blk_cnt.numel(), B * H
+    nn = NB * NB
+    ka, kab = max(0, min(int(budget_a), nn)), max(0, min(int(budget_ab), nn))
+    _check(BH * kab < 2 ** 31, "vsa2_rep: selected blocks exceed int32 CSR range")
+    W = (NB + 31) // 32
+    dev = qr.device
+    i32 = dict(device=dev, dtype=torch.int32)
+    a_out = _csr(B, H, NB, max(BH * ka, 1), dev)
+    ab_out = _csr(B, H, NB, max(BH * kab, 1), dev)
+    bits_a = torch.zeros(B, H, NB, W, **i32)
+    bits_ab = torch.zeros(B, H, NB, W, **i32)
+    lse2 = router_lse(qr, kr, blk_cnt, R)
+    chunk = int(max(1, min(BH, int(max_score_bytes) // max(nn * 4, 1), 65535)))
+    ws = _workspace(chunk, NB, dev)
+    scores = torch.empty(chunk, NB, NB, device=dev, dtype=torch.float32)
+    for bh0 in range(0, BH, chunk):
+        cnt = min(chunk, BH - bh0)
+        s = scores[:cnt]
+        _lib.call("vsa_router_scores", qr, kr, lse2, blk_cnt, s, NB, int(R), int(row_norm), bh0, cnt, qr.shape[3])
+        if kab != ka:
+            _lib.call("vsa_global_topk", s, NB, bh0, cnt, kab, *ab_out, bits_ab, ws, ws.numel())
+        _lib.call("vsa_global_topk", s, NB, bh0, cnt, ka, *a_out, bits_a, ws, ws.numel())
+    b_ptr = torch.zeros(B, H, NB + 1, **i32)
+    b_idx = torch.empty(max(1, BH * (kab - ka)), **i32)
+    if kab != ka:
+        _lib.call("vsa_tier_b_lists", ab_out[0], ab_out[1], a_out[0], bits_a, b_ptr, b_idx, BH, NB)
+    else:
+        bits_ab.copy_(bits_a)
+    n = BH * ka
+    return [a_out[0], a_out[1][:max(n, 1)], a_out[2], a_out[3][:max(n, 1)], bits_a, bits_ab, b_ptr, b_idx]
+
+
+def rep_attn_fwd(q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, q2k_ptr, q2k_idx, bits_a, bits_ab, blk_cnt,
+                 mid_reps, phases, diag=0):
+    """(o, lse) of the three-tier attention (reference rep_api.cpp rep_attn_fwd); diag is accepted and ignored."""
+    _attn_args(q, k, v, blk_cnt)
+    B, H, L, D = q.shape
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
+    _lib.call("vsa_rep_attn_fwd", q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, q2k_ptr, q2k_idx, bits_a,
+              bits_ab, blk_cnt, o, lse, B * H, L, D, int(mid_reps), int(phases))
+    return o, lse
+
+
+def rep_attn_bwd_q(q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, dout, lse, delta, q2k_ptr, q2k_idx,
+                   bits_a, bits_ab, blk_cnt, dk_mid, dv_mid, dk_tail, dv_tail, mid_reps, phases, add_dq=None,
+                   dq_acc=None, diag=0):
+    """dQ over the tiers of `phases` (+ dq_acc + add_dq / cnt), and the representative dK / dV of tiers B and C added
+    into dk_mid / dv_mid / dk_tail / dv_tail (reference rep_api.cpp rep_attn_bwd_q). Deterministic: dQ in registers,
+    the tables by a KV-owner pass instead of atomics."""
+    _attn_args(q, k, v, blk_cnt)
+    B, H, L, D = q.shape
+    dq = torch.empty_like(q)
+    _lib.call("vsa_rep_attn_bwd_q", q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, dout, lse, delta, q2k_ptr,
+              q2k_idx, bits_a, bits_ab, blk_cnt, add_dq, add_dq.shape[2] if add_dq is not None else 0, dq_acc, dq,
+              B * H, L, D, int(mid_reps), int(phases))
+    if phases & 2:
+        _lib.call("vsa_rep_bwd_tables", q, dout, k_mid, v_mid, lc_mid, lse, delta, bits_a, bits_ab, dk_mid, dv_mid,
+                  B * H, L, D, int(mid_reps), 2)
+    if phases & 4:
+        _lib.call("vsa_rep_bwd_tables", q, dout, k_tail, v_tail, lc_tail, lse, delta, bits_a, bits_ab, dk_tail,
+                  dv_tail, B * H, L, D, int(mid_reps), 4)
+    return dq
+
+
+def tier_a_bwd_kv(q, k, v, dout, lse, delta, k2q_ptr, k2q_idx, blk_cnt, dq_acc=None):
+    """fp32 (dk, dv) of the tier-A tokens over the tier-A k2q lists (reference rep_api.cpp tier_a_bwd_kv); a given
+    dq_acc receives the tier-A dQ (computed without atomics)."""
+    return attn_bwd(q, k, v, dout, lse, delta, k2q_ptr, k2q_idx, blk_cnt, dq_acc, None, None, True)
+
+
+def rep_unpool(dk_a, dv_a, dk_mid, dv_mid, dk_tail, dv_tail, blk_cnt, like, mid_reps):
+    """(dk, dv) in like's dtype: tier-A gradients + the representative gradients spread as / count."""
+    B, H, L, D = like.shape
+    dk = torch.empty(like.shape, dtype=like.dtype, device=blk_cnt.device)
+    dv = torch.empty_like(dk)
+    _lib.call("vsa_rep_unpool", dk_a, dv_a, dk_mid, dv_mid, dk_tail, dv_tail, blk_cnt, dk, dv, B * H, L, D,
+              int(mid_reps))
+    return dk, dv
+
+
+def row_dot(a, b, blk_cnt):
+    """[B, H, L] fp32 rowsum(a * b) on valid rows, 0 on padding (reference rep_api.cpp row_dot)."""
+    B, H, L, D = a.shape
+    out = torch.empty(B, H, L, device=a.device, dtype=torch.float32)
+    _lib.call("vsa_row_dot", a, b, blk_cnt, out, B * H, L, D)
+    return out

@@ -40,3 +40,10 @@ def check_close(name, got, ref, max_abs=MAX_ABS, rel=REL_L2, mask=None):
     r = rel_l2(got, ref)
     assert err <= max_abs and r <= rel, f"{name}: max-abs {err:.3g} (<= {max_abs}), rel-L2 {r:.3g} (<= {rel})"
     return err, r
+
+
+def bf16_max_abs(ref, floor=MAX_ABS):
+    """The max-abs bound for a bf16-stored output: 2e-2, or half a bf16 step at the largest magnitude when that is
+    larger (a bf16 value of |x| in [2^e, 2^(e+1)) is only defined to 2^(e-8)), so gradients of magnitude > 4 are
+    held to their storage precision while the rel-L2 bound stays 1e-2."""
+    return max(floor, 2.0 ** -8 * float(np.abs(np.asarray(ref, np.float64)).max(initial=0.0)))

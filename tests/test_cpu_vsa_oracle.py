@@ -296,3 +296,56 @@ def test_import_does_not_load_the_library():
     code = ("import sys, self_trainable_or_free_attn_amd.vsa; "
             "assert self_trainable_or_free_attn_amd._lib._lib is None")
     subprocess.run([sys.executable, "-c", code], check=True, cwd=__file__.rsplit("/tests/", 1)[0])
+
+
+# --------------------------------------------------------------------------- three-tier representatives
+def _rep_inputs(seed, cnt, D=16):
+    g = torch.Generator().manual_seed(seed)
+    L = len(cnt) * 64
+    valid = torch.as_tensor(ref.token_valid(cnt, L))[None, None, :, None].double()
+    return [(torch.randn(1, 2, L, D, generator=g, dtype=torch.float64) * valid) for _ in range(3)]
+
+
+def test_rep_tier_a_only_is_fine_attention():
+    cnt = [64, 40, 64, 9]
+    q, k, v = _rep_inputs(0, cnt)
+    m = np.random.default_rng(1).random((1, 2, 4, 4)) < 0.5
+    o, lse = ref.rep_fine_torch(q, k, v, cnt, m, m | (np.random.default_rng(2).random((1, 2, 4, 4)) < 0.5), 4, 1)
+    wo, wl = ref.fine_attention(q.numpy(), k.numpy(), v.numpy(), cnt, m)
+    assert np.allclose(o.numpy(), wo) and np.allclose(np.where(np.isfinite(wl), lse.numpy(), 0), np.where(np.isfinite(wl), wl, 0))
+
+
+def test_rep_constant_groups_equal_dense_attention():
+    """A representative of c identical tokens with + ln c is exactly those c columns: with every group constant,
+    any tier assignment gives dense attention over the valid tokens."""
+    cnt = [64, 64, 37]
+    D, RM = 8, 4
+    g = torch.Generator().manual_seed(3)
+    L = 192
+    base = torch.randn(1, 1, L // 16, D, generator=g, dtype=torch.float64)
+    k = base.repeat_interleave(16, 2)          # constant over every 16-token group
+    v = torch.randn(1, 1, L // 16, D, generator=g, dtype=torch.float64).repeat_interleave(16, 2)
+    q = torch.randn(1, 1, L, D, generator=g, dtype=torch.float64)
+    valid = torch.as_tensor(ref.token_valid(cnt, L))[None, None, :, None].double()
+    q, k, v = q * valid, k * valid, v * valid
+    ma = np.array([[[[1, 0, 0], [0, 0, 1], [0, 0, 0]]]], bool)
+    mab = np.ones_like(ma)  # tiers A and B only: the groups are constant, the blocks are not
+    o, _ = ref.rep_fine_torch(q, k, v, cnt, ma, mab, RM)
+    wo, _ = ref.fine_attention(q.numpy(), k.numpy(), v.numpy(), cnt, np.ones((1, 1, 3, 3), bool))
+    assert np.allclose(o.numpy(), wo, atol=1e-12)
+    # the tail tier alone with blocks made constant
+    kc = k.reshape(1, 1, 3, 64, D)[:, :, :, :1].expand(1, 1, 3, 64, D).reshape(1, 1, L, D) * valid
+    vc = v.reshape(1, 1, 3, 64, D)[:, :, :, :1].expand(1, 1, 3, 64, D).reshape(1, 1, L, D) * valid
+    o, _ = ref.rep_fine_torch(q, kc, vc, cnt, np.zeros_like(ma), np.zeros_like(ma), RM)
+    wo, _ = ref.fine_attention(q.numpy(), kc.numpy(), vc.numpy(), cnt, np.ones((1, 1, 3, 3), bool))
+    assert np.allclose(o.numpy(), wo, atol=1e-12)
+
+
+def test_rep_tables_counts():
+    cnt = [64, 20, 1]
+    x = np.random.default_rng(4).standard_normal((1, 1, 192, 8)).astype(np.float32)
+    km, vm, kt, vt, lcm, lct = ref.rep_tables(x, x, cnt, 4)
+    assert np.allclose(lcm, np.log2([16, 16, 16, 16, 16, 4, 1, 1, 1, 1, 1, 1])[:12].clip(0) * 0 +
+                       np.array([4, 4, 4, 4, 4, 2, -np.inf, -np.inf, 0, -np.inf, -np.inf, -np.inf]))
+    assert np.allclose(lct, np.log2(cnt))
+    assert np.array_equal(km, vm) and (km[0, 0, 6] == 0).all()
