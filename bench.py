@@ -39,6 +39,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--workload", default="echosparse", choices=["echosparse", "vsa", "vsa2_rep", "split"],
+                    help="echosparse: the headline sparse step (default); vsa / vsa2_rep / split: the VSA "
+                         "configurations (fine fwd+bwd at 30720 tokens, three-tier at the HunyuanVideo shape, "
+                         "Zipf-skewed split-KV)")
     return ap.parse_args()
 
 
@@ -89,6 +93,8 @@ def main():
         print("bench.py runs on one GPU only: the EchoSparse path shards by head with no exchange inside the "
               "attention, so this build measures one GPU's share; --gpus must be 1", file=sys.stderr)
         sys.exit(2)
+    if args.workload != "echosparse":
+        return run_vsa_workload(args)
     from self_trainable_or_free_attn_amd import EchoSparseAttention
     from self_trainable_or_free_attn_amd import synthetic
     from self_trainable_or_free_attn_amd.kernels import gfx950
@@ -203,6 +209,172 @@ def main():
         c0, c1 = branches[0][0], None
         result["cpu_baseline"] = cpu_baseline(*c0, attn, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+# ------------------------------------------------------------------------------------------------ VSA workloads
+def _timed(fn, steps, warmup):
+    """(mean ms per call over `steps` calls after `warmup`, last result), bracketed by synchronisations."""
+    out = None
+    for _ in range(warmup):
+        out = fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps * 1e3, out
+
+
+def _events(fn, steps):
+    """mean ms of fn measured with HIP events on torch's current stream (the stream every kernel here uses)."""
+    ms = []
+    for _ in range(steps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1))
+    return sum(ms) / len(ms)
+
+
+def _vsa_cpu_baseline(q, k, v, blk, sel, seconds):
+    """The blockwise numpy port of the fine forward (oracle) on query blocks of head 0 until `seconds` pass."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import vsa_ref as ref
+    f = lambda x: x[0].float().cpu().numpy()
+    qn, kn, vn = f(q), f(k), f(v)
+    cnt = blk.cpu().numpy()
+    ptr, idx = sel.q2k_ptr.cpu().numpy(), sel.q2k_idx.cpu().numpy()
+    nb = cnt.size
+    done, cols, t0 = 0, 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds and done < nb:
+        ref.fine_attention_blocks(qn, kn, vn, cnt, ptr, idx, 0, [done])
+        cols += int(ptr[0, 0, done + 1] - ptr[0, 0, done])
+        done += 1
+    el = time.perf_counter() - t0
+    flops = 4.0 * 64 * 64 * q.shape[-1] * cols
+    return {"value": round(flops / el / 1e12, 5), "unit": "TFLOP/s (fine forward, executed blocks)",
+            "cores": 1, "kind": "port",
+            "sample": f"blockwise numpy port of the fine forward (oracle/vsa_ref.py fine_attention_blocks), head 0, "
+                      f"query blocks 0..{done - 1} of {nb}, {cols} block pairs, {el:.1f} s, one thread"}
+
+
+def run_vsa_workload(args):
+    from self_trainable_or_free_attn_amd import synthetic
+    from self_trainable_or_free_attn_amd.vsa import ops, rep
+    dev = torch.device("cuda:0")
+    W, K = max(1, args.warmup), max(1, args.steps)
+    D = 128
+    if args.workload in ("vsa", "split"):
+        if args.workload == "vsa":   # C2: B1 H24 N30720, top-60 by the original-VSA router, N(0, 1) seed 1
+            B, H, NB = 1, 24, 480
+        else:                        # C5: B1 H40 L75648, Zipf(1.2) lists clipped to [8, 512], seed 4
+            B, H, NB = 1, 40, 1182
+        g = torch.Generator(device=dev).manual_seed(1 if args.workload == "vsa" else 4)
+        q, k, v, dout = (torch.randn(B, H, NB * 64, D, device=dev, generator=g).to(torch.bfloat16) for _ in range(4))
+        blk = torch.full((NB,), 64, dtype=torch.int32, device=dev)
+        if args.workload == "vsa":
+            sel = ops.route_rows(q, k, blk, 60)
+        else:
+            import numpy as np
+            rng = np.random.default_rng(4)
+            mask = np.zeros((B, H, NB, NB), bool)
+            n = np.clip(rng.zipf(1.2, size=(B, H, NB)), 8, 512)
+            for h in range(H):
+                for i in range(NB):
+                    mask[0, h, i, rng.choice(NB, size=int(n[0, h, i]), replace=False)] = True
+            sel = ops.mask_to_selection(torch.as_tensor(mask, device=dev))
+        nnz = int((sel.q2k_ptr[..., -1] - sel.q2k_ptr[..., 0]).sum())
+        qg, kg, vg = (x.detach().clone().requires_grad_(True) for x in (q, k, v))
+        # C5: the manual policy (every list longer than 64 blocks runs as balanced 64-block chunks + ordered merge)
+        split = ops.SplitKV(chunk=64) if args.workload == "split" else None
+
+        def fwd():
+            return ops.fine_block_sparse_attention(qg, kg, vg, blk, sel, split_kv=split)
+
+        def fwd_bwd():
+            o, _ = fwd()
+            return torch.autograd.grad(o, (qg, kg, vg), dout)
+
+        fwd_ms, _ = _timed(lambda: fwd(), K, W)
+        step_ms, _ = _timed(fwd_bwd, K, W)
+        fwd_ev = _events(lambda: fwd(), min(K, 5))
+        fl_fwd = 4.0 * 64 * 64 * D * nnz
+        fl_bwd = 14.0 * 64 * 64 * D * nnz    # KV-owner (4 products) + Q-owner (3 products) per pair
+        res = {"metric": "ms/layer + TFLOPS on executed blocks (% bf16 MFMA peak), VSA fine attention fwd+bwd",
+               "value": round((fl_fwd + fl_bwd) / (step_ms * 1e-3) / 1e12, 2),
+               "unit": "TFLOP/s (executed blocks, fine fwd+bwd)", "n_gpus": 1, "steps": K, "warmup": W,
+               "ms_per_step": round(step_ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+               "dtype": "bf16", "data": "synthetic (N(0,1) q/k/v/dO, seeded)",
+               "config": {"workload": "vsa_c2_fine_fwd_bwd" if args.workload == "vsa" else "vsa_c5_zipf_split",
+                          "batch": B, "heads": H, "seq_len": NB * 64, "head_dim": D, "nnz_pairs": nnz,
+                          "split_kv": "manual chunk 64" if split else None},
+               "fwd_ms": round(fwd_ms, 3), "bwd_ms": round(step_ms - fwd_ms, 3),
+               "fwd_tflops": round(fl_fwd / (fwd_ms * 1e-3) / 1e12, 2),
+               "roofline": {"kernel": "vsa_fwd_kernel (fine forward)", "bound": "mfma",
+                            "achieved": round(fl_fwd / (fwd_ev * 1e-3) / 1e12, 2), "peak": PEAK_BF16 / 1e12,
+                            "unit": "TFLOP/s", "frac": round(fl_fwd / (fwd_ev * 1e-3) / PEAK_BF16, 4),
+                            "traffic": None, "avg_launch_ms": round(fwd_ev, 3)}}
+        if args.workload == "split":
+            unsplit_ms, _ = _timed(lambda: torch.autograd.grad(
+                ops.fine_block_sparse_attention(qg, kg, vg, blk, sel)[0], (qg, kg, vg), dout), K, W)
+            res["unsplit_ms_per_step"] = round(unsplit_ms, 3)
+            res["split_speedup"] = round(unsplit_ms / step_ms, 3)
+            res["split_plan"] = ops.describe_split(qg, sel, split)["fwd"]["info"]
+        if not args.no_cpu:
+            res["cpu_baseline"] = _vsa_cpu_baseline(q, k, v, blk, sel, args.cpu_seconds)
+        print(json.dumps(res), flush=True)
+        return
+    # C4: VSA2 three-tier at the HunyuanVideo shape: B2 H24, 33 x 45 x 80 grid (118800 tokens, 1857 blocks),
+    # Fourier-field Q / K, N(0, 1) V; tiers 5 % full, 20 % x 4 representatives, the rest block means
+    grid = (33, 45, 80)
+    Lr = grid[0] * grid[1] * grid[2]
+    NB = -(-Lr // 64)
+    B, H = 2, 24
+    xs = []
+    for b in range(B):
+        qb, kb, vb, _ = synthetic.fourier_qkv(grid, H, D, seed=21 + b, device=dev, pad_to=NB * 64)
+        xs.append([t.permute(1, 0, 2) for t in (qb, kb, vb)])
+    q, k, v = (torch.stack([x[i] for x in xs]).contiguous() for i in range(3))
+    del xs
+    blk = torch.full((NB,), 64, dtype=torch.int32, device=dev)
+    blk[-1] = Lr - 64 * (NB - 1)
+    g = torch.Generator(device=dev).manual_seed(5)
+    dout = torch.randn(q.shape, device=dev, generator=g).to(torch.bfloat16)
+    tiers = rep.RepTiers(frac_full=0.05, frac_mid=0.20, mid_reps=4)
+    sel = rep.route_tiers(q, k, blk, tiers, R=16)
+    a, b, c = sel.tier_masks(NB)
+    na, nbm, ncm = (int(m.sum()) for m in (a, b, c))
+    cols = 64 * na + 4 * nbm + ncm                 # columns over all (b, h, query block)
+    fl_fwd = 4.0 * 64 * D * cols
+    qg, kg, vg = (x.detach().clone().requires_grad_(True) for x in (q, k, v))
+
+    def fwd():
+        return rep.rep_fine_attention(qg, kg, vg, blk, sel, mid_reps=4)
+
+    def fwd_bwd():
+        o, _ = fwd()
+        return torch.autograd.grad(o, (qg, kg, vg), dout)
+
+    fwd_ms, _ = _timed(fwd, K, W)
+    step_ms, _ = _timed(fwd_bwd, K, W)
+    route_ms, _ = _timed(lambda: rep.route_tiers(q, k, blk, tiers, R=16), min(K, 3), 1)
+    fwd_ev = _events(fwd, min(K, 5))
+    res = {"metric": "ms/layer + TFLOPS on executed blocks (% bf16 MFMA peak), VSA2 64/4/1 three-tier fine fwd+bwd",
+           "value": round(fl_fwd / (fwd_ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s (executed columns, fine forward)",
+           "n_gpus": 1, "steps": K, "warmup": W, "ms_per_step": round(step_ms, 3), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+           "data": "synthetic (Fourier-field Q/K, N(0,1) V and dO, Morton order; seeded)",
+           "config": {"workload": "vsa2_rep_c4_hunyuan", "batch": B, "heads": H, "seq_len": NB * 64,
+                      "valid_tokens": Lr, "head_dim": D, "tier_pairs": {"A": na, "B": nbm, "C": ncm},
+                      "columns_per_query_block": round(cols / (B * H * NB), 1)},
+           "fwd_ms": round(fwd_ms, 3), "bwd_ms": round(step_ms - fwd_ms, 3), "route_tiers_ms": round(route_ms, 3),
+           "roofline": {"kernel": "rep_q_kernel<false> (three-tier forward)", "bound": "mfma",
+                        "achieved": round(fl_fwd / (fwd_ev * 1e-3) / 1e12, 2), "peak": PEAK_BF16 / 1e12,
+                        "unit": "TFLOP/s", "frac": round(fl_fwd / (fwd_ev * 1e-3) / PEAK_BF16, 4), "traffic": None,
+                        "avg_launch_ms": round(fwd_ev, 3)}}
+    print(json.dumps(res), flush=True)
 
 
 if __name__ == "__main__":

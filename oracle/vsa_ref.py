@@ -348,3 +348,34 @@ def rep_fine_torch(q, k, v, blk_cnt, mask_a, mask_ab, RM, phases=7, tables=None)
     o = p @ Vc
     lse = torch.where(has[..., 0], torch.logsumexp(s_safe, -1), torch.full_like(s[..., 0], float("-inf")))
     return o, lse
+
+
+def fine_attention_blocks(q, k, v, blk_cnt, ptr, idx, bh, qblocks):
+    """Blockwise float32 CPU port of the fine forward over CSR lists for the listed query blocks of head bh only:
+    (O [n, 64, D], lse [n, 64]); never materialises L x L (the CPU-baseline leg of bench.py times this). Pinned by
+    agreeing with fine_attention on the same inputs (tests/test_cpu_vsa_oracle.py)."""
+    q, k, v = (np.asarray(x[bh], np.float32) for x in (q, k, v))
+    D = q.shape[-1]
+    cnt = np.asarray(blk_cnt, np.int64)
+    p = np.asarray(ptr, np.int64).reshape(-1, cnt.size + 1)[bh]
+    cols = np.asarray(idx, np.int64)
+    outs, lses = [], []
+    for i in qblocks:
+        qs = q[i * BLOCK:(i + 1) * BLOCK] * np.float32(1.0 / math.sqrt(D))
+        blocks = cols[p[i]:p[i + 1]]
+        m = np.full(BLOCK, -np.inf, np.float32)
+        l = np.zeros(BLOCK, np.float32)
+        o = np.zeros((BLOCK, D), np.float32)
+        for j in blocks:
+            n = int(cnt[j])
+            s = qs @ k[j * BLOCK:j * BLOCK + n].T
+            mn = np.maximum(m, s.max(1))
+            a = np.exp(m - mn)
+            e = np.exp(s - mn[:, None])
+            l = l * a + e.sum(1)
+            o = o * a[:, None] + e @ v[j * BLOCK:j * BLOCK + n]
+            m = mn
+        live = (l > 0) & (np.arange(BLOCK) < cnt[i])
+        outs.append(np.where(live[:, None], o / np.where(live, l, 1)[:, None], 0))
+        lses.append(np.where(live, m + np.log(np.where(live, l, 1)), -np.inf))
+    return np.stack(outs), np.stack(lses)

@@ -349,3 +349,18 @@ def test_rep_tables_counts():
                        np.array([4, 4, 4, 4, 4, 2, -np.inf, -np.inf, 0, -np.inf, -np.inf, -np.inf]))
     assert np.allclose(lct, np.log2(cnt))
     assert np.array_equal(km, vm) and (km[0, 0, 6] == 0).all()
+
+
+def test_blockwise_port_matches_fine_attention():
+    cnt = [64, 40, 64, 9]
+    q, k, v = (x.numpy().astype(np.float32) for x in _inputs(5, cnt))
+    m = np.random.default_rng(6).random((1, 2, 4, 4)) < 0.5
+    m[:, :, 2] = False
+    ptr, idx = ref.csr_from_mask(m)
+    wo, wl = ref.fine_attention(q, k, v, cnt, m)
+    for bh in range(2):
+        o, lse = ref.fine_attention_blocks(q[0], k[0], v[0], cnt, ptr, idx, bh, range(4))
+        assert np.allclose(o.reshape(256, -1), wo[0, bh], atol=1e-5)
+        fin = np.isfinite(wl[0, bh])
+        assert np.array_equal(np.isfinite(lse.reshape(-1)), fin)
+        assert np.allclose(lse.reshape(-1)[fin], wl[0, bh][fin], atol=1e-5)
