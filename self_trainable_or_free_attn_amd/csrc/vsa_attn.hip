@@ -634,12 +634,12 @@ using namespace es;
 static int vsa_check_qkv(const void* q, const void* k, const void* v, int BH, int L, int D) {
   ES_REQUIRE(q && k && v, ES_ERR_INVALID, "VSA: null q / k / v");
   ES_REQUIRE(BH > 0 && L > 0 && L % BK == 0, ES_ERR_INVALID, "VSA: tokens must be [BH, L = NB * 64, D]");
-  ES_REQUIRE(D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 128");
+  ES_REQUIRE(D == 64 || D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 64 or 128 (rows stored with 128 columns)");
   ES_REQUIRE((size_t)L * HD * 2 < (1ull << 31), ES_ERR_UNSUPPORTED, "VSA: one head's tokens exceed 2 GiB");
   return ES_OK;
 }
 
-static VsaFwdArgs fwd_args(const void* q, const void* k, const void* v, const int* blk_cnt, int BH, int L) {
+static VsaFwdArgs fwd_args(const void* q, const void* k, const void* v, const int* blk_cnt, int BH, int L, int D) {
   VsaFwdArgs a = {};
   a.q = (const bf16_t*)q;
   a.k = (const bf16_t*)k;
@@ -648,7 +648,7 @@ static VsaFwdArgs fwd_args(const void* q, const void* k, const void* v, const in
   a.L = L;
   a.NB = L / BK;
   a.BH = BH;
-  a.scale = LOG2E / sqrtf((float)HD);
+  a.scale = LOG2E / sqrtf((float)D);  // D: the logical head dimension (64 or 128)
   return a;
 }
 
@@ -656,7 +656,7 @@ extern "C" int vsa_attn_fwd(const void* q, const void* k, const void* v, const i
                             const int* blk_cnt, void* out, float* lse, int BH, int L, int D, hipStream_t stream) {
   if (int st = vsa_check_qkv(q, k, v, BH, L, D)) return st;
   ES_REQUIRE(row_ptr && blk_cnt && out && lse, ES_ERR_INVALID, "VSA: null tensor pointer");
-  VsaFwdArgs a = fwd_args(q, k, v, blk_cnt, BH, L);
+  VsaFwdArgs a = fwd_args(q, k, v, blk_cnt, BH, L, D);
   a.row_ptr = row_ptr;
   a.col_idx = col_idx;
   a.out = (bf16_t*)out;
@@ -677,7 +677,7 @@ extern "C" int vsa_attn_fwd_tasks(const void* q, const void* k, const void* v, c
   ES_REQUIRE(blk_cnt && tasks && info && out && lse, ES_ERR_INVALID, "VSA: null tensor pointer");
   ES_REQUIRE(max_tasks >= 0, ES_ERR_INVALID, "VSA: negative task capacity");
   if (max_tasks == 0) return ES_OK;
-  VsaFwdArgs a = fwd_args(q, k, v, blk_cnt, BH, L);
+  VsaFwdArgs a = fwd_args(q, k, v, blk_cnt, BH, L, D);
   a.col_idx = col_idx;
   a.tasks = (const int4*)tasks;
   a.info = info;
@@ -691,7 +691,7 @@ extern "C" int vsa_attn_fwd_tasks(const void* q, const void* k, const void* v, c
 
 
 static VsaBwdArgs bwd_args(const void* q, const void* k, const void* v, const void* dout, const float* lse,
-                           const float* delta, const int* blk_cnt, int BH, int L) {
+                           const float* delta, const int* blk_cnt, int BH, int L, int D) {
   VsaBwdArgs a = {};
   a.q = (const bf16_t*)q;
   a.k = (const bf16_t*)k;
@@ -704,8 +704,8 @@ static VsaBwdArgs bwd_args(const void* q, const void* k, const void* v, const vo
   a.NB = L / BK;
   a.BH = BH;
   a.per_xcd = (a.NB + 7) / 8;
-  a.scale = 1.0f / sqrtf((float)HD);
-  a.scale_log2 = LOG2E / sqrtf((float)HD);
+  a.scale = 1.0f / sqrtf((float)D);
+  a.scale_log2 = LOG2E / sqrtf((float)D);
   return a;
 }
 
@@ -717,7 +717,7 @@ extern "C" int vsa_attn_bwd_kv(const void* q, const void* k, const void* v, cons
   ES_REQUIRE(dout && lse && delta && k2q_ptr && blk_cnt && dk && dv, ES_ERR_INVALID, "VSA: null tensor pointer");
   ES_REQUIRE((add_dk == nullptr && add_dv == nullptr) || add_nb >= L / BK, ES_ERR_INVALID,
              "VSA: per-block gradient has fewer rows than blocks");
-  VsaBwdArgs a = bwd_args(q, k, v, dout, lse, delta, blk_cnt, BH, L);
+  VsaBwdArgs a = bwd_args(q, k, v, dout, lse, delta, blk_cnt, BH, L, D);
   a.row_ptr = k2q_ptr;
   a.col_idx = k2q_idx;
   a.add_a = add_dk;
@@ -745,7 +745,7 @@ extern "C" int vsa_attn_bwd_kv_tasks(const void* q, const void* k, const void* v
   ES_REQUIRE(dout && lse && delta && blk_cnt && tasks && info && dk && dv, ES_ERR_INVALID, "VSA: null tensor pointer");
   ES_REQUIRE(max_tasks >= 0, ES_ERR_INVALID, "VSA: negative task capacity");
   if (max_tasks == 0) return ES_OK;
-  VsaBwdArgs a = bwd_args(q, k, v, dout, lse, delta, blk_cnt, BH, L);
+  VsaBwdArgs a = bwd_args(q, k, v, dout, lse, delta, blk_cnt, BH, L, D);
   a.col_idx = k2q_idx;
   a.tasks = (const int4*)tasks;
   a.info = info;
@@ -767,7 +767,7 @@ extern "C" int vsa_attn_bwd_q(const void* q, const void* k, const void* v, const
   if (int st = vsa_check_qkv(q, k, v, BH, L, D)) return st;
   ES_REQUIRE(dout && lse && delta && q2k_ptr && blk_cnt && (dq || dq_acc), ES_ERR_INVALID, "VSA: null tensor pointer");
   ES_REQUIRE(add_dq == nullptr || add_nb >= L / BK, ES_ERR_INVALID, "VSA: per-block gradient has fewer rows than blocks");
-  VsaBwdArgs a = bwd_args(q, k, v, dout, lse, delta, blk_cnt, BH, L);
+  VsaBwdArgs a = bwd_args(q, k, v, dout, lse, delta, blk_cnt, BH, L, D);
   a.row_ptr = q2k_ptr;
   a.col_idx = q2k_idx;
   a.add_a = add_dq;
@@ -788,7 +788,7 @@ extern "C" int vsa_attn_bwd_q_tasks(const void* q, const void* k, const void* v,
   ES_REQUIRE(dout && lse && delta && blk_cnt && tasks && info && dq, ES_ERR_INVALID, "VSA: null tensor pointer");
   ES_REQUIRE(max_tasks >= 0, ES_ERR_INVALID, "VSA: negative task capacity");
   if (max_tasks == 0) return ES_OK;
-  VsaBwdArgs a = bwd_args(q, k, v, dout, lse, delta, blk_cnt, BH, L);
+  VsaBwdArgs a = bwd_args(q, k, v, dout, lse, delta, blk_cnt, BH, L, D);
   a.col_idx = q2k_idx;
   a.tasks = (const int4*)tasks;
   a.info = info;

@@ -263,7 +263,7 @@ using namespace es;
 static int check_tokens(int BH, int L, int D) {
   ES_REQUIRE(BH > 0 && BH <= 65535 && L > 0 && L % BK == 0, ES_ERR_INVALID,
              "VSA: tokens must be [BH <= 65535, L = NB * 64, D]");
-  ES_REQUIRE(D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 128");
+  ES_REQUIRE(D == 64 || D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 64 or 128 (rows stored with 128 columns)");
   return ES_OK;
 }
 

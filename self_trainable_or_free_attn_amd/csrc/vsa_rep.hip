@@ -644,7 +644,7 @@ using namespace es;
 
 static int rep_check(int BH, int L, int D, int RM) {
   ES_REQUIRE(BH > 0 && BH <= 65535 && L > 0 && L % BK == 0, ES_ERR_INVALID, "VSA2-rep: tokens must be [BH, L = NB * 64, D]");
-  ES_REQUIRE(D == HD, ES_ERR_UNSUPPORTED, "VSA2-rep: head dim must be 128");
+  ES_REQUIRE(D == 64 || D == HD, ES_ERR_UNSUPPORTED, "VSA2-rep: head dim must be 64 or 128 (rows stored with 128 columns)");
   ES_REQUIRE(L / BK <= REP_MAX_NB, ES_ERR_UNSUPPORTED, "VSA2-rep: NB <= 2048 blocks");
   ES_REQUIRE(RM == 1 || RM == 2 || RM == 4 || RM == 8 || RM == 16, ES_ERR_INVALID,
              "RepTiers.mid_reps must be one of (1, 2, 4, 8, 16)");
@@ -655,7 +655,7 @@ static int rep_check(int BH, int L, int D, int RM) {
 static RepArgs rep_args(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
                         const float* lc_mid, const void* k_tail, const void* v_tail, const float* lc_tail,
                         const int* q2k_ptr, const int* q2k_idx, const unsigned* bits_a, const unsigned* bits_ab,
-                        const int* blk_cnt, int BH, int L, int RM, int phases) {
+                        const int* blk_cnt, int BH, int L, int D, int RM, int phases) {
   RepArgs a = {};
   a.q = (const bf16_t*)q;
   a.k = (const bf16_t*)k;
@@ -680,8 +680,8 @@ static RepArgs rep_args(const void* q, const void* k, const void* v, const void*
   a.phases = phases;
   a.mid_rows = (a.NB * RM + 63) / 64 * 64;
   a.tail_rows = (a.NB + 63) / 64 * 64;
-  a.scale_log2 = LOG2E / sqrtf((float)HD);
-  a.scale = 1.0f / sqrtf((float)HD);
+  a.scale_log2 = LOG2E / sqrtf((float)D);
+  a.scale = 1.0f / sqrtf((float)D);
   return a;
 }
 
@@ -696,7 +696,7 @@ extern "C" int vsa_rep_attn_fwd(const void* q, const void* k, const void* v, con
              ES_ERR_INVALID, "VSA2-rep: null tensor pointer");
   ES_REQUIRE(phases >= 0 && phases <= 7, ES_ERR_INVALID, "VSA2-rep: phases must be a mask of 1 | 2 | 4");
   RepArgs a = rep_args(q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, q2k_ptr, q2k_idx, bits_a, bits_ab,
-                       blk_cnt, BH, L, RM, phases);
+                       blk_cnt, BH, L, D, RM, phases);
   a.out = (bf16_t*)out;
   a.lse_out = lse;
   hipLaunchKernelGGL(rep_q_kernel<false>, dim3(8 * BH * a.per_xcd), dim3(256), 0, stream, a);
@@ -715,7 +715,7 @@ extern "C" int vsa_rep_attn_bwd_q(const void* q, const void* k, const void* v, c
              ES_ERR_INVALID, "VSA2-rep: null tensor pointer");
   ES_REQUIRE(add_dq == nullptr || add_nb >= L / BK, ES_ERR_INVALID, "VSA2-rep: add_dq has fewer rows than blocks");
   RepArgs a = rep_args(q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, q2k_ptr, q2k_idx, bits_a, bits_ab,
-                       blk_cnt, BH, L, RM, phases);
+                       blk_cnt, BH, L, D, RM, phases);
   a.dout = (const bf16_t*)dout;
   a.lse = lse;
   a.delta = delta;
@@ -754,8 +754,8 @@ extern "C" int vsa_rep_bwd_tables(const void* q, const void* dout, const void* k
   a.tier = tier;
   a.rows = tier == 2 ? a.NB * RM : a.NB;
   a.rows_pad = (a.rows + 63) / 64 * 64;
-  a.scale_log2 = LOG2E / sqrtf((float)HD);
-  a.scale = 1.0f / sqrtf((float)HD);
+  a.scale_log2 = LOG2E / sqrtf((float)D);
+  a.scale = 1.0f / sqrtf((float)D);
   hipLaunchKernelGGL(rep_bwd_tab_kernel, dim3(a.rows_pad / 64, BH), dim3(256), 0, stream, a);
   return check_launch("vsa_rep_bwd_tables");
 }
@@ -777,7 +777,7 @@ extern "C" int vsa_row_dot(const void* x, const void* y, const int* blk_cnt, flo
                            hipStream_t stream) {
   ES_REQUIRE(x && y && blk_cnt && out, ES_ERR_INVALID, "VSA: null tensor pointer");
   ES_REQUIRE(BH > 0 && BH <= 65535 && L > 0 && L % BK == 0, ES_ERR_INVALID, "VSA: tokens must be [BH, L = NB * 64, D]");
-  ES_REQUIRE(D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 128");
+  ES_REQUIRE(D == 64 || D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 64 or 128 (rows stored with 128 columns)");
   const int NB = L / BK;
   hipLaunchKernelGGL(row_dot_kernel, dim3((NB + 3) / 4, BH), dim3(256), 0, stream, (const bf16_t*)x, (const bf16_t*)y,
                      out, blk_cnt, L, NB);

@@ -658,7 +658,7 @@ static int invert(const TopkCarve& c, int* k2q_ptr, int* k2q_idx, int NB, int bh
 
 static int rows_common(const void* qc, const void* kc, const void* scores_in, void* scores_out, int NB, int NBc_pad,
                        int bh0, int bh_count, int K, int* q2k_ptr, int* q2k_idx, int* k2q_ptr, int* k2q_idx,
-                       void* workspace, size_t workspace_bytes, hipStream_t stream, const char* what) {
+                       void* workspace, size_t workspace_bytes, int D, hipStream_t stream, const char* what) {
   ES_REQUIRE(NB >= 1 && NB <= MAX_NB, ES_ERR_UNSUPPORTED, "VSA: route_rows supports 1 <= NB <= 2048 blocks");
   ES_REQUIRE(bh0 >= 0 && bh_count >= 1 && bh_count <= 65535, ES_ERR_INVALID, "VSA: bad (b,h) range");
   RowsArgs a = {};
@@ -670,7 +670,7 @@ static int rows_common(const void* qc, const void* kc, const void* scores_in, vo
   a.NBc_pad = NBc_pad;
   a.bh0 = bh0;
   a.W = (NB + 31) / 32;
-  a.scale = 1.0f / sqrtf((float)HD);
+  a.scale = 1.0f / sqrtf((float)D);  // D: the logical head dimension (64 or 128)
   const size_t lds = (size_t)ROWS * ((NB + 63) & ~63) * 2;
   const dim3 grid((NB + ROWS - 1) / ROWS, bh_count);
   if (K < 0) {  // scores only
@@ -706,21 +706,21 @@ static int rows_common(const void* qc, const void* kc, const void* scores_in, vo
 extern "C" int vsa_block_scores(const void* qc, const void* kc, void* scores, int NB, int NBc_pad, int bh0,
                                 int bh_count, int D, hipStream_t stream) {
   ES_REQUIRE(qc && kc && scores, ES_ERR_INVALID, "VSA: null tensor pointer");
-  ES_REQUIRE(D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 128");
+  ES_REQUIRE(D == 64 || D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 64 or 128 (rows stored with 128 columns)");
   ES_REQUIRE(NBc_pad == (NB + 63) / 64 * 64, ES_ERR_INVALID, "qc must hold ceil(nb/64)*64 pooled rows");
   return rows_common(qc, kc, nullptr, scores, NB, NBc_pad, bh0, bh_count, -1, nullptr, nullptr, nullptr, nullptr,
-                     nullptr, 0, stream, "vsa_block_scores");
+                     nullptr, 0, D, stream, "vsa_block_scores");
 }
 
 extern "C" int vsa_route_rows(const void* qc, const void* kc, int NB, int NBc_pad, int bh0, int bh_count, int K,
                               int D, int* q2k_ptr, int* q2k_idx, int* k2q_ptr, int* k2q_idx, void* workspace,
                               size_t workspace_bytes, hipStream_t stream) {
   ES_REQUIRE(qc && kc, ES_ERR_INVALID, "VSA: null tensor pointer");
-  ES_REQUIRE(D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 128");
+  ES_REQUIRE(D == 64 || D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 64 or 128 (rows stored with 128 columns)");
   ES_REQUIRE(NBc_pad == (NB + 63) / 64 * 64, ES_ERR_INVALID, "qc must hold ceil(nb/64)*64 pooled rows");
   ES_REQUIRE(K >= 0 && K <= NB, ES_ERR_INVALID, "VSA: K must be in [0, NB]");
   return rows_common(qc, kc, nullptr, nullptr, NB, NBc_pad, bh0, bh_count, K, q2k_ptr, q2k_idx, k2q_ptr, k2q_idx,
-                     workspace, workspace_bytes, stream, "vsa_route_rows");
+                     workspace, workspace_bytes, D, stream, "vsa_route_rows");
 }
 
 extern "C" int vsa_row_topk(const void* scores, int NB, int bh0, int bh_count, int K, int* q2k_ptr, int* q2k_idx,
@@ -728,7 +728,7 @@ extern "C" int vsa_row_topk(const void* scores, int NB, int bh0, int bh_count, i
   ES_REQUIRE(scores, ES_ERR_INVALID, "VSA: null tensor pointer");
   ES_REQUIRE(K >= 0 && K <= NB, ES_ERR_INVALID, "VSA: K must be in [0, NB]");
   return rows_common(nullptr, nullptr, scores, nullptr, NB, 0, bh0, bh_count, K, q2k_ptr, q2k_idx, k2q_ptr, k2q_idx,
-                     workspace, workspace_bytes, stream, "vsa_row_topk");
+                     workspace, workspace_bytes, HD, stream, "vsa_row_topk");
 }
 
 extern "C" int vsa_global_topk(const float* scores, int NB, int bh0, int bh_count, long long budget, int* q2k_ptr,
@@ -783,7 +783,7 @@ static void launch_psp(const PspArgs& a, bool scores, int bh_count, hipStream_t 
 static int psp(const void* qr, const void* kr, const int* blk_cnt, float* lse2, float* scores, int NB, int R,
                int row_norm, int bh0, int bh_count, int D, bool do_scores, hipStream_t stream, const char* what) {
   ES_REQUIRE(qr && kr && blk_cnt && lse2 && (!do_scores || scores), ES_ERR_INVALID, "VSA: null tensor pointer");
-  ES_REQUIRE(D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 128");
+  ES_REQUIRE(D == 64 || D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 64 or 128 (rows stored with 128 columns)");
   ES_REQUIRE(R == 4 || R == 8 || R == 16 || R == 32, ES_ERR_INVALID, "VSA2: router pool size R must be 4, 8, 16 or 32");
   ES_REQUIRE(row_norm == 0 || row_norm == 1, ES_ERR_INVALID, "VSA2: row_norm must be 0 (valid_groups) or 1 (paper)");
   ES_REQUIRE(NB >= 1 && bh0 >= 0 && bh_count >= 1 && bh_count <= 65535, ES_ERR_INVALID, "VSA: bad (b,h) range");
@@ -800,7 +800,7 @@ static int psp(const void* qr, const void* kr, const int* blk_cnt, float* lse2, 
   a.Lr_pad = (NB * G + 63) / 64 * 64;
   a.bh0 = bh0;
   a.row_norm = row_norm;
-  a.scale_log2 = LOG2E / sqrtf((float)HD);
+  a.scale_log2 = LOG2E / sqrtf((float)D);
   ES_REQUIRE((size_t)a.Lr_pad * HD * 2 < (1ull << 31), ES_ERR_UNSUPPORTED, "VSA2: pooled rows exceed 2 GiB");
   switch (G) {
     case 2: launch_psp<2>(a, do_scores, bh_count, stream); break;

@@ -272,7 +272,7 @@ extern "C" int vsa_split_plan(const int* ptr, int BH, int NB, int chunk, int max
 extern "C" int vsa_split_merge_fwd(const float* part_o, const float* part_lse, const int* merges, const int* info,
                                    int max_merges, const int* blk_cnt, void* o, float* lse, int BH, int L, int D,
                                    int mask_rows, hipStream_t stream) {
-  ES_REQUIRE(D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 128");
+  ES_REQUIRE(D == 64 || D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 64 or 128 (rows stored with 128 columns)");
   ES_REQUIRE(BH >= 1 && L > 0 && L % BK == 0, ES_ERR_INVALID, "o must be [B,H,L,D]");
   if (max_merges <= 0) return ES_OK;
   ES_REQUIRE(part_o && part_lse && merges && info && blk_cnt && o && lse, ES_ERR_INVALID, "VSA2: null tensor pointer");
@@ -284,7 +284,7 @@ extern "C" int vsa_split_merge_fwd(const float* part_o, const float* part_lse, c
 extern "C" int vsa_split_merge_sum(const float* part, const int* merges, const int* info, int max_merges,
                                    const float* add, int add_nb, const int* blk_cnt, void* out, float* out_f32, int BH,
                                    int L, int D, hipStream_t stream) {
-  ES_REQUIRE(D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 128");
+  ES_REQUIRE(D == 64 || D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 64 or 128 (rows stored with 128 columns)");
   ES_REQUIRE(BH >= 1 && L > 0 && L % BK == 0, ES_ERR_INVALID, "out must be [B,H,L,D]");
   if (max_merges <= 0) return ES_OK;
   ES_REQUIRE(part && merges && info && blk_cnt && (out || out_f32), ES_ERR_INVALID, "VSA2: null tensor pointer");

@@ -13,10 +13,12 @@ chunking of ``route``.
 import math
 
 import torch
+import torch.nn.functional as F
 
 from .. import _lib
 
 BLOCK = 64
+HD = 128                # columns of every token row handed to the C ABI
 _FWD_VARIANT = [0]
 
 
@@ -29,7 +31,7 @@ def _tokens(x, name):
     _check(isinstance(x, torch.Tensor) and x.is_cuda, f"{name} must be a CUDA tensor")
     _check(x.dim() == 4 and x.is_contiguous(), f"{name} must be contiguous [B, H, L, D]")
     _check(x.dtype == torch.bfloat16, f"{name} must be bf16 (this build computes in bf16)")
-    _check(x.shape[3] == 128, f"{name}: head dim must be 128 (this build)")
+    _check(x.shape[3] in (64, HD), f"{name}: head dim must be 64 or 128 (this build)")
     _check(x.shape[2] % BLOCK == 0, f"{name}: L must be a multiple of 64")
 
 
@@ -41,6 +43,30 @@ def _i32(x, name):
 def _f32(x, name):
     _check(isinstance(x, torch.Tensor) and x.is_cuda and x.dtype == torch.float32 and x.is_contiguous(),
            f"{name} must be a contiguous fp32 CUDA tensor")
+
+
+def _wide(x):
+    """x with its last dim zero-padded to 128 columns (x itself when already 128 wide, or None). The C ABI stores
+    every row with 128 columns and takes the logical head dim D (64 or 128) separately: zero columns add exact zeros
+    to every dot product, and every output column past D comes out zero, so narrowing back loses nothing."""
+    if x is None or x.shape[-1] == HD:
+        return x
+    return F.pad(x, (0, HD - x.shape[-1])).contiguous()
+
+
+def _narrow(x, D):
+    return x if x is None or D == HD else x[..., :D].contiguous()
+
+
+class _InPlace:
+    """A 128-column view of an in-place argument; put() writes its first D columns back."""
+
+    def __init__(self, x):
+        self.x, self.w = x, _wide(x)
+
+    def put(self):
+        if self.x is not None and self.w is not self.x:
+            self.x.copy_(self.w[..., :self.x.shape[-1]])
 
 
 def _ceil64(n):
@@ -78,12 +104,12 @@ def pool_fwd(q, k, v, blk_cnt, R):
     NB = L // BLOCK
     _check(blk_cnt.numel() == NB, "blk_cnt must have L/64 entries")
     G = BLOCK // R
-    qr = torch.zeros(B, H, _ceil64(NB * G), D, device=q.device, dtype=q.dtype)
+    qr = torch.zeros(B, H, _ceil64(NB * G), HD, device=q.device, dtype=q.dtype)
     kr = torch.zeros_like(qr)
-    qc = torch.zeros(B, H, _ceil64(NB), D, device=q.device, dtype=q.dtype)
+    qc = torch.zeros(B, H, _ceil64(NB), HD, device=q.device, dtype=q.dtype)
     kc, vc = torch.zeros_like(qc), torch.zeros_like(qc)
-    _lib.call("vsa_pool", q, k, v, blk_cnt, qr, kr, None, qc, kc, vc, B * H, L, D, int(R))
-    return qr, kr, qc, kc, vc
+    _lib.call("vsa_pool", _wide(q), _wide(k), _wide(v), blk_cnt, qr, kr, None, qc, kc, vc, B * H, L, D, int(R))
+    return [_narrow(t, D) for t in (qr, kr, qc, kc, vc)]
 
 
 def fuse_fwd(of, oc, gate, blk_cnt, gate_act):
@@ -99,9 +125,10 @@ def fuse_fwd(of, oc, gate, blk_cnt, gate_act):
             mode = 2
         else:
             raise RuntimeError("gate must be [B, H, L] or [B, H, L, D]")
-    o = torch.empty_like(of)
-    _lib.call("vsa_fuse_fwd", of, oc, gate, o, blk_cnt, B * H, L, D, oc.shape[2], mode, int(gate_act))
-    return o
+    o = torch.empty(B, H, L, HD, device=of.device, dtype=of.dtype)
+    _lib.call("vsa_fuse_fwd", _wide(of), _wide(oc), _wide(gate) if mode == 2 else gate, o, blk_cnt, B * H, L, D,
+              oc.shape[2], mode, int(gate_act))
+    return _narrow(o, D)
 
 
 def fuse_bwd(dout, of, oc, gate, blk_cnt, gate_act, write_dout_f=True):
@@ -109,23 +136,24 @@ def fuse_bwd(dout, of, oc, gate, blk_cnt, gate_act, write_dout_f=True):
     _tokens(dout, "dout")
     B, H, L, D = dout.shape
     mode = 0 if gate is None else (1 if gate.dim() == 3 else 2)
-    dout_f = torch.empty_like(dout) if write_dout_f else None
+    dout_f = torch.empty(B, H, L, HD, device=dout.device, dtype=dout.dtype) if write_dout_f else None
     delta_f = torch.empty(B, H, L, device=dout.device, dtype=torch.float32)
-    dout_c = torch.zeros(B, H, oc.shape[2], D, device=dout.device, dtype=dout.dtype)
+    dout_c = torch.zeros(B, H, oc.shape[2], HD, device=dout.device, dtype=dout.dtype)
     delta_c = torch.zeros(B, H, oc.shape[2], device=dout.device, dtype=torch.float32)
-    dgate = torch.empty_like(gate) if gate is not None else None
-    _lib.call("vsa_fuse_bwd", dout, of, oc, gate, dout_f, delta_f, dout_c, delta_c, dgate, blk_cnt, B * H, L, D,
-              oc.shape[2], mode, int(gate_act))
-    return dout_f, delta_f, dout_c, delta_c, dgate
+    gate_w = _wide(gate) if mode == 2 else gate
+    dgate = torch.empty_like(gate_w) if gate is not None else None
+    _lib.call("vsa_fuse_bwd", _wide(dout), _wide(of), _wide(oc), gate_w, dout_f, delta_f, dout_c,
+              delta_c, dgate, blk_cnt, B * H, L, D, oc.shape[2], mode, int(gate_act))
+    return _narrow(dout_f, D), delta_f, _narrow(dout_c, D), delta_c, _narrow(dgate, D) if mode == 2 else dgate
 
 
 def finalize(acc, add, blk_cnt, like):
     """valid ? acc + add[blk] / cnt : 0 in like's dtype (reference fuse.cu:9)."""
     B, H, L, D = like.shape
-    out = torch.empty(like.shape, dtype=like.dtype, device=blk_cnt.device)
+    out = torch.empty(B, H, L, HD, dtype=like.dtype, device=blk_cnt.device)
     add_nb = add.shape[2] if add is not None else 0
-    _lib.call("vsa_finalize", acc, add, add_nb, out, blk_cnt, B * H, L, D)
-    return out
+    _lib.call("vsa_finalize", _wide(acc), _wide(add), add_nb, out, blk_cnt, B * H, L, D)
+    return _narrow(out, D)
 
 
 # ------------------------------------------------------------------ routers
@@ -135,7 +163,7 @@ def _workspace(bh_count, NB, device):
 
 def _block_args(qc, kc, nb):
     _check(qc.dim() == 4 and qc.shape == kc.shape, "qc/kc must be [B, H, NBc_pad, D] (pool_fwd)")
-    _check(qc.shape[3] == 128, "qc: head dim must be 128 (this build)")
+    _check(qc.shape[3] in (64, HD), "qc: head dim must be 64 or 128 (this build)")
     _check(nb >= 1 and qc.shape[2] == _ceil64(nb), "qc must hold ceil(nb/64)*64 pooled rows")
 
 
@@ -147,7 +175,8 @@ def block_scores(qc, kc, nb, bh0=0, bh_count=0):
         bh_count = BH - bh0
     _check(bh0 >= 0 and bh_count <= 65535 and bh0 + bh_count <= BH, "bad (b,h) range")
     scores = torch.empty(bh_count, nb, nb, device=qc.device, dtype=qc.dtype)
-    _lib.call("vsa_block_scores", qc, kc, scores, int(nb), qc.shape[2], int(bh0), int(bh_count), qc.shape[3])
+    _lib.call("vsa_block_scores", _wide(qc), _wide(kc), scores, int(nb), qc.shape[2], int(bh0), int(bh_count),
+              qc.shape[3])
     return scores
 
 
@@ -181,9 +210,10 @@ def route_rows(qc, kc, nb, topk, max_score_bytes=2 << 30):
     out = _csr(B, H, NB, BH * NB * K, qc.device)
     chunk = min(BH, 65535)
     ws = _workspace(chunk, NB, qc.device)
+    D, qc, kc = qc.shape[3], _wide(qc), _wide(kc)
     for bh0 in range(0, BH, chunk):
         cnt = min(chunk, BH - bh0)
-        _lib.call("vsa_route_rows", qc, kc, NB, qc.shape[2], bh0, cnt, K, qc.shape[3], *out, ws, ws.numel())
+        _lib.call("vsa_route_rows", qc, kc, NB, qc.shape[2], bh0, cnt, K, D, *out, ws, ws.numel())
     return list(out)
 
 
@@ -191,7 +221,7 @@ def router_lse(qr, kr, blk_cnt, R):
     """lse2 [B, H, Lr_pad] of every pooled query row (reference vsa2_api.cpp:122-135)."""
     B, H, Lr_pad, D = qr.shape
     lse2 = torch.empty(B, H, Lr_pad, device=qr.device, dtype=torch.float32)
-    _lib.call("vsa_router_lse", qr, kr, blk_cnt, lse2, blk_cnt.numel(), int(R), B * H, D)
+    _lib.call("vsa_router_lse", _wide(qr), _wide(kr), blk_cnt, lse2, blk_cnt.numel(), int(R), B * H, D)
     return lse2
 
 
@@ -202,7 +232,7 @@ def router_scores(qr, kr, lse2, blk_cnt, R, row_norm, bh0=0, bh_count=0):
     if bh_count <= 0:
         bh_count = B * H - bh0
     scores = torch.empty(bh_count, NB, NB, device=qr.device, dtype=torch.float32)
-    _lib.call("vsa_router_scores", qr, kr, lse2, blk_cnt, scores, NB, int(R), int(row_norm), int(bh0), int(bh_count), D)
+    _lib.call("vsa_router_scores", _wide(qr), _wide(kr), lse2, blk_cnt, scores, NB, int(R), int(row_norm), int(bh0), int(bh_count), D)
     return scores
 
 
@@ -228,13 +258,14 @@ def route(qr, kr, blk_cnt, R, budget, row_norm, max_score_bytes=2 << 30):
     _check(BH * keff < 2 ** 31, "VSA2: total selected blocks exceed int32 CSR range")
     out = _csr(B, H, NB, BH * keff, qr.device)
     lse2 = router_lse(qr, kr, blk_cnt, R)
+    D, qr, kr = qr.shape[3], _wide(qr), _wide(kr)
     chunk = int(max(1, min(BH, int(max_score_bytes) // max(nn * 4, 1), 65535)))
     ws = _workspace(chunk, NB, qr.device)
     scores = torch.empty(chunk, NB, NB, device=qr.device, dtype=torch.float32)
     for bh0 in range(0, BH, chunk):
         cnt = min(chunk, BH - bh0)
         s = scores[:cnt]
-        _lib.call("vsa_router_scores", qr, kr, lse2, blk_cnt, s, NB, int(R), int(row_norm), bh0, cnt, qr.shape[3])
+        _lib.call("vsa_router_scores", qr, kr, lse2, blk_cnt, s, NB, int(R), int(row_norm), bh0, cnt, D)
         _lib.call("vsa_global_topk", s, NB, bh0, cnt, int(budget), *out, None, ws, ws.numel())
     return list(out)
 
@@ -269,10 +300,10 @@ def attn_fwd(q, k, v, row_ptr, col_idx, blk_cnt, use_tk=False):
     _i32(col_idx, "col_idx")
     B, H, L, D = q.shape
     _check(row_ptr.numel() == B * H * (L // BLOCK + 1), "metadata shape mismatch")
-    o = torch.empty_like(q)
+    o = torch.empty(B, H, L, HD, device=q.device, dtype=q.dtype)
     lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
-    _lib.call("vsa_attn_fwd", q, k, v, row_ptr, col_idx, blk_cnt, o, lse, B * H, L, D)
-    return o, lse
+    _lib.call("vsa_attn_fwd", _wide(q), _wide(k), _wide(v), row_ptr, col_idx, blk_cnt, o, lse, B * H, L, D)
+    return _narrow(o, D), lse
 
 
 def attn_bwd(q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, dq_acc=None, add_dk=None, add_dv=None,
@@ -283,25 +314,28 @@ def attn_bwd(q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, dq_acc=None, 
     if dq_acc is not None:
         _check(dq_acc.dtype == torch.float32 and dq_acc.shape == q.shape, "dq_acc must be fp32 like q")
     f = dict(device=q.device, dtype=torch.float32) if out_fp32 else dict(device=q.device, dtype=q.dtype)
-    dk, dv = torch.empty(q.shape, **f), torch.empty(q.shape, **f)
+    dk, dv = torch.empty(B, H, L, HD, **f), torch.empty(B, H, L, HD, **f)
     add_nb = add_dk.shape[2] if add_dk is not None else (add_dv.shape[2] if add_dv is not None else 0)
-    _lib.call("vsa_attn_bwd_kv", q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, add_dk, add_dv, add_nb, dk, dv,
-              1 if out_fp32 else 0, B * H, L, D)
+    q, k, v, dout = _wide(q), _wide(k), _wide(v), _wide(dout)
+    _lib.call("vsa_attn_bwd_kv", q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, _wide(add_dk), _wide(add_dv),
+              add_nb, dk, dv, 1 if out_fp32 else 0, B * H, L, D)
     if dq_acc is not None:
         q2k_ptr, q2k_idx = csr_transpose(row_ptr, col_idx)
-        _lib.call("vsa_attn_bwd_q", q, k, v, dout, lse, delta, q2k_ptr, q2k_idx, blk_cnt, None, 0, None, dq_acc,
+        acc = _InPlace(dq_acc)
+        _lib.call("vsa_attn_bwd_q", q, k, v, dout, lse, delta, q2k_ptr, q2k_idx, blk_cnt, None, 0, None, acc.w,
                   B * H, L, D)
-    return dk, dv
+        acc.put()
+    return _narrow(dk, D), _narrow(dv, D)
 
 
 def attn_bwd_q(q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, add_dq=None):
     """dQ over the q2k CSR without atomics, + add_dq / cnt (reference vsa2_api.cpp:419-457)."""
     _attn_args(q, k, v, blk_cnt)
     B, H, L, D = q.shape
-    dq = torch.empty_like(q)
-    _lib.call("vsa_attn_bwd_q", q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, add_dq,
-              add_dq.shape[2] if add_dq is not None else 0, dq, None, B * H, L, D)
-    return dq
+    dq = torch.empty(B, H, L, HD, device=q.device, dtype=q.dtype)
+    _lib.call("vsa_attn_bwd_q", _wide(q), _wide(k), _wide(v), _wide(dout), lse, delta, row_ptr, col_idx, blk_cnt,
+              _wide(add_dq), add_dq.shape[2] if add_dq is not None else 0, dq, None, B * H, L, D)
+    return _narrow(dq, D)
 
 
 # ------------------------------------------------------------------ split-KV
@@ -329,11 +363,13 @@ def attn_fwd_tasks(q, k, v, col_idx, blk_cnt, tasks, info, part_o, part_lse):
     _attn_args(q, k, v, blk_cnt)
     B, H, L, D = q.shape
     _check(part_lse.numel() == part_o.numel() // D, "part_lse must be [slots, 64]")
-    o = torch.empty_like(q)
+    o = torch.empty(B, H, L, HD, device=q.device, dtype=q.dtype)
     lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
-    _lib.call("vsa_attn_fwd_tasks", q, k, v, col_idx, blk_cnt, tasks, info, tasks.shape[0], o, lse,
-              part_o if part_o.numel() else None, part_lse if part_lse.numel() else None, B * H, L, D)
-    return o, lse
+    po = _InPlace(part_o if part_o.numel() else None)
+    _lib.call("vsa_attn_fwd_tasks", _wide(q), _wide(k), _wide(v), col_idx, blk_cnt, tasks, info, tasks.shape[0], o,
+              lse, po.w, part_lse if part_lse.numel() else None, B * H, L, D)
+    po.put()
+    return _narrow(o, D), lse
 
 
 def split_merge_fwd(part_o, part_lse, merges, info, blk_cnt, o, lse, mask_rows=True):
@@ -341,8 +377,10 @@ def split_merge_fwd(part_o, part_lse, merges, info, blk_cnt, o, lse, mask_rows=T
     if part_o.numel() == 0:
         return
     B, H, L, D = o.shape
-    _lib.call("vsa_split_merge_fwd", part_o, part_lse, merges, info, merges.shape[0], blk_cnt, o, lse, B * H, L, D,
-              1 if mask_rows else 0)
+    ow = _InPlace(o)
+    _lib.call("vsa_split_merge_fwd", _wide(part_o), part_lse, merges, info, merges.shape[0], blk_cnt, ow.w, lse,
+              B * H, L, D, 1 if mask_rows else 0)
+    ow.put()
 
 
 def split_merge_sum(part, merges, info, add, blk_cnt, out):
@@ -351,8 +389,11 @@ def split_merge_sum(part, merges, info, add, blk_cnt, out):
         return
     B, H, L, D = out.shape
     f32 = out.dtype == torch.float32
-    _lib.call("vsa_split_merge_sum", part, merges, info, merges.shape[0], add, add.shape[2] if add is not None else 0,
-              blk_cnt, None if f32 else out, out if f32 else None, B * H, L, D)
+    ow = _InPlace(out)
+    _lib.call("vsa_split_merge_sum", _wide(part), merges, info, merges.shape[0], _wide(add),
+              add.shape[2] if add is not None else 0, blk_cnt, None if f32 else ow.w, ow.w if f32 else None,
+              B * H, L, D)
+    ow.put()
 
 
 def attn_bwd_tasks(q, k, v, dout, lse, delta, col_idx, blk_cnt, tasks, info, dq_acc, add_dk, add_dv, part_dk,
@@ -363,23 +404,27 @@ def attn_bwd_tasks(q, k, v, dout, lse, delta, col_idx, blk_cnt, tasks, info, dq_
     _check(dq_acc is None, "attn_bwd_tasks: dQ comes from attn_bwd_q_tasks on this build (no atomics)")
     _attn_args(q, k, v, blk_cnt)
     B, H, L, D = q.shape
-    dk, dv = torch.empty_like(q), torch.empty_like(q)
+    dk = torch.empty(B, H, L, HD, device=q.device, dtype=q.dtype)
+    dv = torch.empty_like(dk)
     add_nb = add_dk.shape[2] if add_dk is not None else (add_dv.shape[2] if add_dv is not None else 0)
-    _lib.call("vsa_attn_bwd_kv_tasks", q, k, v, dout, lse, delta, col_idx, blk_cnt, tasks, info, tasks.shape[0],
-              add_dk, add_dv, add_nb, dk, dv, part_dk if part_dk.numel() else None,
-              part_dv if part_dv.numel() else None, B * H, L, D)
-    return dk, dv
+    pk, pv = _InPlace(part_dk if part_dk.numel() else None), _InPlace(part_dv if part_dv.numel() else None)
+    _lib.call("vsa_attn_bwd_kv_tasks", _wide(q), _wide(k), _wide(v), _wide(dout), lse, delta, col_idx, blk_cnt, tasks,
+              info, tasks.shape[0], _wide(add_dk), _wide(add_dv), add_nb, dk, dv, pk.w, pv.w, B * H, L, D)
+    pk.put()
+    pv.put()
+    return _narrow(dk, D), _narrow(dv, D)
 
 
 def attn_bwd_q_tasks(q, k, v, dout, lse, delta, col_idx, blk_cnt, tasks, info, add_dq, part_dq):
     """dQ of direct q2k tasks; split chunks fill part_dq (reference vsa2_api.cpp:687-730)."""
     _attn_args(q, k, v, blk_cnt)
     B, H, L, D = q.shape
-    dq = torch.empty_like(q)
-    _lib.call("vsa_attn_bwd_q_tasks", q, k, v, dout, lse, delta, col_idx, blk_cnt, tasks, info, tasks.shape[0],
-              add_dq, add_dq.shape[2] if add_dq is not None else 0, dq, part_dq if part_dq.numel() else None,
-              B * H, L, D)
-    return dq
+    dq = torch.empty(B, H, L, HD, device=q.device, dtype=q.dtype)
+    pq = _InPlace(part_dq if part_dq.numel() else None)
+    _lib.call("vsa_attn_bwd_q_tasks", _wide(q), _wide(k), _wide(v), _wide(dout), lse, delta, col_idx, blk_cnt, tasks,
+              info, tasks.shape[0], _wide(add_dq), add_dq.shape[2] if add_dq is not None else 0, dq, pq.w, B * H, L, D)
+    pq.put()
+    return _narrow(dq, D)
 
 
 def attn_bwd_q_acc(q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, dq_acc):
@@ -387,8 +432,10 @@ def attn_bwd_q_acc(q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, dq_acc)
     _attn_args(q, k, v, blk_cnt)
     _f32(dq_acc, "dq_acc")
     B, H, L, D = q.shape
-    _lib.call("vsa_attn_bwd_q", q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, None, 0, None, dq_acc, B * H,
-              L, D)
+    acc = _InPlace(dq_acc)
+    _lib.call("vsa_attn_bwd_q", _wide(q), _wide(k), _wide(v), _wide(dout), lse, delta, row_ptr, col_idx, blk_cnt, None,
+              0, None, acc.w, B * H, L, D)
+    acc.put()
     return dq_acc
 
 
@@ -401,13 +448,15 @@ def rep_build(k, v, blk_cnt, mid_reps):
     _tokens(v, "v")
     B, H, L, D = k.shape
     NB, RM = L // BLOCK, int(mid_reps)
-    k_mid = torch.zeros(B, H, _ceil64(NB * RM), D, device=k.device, dtype=k.dtype)
+    k_mid = torch.zeros(B, H, _ceil64(NB * RM), HD, device=k.device, dtype=k.dtype)
     v_mid = torch.zeros_like(k_mid)
-    k_tail = torch.zeros(B, H, _ceil64(NB), D, device=k.device, dtype=k.dtype)
+    k_tail = torch.zeros(B, H, _ceil64(NB), HD, device=k.device, dtype=k.dtype)
     v_tail = torch.zeros_like(k_tail)
     lc_mid = torch.empty(NB * RM, device=k.device, dtype=torch.float32)
     lc_tail = torch.empty(NB, device=k.device, dtype=torch.float32)
-    _lib.call("vsa_rep_build", k, v, blk_cnt, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, B * H, L, D, RM)
+    _lib.call("vsa_rep_build", _wide(k), _wide(v), blk_cnt, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, B * H, L, D,
+              RM)
+    k_mid, v_mid, k_tail, v_tail = (_narrow(t, D) for t in (k_mid, v_mid, k_tail, v_tail))
     return [k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail]
 
 
@@ -430,13 +479,14 @@ def route_tiers(qr, kr, blk_cnt, R, budget_a, budget_ab, row_norm, max_score_byt
     bits_a = torch.zeros(B, H, NB, W, **i32)
     bits_ab = torch.zeros(B, H, NB, W, **i32)
     lse2 = router_lse(qr, kr, blk_cnt, R)
+    D, qr, kr = qr.shape[3], _wide(qr), _wide(kr)
     chunk = int(max(1, min(BH, int(max_score_bytes) // max(nn * 4, 1), 65535)))
     ws = _workspace(chunk, NB, dev)
     scores = torch.empty(chunk, NB, NB, device=dev, dtype=torch.float32)
     for bh0 in range(0, BH, chunk):
         cnt = min(chunk, BH - bh0)
         s = scores[:cnt]
-        _lib.call("vsa_router_scores", qr, kr, lse2, blk_cnt, s, NB, int(R), int(row_norm), bh0, cnt, qr.shape[3])
+        _lib.call("vsa_router_scores", qr, kr, lse2, blk_cnt, s, NB, int(R), int(row_norm), bh0, cnt, D)
         if kab != ka:
             _lib.call("vsa_global_topk", s, NB, bh0, cnt, kab, *ab_out, bits_ab, ws, ws.numel())
         _lib.call("vsa_global_topk", s, NB, bh0, cnt, ka, *a_out, bits_a, ws, ws.numel())
@@ -455,11 +505,12 @@ def rep_attn_fwd(q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, q2k_ptr
     """(o, lse) of the three-tier attention (reference rep_api.cpp rep_attn_fwd); diag is accepted and ignored."""
     _attn_args(q, k, v, blk_cnt)
     B, H, L, D = q.shape
-    o = torch.empty_like(q)
+    o = torch.empty(B, H, L, HD, device=q.device, dtype=q.dtype)
     lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
-    _lib.call("vsa_rep_attn_fwd", q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, q2k_ptr, q2k_idx, bits_a,
-              bits_ab, blk_cnt, o, lse, B * H, L, D, int(mid_reps), int(phases))
-    return o, lse
+    _lib.call("vsa_rep_attn_fwd", _wide(q), _wide(k), _wide(v), _wide(k_mid), _wide(v_mid), lc_mid, _wide(k_tail),
+              _wide(v_tail), lc_tail, q2k_ptr, q2k_idx, bits_a, bits_ab, blk_cnt, o, lse, B * H, L, D, int(mid_reps),
+              int(phases))
+    return _narrow(o, D), lse
 
 
 def rep_attn_bwd_q(q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, dout, lse, delta, q2k_ptr, q2k_idx,
@@ -470,17 +521,27 @@ def rep_attn_bwd_q(q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, dout,
     the tables by a KV-owner pass instead of atomics."""
     _attn_args(q, k, v, blk_cnt)
     B, H, L, D = q.shape
-    dq = torch.empty_like(q)
+    dq = torch.empty(B, H, L, HD, device=q.device, dtype=q.dtype)
+    q, k, v, dout = _wide(q), _wide(k), _wide(v), _wide(dout)
+    k_mid, v_mid, k_tail, v_tail = _wide(k_mid), _wide(v_mid), _wide(k_tail), _wide(v_tail)
+    acc = _InPlace(dq_acc)
     _lib.call("vsa_rep_attn_bwd_q", q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, dout, lse, delta, q2k_ptr,
-              q2k_idx, bits_a, bits_ab, blk_cnt, add_dq, add_dq.shape[2] if add_dq is not None else 0, dq_acc, dq,
-              B * H, L, D, int(mid_reps), int(phases))
+              q2k_idx, bits_a, bits_ab, blk_cnt, _wide(add_dq), add_dq.shape[2] if add_dq is not None else 0, acc.w,
+              dq, B * H, L, D, int(mid_reps), int(phases))
+    acc.put()
     if phases & 2:
-        _lib.call("vsa_rep_bwd_tables", q, dout, k_mid, v_mid, lc_mid, lse, delta, bits_a, bits_ab, dk_mid, dv_mid,
+        dkm, dvm = _InPlace(dk_mid), _InPlace(dv_mid)
+        _lib.call("vsa_rep_bwd_tables", q, dout, k_mid, v_mid, lc_mid, lse, delta, bits_a, bits_ab, dkm.w, dvm.w,
                   B * H, L, D, int(mid_reps), 2)
+        dkm.put()
+        dvm.put()
     if phases & 4:
-        _lib.call("vsa_rep_bwd_tables", q, dout, k_tail, v_tail, lc_tail, lse, delta, bits_a, bits_ab, dk_tail,
-                  dv_tail, B * H, L, D, int(mid_reps), 4)
-    return dq
+        dkt, dvt = _InPlace(dk_tail), _InPlace(dv_tail)
+        _lib.call("vsa_rep_bwd_tables", q, dout, k_tail, v_tail, lc_tail, lse, delta, bits_a, bits_ab, dkt.w, dvt.w,
+                  B * H, L, D, int(mid_reps), 4)
+        dkt.put()
+        dvt.put()
+    return _narrow(dq, D)
 
 
 def tier_a_bwd_kv(q, k, v, dout, lse, delta, k2q_ptr, k2q_idx, blk_cnt, dq_acc=None):
@@ -492,16 +553,16 @@ def tier_a_bwd_kv(q, k, v, dout, lse, delta, k2q_ptr, k2q_idx, blk_cnt, dq_acc=N
 def rep_unpool(dk_a, dv_a, dk_mid, dv_mid, dk_tail, dv_tail, blk_cnt, like, mid_reps):
     """(dk, dv) in like's dtype: tier-A gradients + the representative gradients spread as / count."""
     B, H, L, D = like.shape
-    dk = torch.empty(like.shape, dtype=like.dtype, device=blk_cnt.device)
+    dk = torch.empty(B, H, L, HD, dtype=like.dtype, device=blk_cnt.device)
     dv = torch.empty_like(dk)
-    _lib.call("vsa_rep_unpool", dk_a, dv_a, dk_mid, dv_mid, dk_tail, dv_tail, blk_cnt, dk, dv, B * H, L, D,
-              int(mid_reps))
-    return dk, dv
+    _lib.call("vsa_rep_unpool", *(_wide(t) for t in (dk_a, dv_a, dk_mid, dv_mid, dk_tail, dv_tail)), blk_cnt, dk, dv,
+              B * H, L, D, int(mid_reps))
+    return _narrow(dk, D), _narrow(dv, D)
 
 
 def row_dot(a, b, blk_cnt):
     """[B, H, L] fp32 rowsum(a * b) on valid rows, 0 on padding (reference rep_api.cpp row_dot)."""
     B, H, L, D = a.shape
     out = torch.empty(B, H, L, device=a.device, dtype=torch.float32)
-    _lib.call("vsa_row_dot", a, b, blk_cnt, out, B * H, L, D)
+    _lib.call("vsa_row_dot", _wide(a), _wide(b), blk_cnt, out, B * H, L, D)
     return out

@@ -10,7 +10,7 @@ the coarse gradients spread over each block's valid tokens.
 
 Tensor contract (the reference's): q, k, v [B, H, L, D] contiguous bf16, L = NB * 64 in block-major order with
 blk_cnt[i] (int32, 1..64) valid tokens first in block i; padding slots hold finite values, are never pooled, output 0
-and get zero gradient. This build supports D = 128.
+and get zero gradient. D is 64 or 128 (the native ops store rows with 128 columns; D = 64 is zero-padded).
 """
 from __future__ import annotations
 
