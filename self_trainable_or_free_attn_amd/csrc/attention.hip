@@ -23,6 +23,8 @@ namespace es {
 
 enum { FIXED = 0, ONLINE = 1, COMPENSATE = 2 };
 
+
+
 struct AttnArgs {
   const bf16_t* q;
   const bf16_t* k;
@@ -48,17 +50,22 @@ struct AttnArgs {
   float threshold, tail_log2, scale;
 };
 
-// Per-lane prefetched sources of one chunk: the ids of this lane's four load rows and (wave 0) of its bias row.
+// Sources of one chunk for this lane: the ids of its four load rows and (wave 0) of its bias row.
 struct ChunkIds {
   int row[4];  // exact: token block id (uniform); mean: mean block id; rep: rep row h-relative; -1 = padding
   int brow;    // the same for bias row = lane (wave 0)
 };
+
 
 template <int MODE, bool COMP, bool MASS>
 __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char kv_s[2][2][BK * 256];
   __shared__ __attribute__((aligned(16))) float bias_s[2][BK];
   __shared__ float mass_s[4][128];
+  // list entries of chunks j, j+1, j+2 (ring slot j % 3), staged from global memory straight into LDS two chunks
+  // ahead, so the loop holds no global->register or scalar loads whose waits would also drain the K / V loads
+  __shared__ int ids_s[3][64];
+  __shared__ float lc_s[BK];  // log2 counts of the next representative chunk's columns (wave 0, global -> LDS)
 
   // XCD-aware tile order: dispatch slot w runs on XCD w % 8; each XCD walks a contiguous run of tiles of one head
   const int w = blockIdx.x;
@@ -102,16 +109,16 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   // Loads go through buffer resources (32-bit offsets; offsets past the end read as zero). Token tensors and the
   // mean table are row-strided by H * 256 bytes from this head's first row; representatives are contiguous rows.
   const unsigned hstride = (unsigned)H * HD * 2;
-  const rsrc_t rk = make_rsrc(a.k + (size_t)h * HD, (unsigned)(((size_t)L * H - h) * HD * 2));
-  const rsrc_t rv = make_rsrc(a.v + (size_t)h * HD, (unsigned)(((size_t)L * H - h) * HD * 2));
-  rsrc_t rkm = rk, rvm = rv, rkr = rk, rvr = rv;
+  const srd_t rk = make_srd(a.k + (size_t)h * HD, (unsigned)(((size_t)L * H - h) * HD * 2));
+  const srd_t rv = make_srd(a.v + (size_t)h * HD, (unsigned)(((size_t)L * H - h) * HD * 2));
+  srd_t rkm = rk, rvm = rv, rkr = rk, rvr = rv;
   if (COMP || MODE == COMPENSATE) {
-    rkm = make_rsrc(a.k_mean + (size_t)h * HD, (unsigned)(((size_t)nb * H - h) * HD * 2));
-    rvm = make_rsrc(a.v_mean + (size_t)h * HD, (unsigned)(((size_t)nb * H - h) * HD * 2));
+    rkm = make_srd(a.k_mean + (size_t)h * HD, (unsigned)(((size_t)nb * H - h) * HD * 2));
+    rvm = make_srd(a.v_mean + (size_t)h * HD, (unsigned)(((size_t)nb * H - h) * HD * 2));
   }
   if (COMP) {
-    rkr = make_rsrc(a.k_rep + (size_t)h * nb4 * HD, (unsigned)(nb4 * HD * 2));
-    rvr = make_rsrc(a.v_rep + (size_t)h * nb4 * HD, (unsigned)(nb4 * HD * 2));
+    rkr = make_srd(a.k_rep + (size_t)h * nb4 * HD, (unsigned)(nb4 * HD * 2));
+    rvr = make_srd(a.v_rep + (size_t)h * nb4 * HD, (unsigned)(nb4 * HD * 2));
   }
   // this lane's four load rows R_i = 16 wv + 4 i + l / 16 and its swizzled 16-byte chunk within them
   const int rbase = wv * 16 + (l >> 4);
@@ -123,44 +130,68 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
     tok_off[i] = (unsigned)R * hstride + chb[i];
   }
 
-  auto fetch = [&](int cj, ChunkIds& c) {
-    if (cj >= nc || MODE == COMPENSATE) return;
+  // wave 0 stages the list entries chunk cj needs into ids_s[cj % 3]: exact -> its block id (every lane, same
+  // word); mean -> the ids of its 64 columns; rep -> the refined block of each of its 64 columns
+  auto stage_ids = [&](int cj) {
+    if (MODE == COMPENSATE || wv != 0 || cj >= nc || (cj < n && g_ex == nullptr)) return;
+    int* dst = ids_s[cj % 3];
     if (cj < n) {
-      c.row[0] = g_ex == nullptr ? cj : sload(g_ex + cj);
+      dma4(make_srd(g_ex, (unsigned)n * 4u), dst, 0, (unsigned)cj * 4u);
+    } else if (cj < n + cm) {
+      dma4(make_srd(g_me, (unsigned)nm * 4u), dst, (unsigned)((cj - n) * BK + l) * 4u, 0);
+    } else {
+      dma4(make_srd(g_rf, (unsigned)nr * 4u), dst, (unsigned)(((cj - n - cm) * BK + l) >> 2) * 4u, 0);
+    }
+  };
+  // this lane's sources of chunk cj from ids_s (staged before the last barrier)
+  auto read_ids = [&](int cj) -> ChunkIds {
+    ChunkIds c = {};
+    if (MODE == COMPENSATE || cj >= nc) return c;
+    const int* src = ids_s[cj % 3];
+    if (cj < n) {
+      c.row[0] = g_ex == nullptr ? cj : __builtin_amdgcn_readfirstlane(src[0]);
     } else if (cj < n + cm) {
       const int c0 = (cj - n) * BK;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int col = c0 + rbase + 4 * i;
-        c.row[i] = col < nm ? g_me[col] : -1;
-      }
-      c.brow = (wv == 0 && c0 + l < nm) ? g_me[c0 + l] : -1;
+      for (int i = 0; i < 4; ++i) c.row[i] = c0 + rbase + 4 * i < nm ? src[rbase + 4 * i] : -1;
+      c.brow = (wv == 0 && c0 + l < nm) ? src[l] : -1;
     } else {
       const int c0 = (cj - n - cm) * BK;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int col = c0 + rbase + 4 * i;
-        c.row[i] = col < 4 * nr ? g_rf[col >> 2] * 4 + (col & 3) : -1;
+        c.row[i] = col < 4 * nr ? src[rbase + 4 * i] * 4 + (col & 3) : -1;
       }
-      const int col = c0 + l;
-      c.brow = (wv == 0 && col < 4 * nr) ? g_rf[col >> 2] * 4 + (col & 3) : -1;
+      c.brow = (wv == 0 && c0 + l < 4 * nr) ? src[l] * 4 + ((c0 + l) & 3) : -1;
     }
+    return c;
   };
-  // stage chunk cj into buffer sb (16 + 16 one-KB instructions, 4 + 4 per wave); returns wave 0's bias value
-  auto issue = [&](int cj, const ChunkIds& c, int sb) -> float {
-    char* kd = kv_s[sb][0] + wv * 4096;
-    char* vd = kv_s[sb][1] + wv * 4096;
+  // the loads that stage one chunk (16 + 16 one-KB instructions, 4 + 4 per wave): sources and this lane's offsets
+  struct Dma {
+    srd_t rk, rv;
+    unsigned off[4];
+    unsigned soff;
+  };
+  auto dma_k = [&](const Dma& d, int sb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(d.rk, kv_s[sb][0] + wv * 4096 + i * 1024, d.off[i], d.soff);
+  };
+  auto dma_v = [&](const Dma& d, int sb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(d.rv, kv_s[sb][1] + wv * 4096 + i * 1024, d.off[i], d.soff);
+  };
+  // the loads of chunk cj into d; returns wave 0's bias value
+  auto plan = [&](int cj, const ChunkIds& c, Dma& d) -> float {
     float bias = 0.0f;
     if (MODE == COMPENSATE || cj < n) {
       // 64 consecutive rows: token block b (exact) or mean blocks 64 cj .. (compensation)
       const int b0 = MODE == COMPENSATE ? cj * BK : __builtin_amdgcn_readfirstlane(c.row[0]) * BK;
       const unsigned soff = (unsigned)b0 * hstride;
-      const rsrc_t r1 = MODE == COMPENSATE ? rkm : rk, r2 = MODE == COMPENSATE ? rvm : rv;
+      d.rk = MODE == COMPENSATE ? rkm : rk;
+      d.rv = MODE == COMPENSATE ? rvm : rv;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        buf2lds16(r1, kd + i * 1024, tok_off[i], soff);
-        buf2lds16(r2, vd + i * 1024, tok_off[i], soff);
-      }
+      for (int i = 0; i < 4; ++i) d.off[i] = tok_off[i];
+      d.soff = soff;
       if (wv == 0) {
         if (MODE == COMPENSATE) {
           const int b = b0 + l;
@@ -172,19 +203,20 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
       }
     } else {
       const bool mean = cj < n + cm;
-      const rsrc_t r1 = mean ? rkm : rkr, r2 = mean ? rvm : rvr;
+      d.rk = mean ? rkm : rkr;
+      d.rv = mean ? rvm : rvr;
       const unsigned stride = mean ? hstride : (unsigned)HD * 2;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const unsigned off = c.row[i] < 0 ? 0x80000000u : (unsigned)c.row[i] * stride + chb[i];
-        buf2lds16(r1, kd + i * 1024, off, 0);
-        buf2lds16(r2, vd + i * 1024, off, 0);
-      }
+      for (int i = 0; i < 4; ++i) d.off[i] = c.row[i] < 0 ? 0x80000000u : (unsigned)c.row[i] * stride + chb[i];
+      d.soff = 0;
       if (wv == 0) {
-        if (mean)
+        if (mean) {
           bias = c.brow < 0 ? -INFINITY : c.brow == nb - 1 ? a.tail_log2 : 6.0f;
-        else
-          bias = c.brow < 0 ? -INFINITY : a.log_counts[(size_t)h * nb4 + c.brow];
+        } else {
+          // the log2 count goes to lc_s; the bias is read back once this chunk's loads have landed
+          dma4(make_srd(a.log_counts + (size_t)h * nb4, (unsigned)nb4 * 4u), lc_s, c.brow < 0 ? 0x80000000u : (unsigned)c.brow * 4u, 0);
+          bias = -INFINITY;
+        }
       }
     }
     return bias;
@@ -318,29 +350,46 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
     for (int kk = 0; kk < 4; ++kk) pv(vb, kk, pk[kk]);
   };
 
-  ChunkIds cur = {}, nxt = {};
-  fetch(0, cur);
+  stage_ids(0);
+  stage_ids(1);
+  dma_wait();
+  __syncthreads();
+  int cur_row = 0;  // exact block id of the chunk being computed
   if (nc > 0) {
-    const float b0 = issue(0, cur, 0);
-    if (wv == 0) bias_s[0][l] = b0;
+    const ChunkIds c = read_ids(0);
+    cur_row = c.row[0];
+    Dma d;
+    const float b0 = plan(0, c, d);
+    dma_k(d, 0);
+    dma_v(d, 0);
+    dma_wait();
+    if (wv == 0) bias_s[0][l] = (COMP && n + cm == 0 && c.brow >= 0) ? lc_s[l] : b0;
   }
-  fetch(1, nxt);
-  wait_vmem();
+  dma_wait();
   __syncthreads();
 
   for (int j = 0; j < nc; ++j) {
     const int sb = j & 1;
     float bnext = 0.0f;
-    if (j + 1 < nc) bnext = issue(j + 1, nxt, sb ^ 1);
-    ChunkIds nn = {};
-    fetch(j + 2, nn);
-    const bool biased = MODE == COMPENSATE || j >= n || (tail_block && cur.row[0] == nb - 1);
+    int next_row = 0;
+    bool next_lc = false;  // the next chunk's bias comes from lc_s
+    if (j + 1 < nc) {
+      const ChunkIds c = read_ids(j + 1);
+      next_row = c.row[0];
+      next_lc = COMP && j + 1 >= n + cm && c.brow >= 0;
+      Dma dn;
+      bnext = plan(j + 1, c, dn);
+      dma_k(dn, sb ^ 1);
+      dma_v(dn, sb ^ 1);
+    }
+    stage_ids(j + 2);
+    const bool biased = MODE == COMPENSATE || j >= n || (tail_block && cur_row == nb - 1);
     if (!COMP || biased)   // (non-COMP variants: one instantiation keeps them within 256 VGPRs)
       compute(j, sb, std::true_type{});
     else
       compute(j, sb, std::false_type{});
-    if (j + 1 < nc && wv == 0) bias_s[sb ^ 1][l] = bnext;
-    wait_vmem();
+    dma_wait();
+    if (j + 1 < nc && wv == 0) bias_s[sb ^ 1][l] = next_lc ? lc_s[l] : bnext;
     __syncthreads();
     if (MODE == FIXED && MASS && j < n && ((j & 63) == 63 || j == n - 1) && tid < 64) {
       const int idx = (j & ~63) + tid;
@@ -350,8 +399,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
         a.mass[((size_t)h * a.nq + t) * nb + b] = m;
       }
     }
-    cur = nxt;
-    nxt = nn;
+    cur_row = next_row;
   }
 
   // ---------------------------------------------------------------- epilogue

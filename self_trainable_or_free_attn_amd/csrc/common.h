@@ -76,6 +76,56 @@ __device__ __forceinline__ void buf2lds16(rsrc_t r, char* lds_base, unsigned vof
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, LDS_PTR(void, lds_base), 16, (int)voff, (int)soff, 0, 0);
 }
 
+// The same global -> LDS transfer written as inline assembly: the compiler does not see these LDS writes, so it
+// adds no conservative vmcnt waits before LDS reads of the other buffer (it would otherwise drain the prefetch).
+// Visibility is the caller's job: dma_wait() then a barrier before any wave reads what was transferred.
+typedef int srd_t __attribute__((ext_vector_type(4)));
+
+// raw buffer descriptor over `bytes` bytes from `base` (offsets past it read as zero); must be wave-uniform
+__device__ __forceinline__ srd_t make_srd(const void* base, unsigned bytes) {
+  const unsigned long long p = (unsigned long long)base;
+  srd_t r;
+  r.x = (int)(unsigned)p;
+  r.y = (int)(unsigned)((p >> 32) & 0xffffu);
+  r.z = (int)bytes;
+  r.w = 0x00020000;
+  return r;
+}
+
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)(unsigned long long)(const __attribute__((address_space(3))) char*)(p);
+}
+
+// the operands of the asm below must sit in SGPRs: make wave-uniformity explicit (free when already uniform)
+__device__ __forceinline__ unsigned uni(unsigned x) { return (unsigned)__builtin_amdgcn_readfirstlane((int)x); }
+__device__ __forceinline__ srd_t uni(srd_t r) {
+  srd_t o;
+  o.x = __builtin_amdgcn_readfirstlane(r.x);
+  o.y = __builtin_amdgcn_readfirstlane(r.y);
+  o.z = __builtin_amdgcn_readfirstlane(r.z);
+  o.w = __builtin_amdgcn_readfirstlane(r.w);
+  return o;
+}
+
+// every lane moves 16 bytes at srd + voff + soff to lds_base + 16 * lane
+__device__ __forceinline__ void dma16(srd_t r, const void* lds_base, unsigned voff, unsigned soff) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(uni(r)), "s"(uni(soff)), "{m0}"(uni(lds_addr(lds_base)))
+               : "memory");
+}
+
+// every lane moves 4 bytes at srd + voff + soff to lds_base + 4 * lane
+__device__ __forceinline__ void dma4(srd_t r, const void* lds_base, unsigned voff, unsigned soff) {
+  asm volatile("buffer_load_dword %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(uni(r)), "s"(uni(soff)), "{m0}"(uni(lds_addr(lds_base)))
+               : "memory");
+}
+
+// every vector memory operation of this wave (dma16 / dma4 included) has completed; also a compiler memory barrier
+__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // uniform load through the scalar cache (the value must not change during the kernel)
 template <typename T>
 __device__ __forceinline__ T sload(const T* p) {

@@ -72,8 +72,8 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
   const size_t head = (size_t)bh * a.L;
 
   const unsigned head_bytes = (unsigned)((size_t)a.L * HD * 2);
-  const rsrc_t rk = make_rsrc(a.k + head * HD, head_bytes);
-  const rsrc_t rv = make_rsrc(a.v + head * HD, head_bytes);
+  const srd_t rk = make_srd(a.k + head * HD, head_bytes);
+  const srd_t rv = make_srd(a.v + head * HD, head_bytes);
   // this lane's four load rows R = 16 wv + 4 i + l / 16 of a chunk and its swizzled 16-byte chunk in them
   unsigned ld_off[4];
 #pragma unroll
@@ -87,8 +87,8 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
     char* vd = kv_s[sb][1] + wv * 4096;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      buf2lds16(rk, kd + i * 1024, ld_off[i], soff);
-      buf2lds16(rv, vd + i * 1024, ld_off[i], soff);
+      dma16(rk, kd + i * 1024, ld_off[i], soff);
+      dma16(rv, vd + i * 1024, ld_off[i], soff);
     }
   };
 
@@ -121,7 +121,7 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
   int ccur = nc > 0 ? sload(a.blk_cnt + bcur) : 0;
   int bnext = nc > 1 ? sload(a.col_idx + beg + 1) : 0;
   if (nc > 0) issue(bcur, 0);
-  wait_vmem();
+  dma_wait();
   __syncthreads();
 
   for (int j = 0; j < nc; ++j) {
@@ -169,7 +169,7 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
       o[db] = mfma32(cat_tr(lds_read_tr(vb, voff[0][db]), lds_read_tr(vb, voff[1][db])), pa, o[db]);
       o[db] = mfma32(cat_tr(lds_read_tr(vb + 4096, voff[0][db]), lds_read_tr(vb + 4096, voff[1][db])), pb, o[db]);
     }
-    wait_vmem();
+    dma_wait();
     __syncthreads();
     bcur = bnext;
     ccur = cnext;
@@ -305,8 +305,8 @@ __global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
   const size_t head = (size_t)bh * a.L;
 
   const unsigned head_bytes = (unsigned)((size_t)a.L * HD * 2);
-  const rsrc_t rq = make_rsrc(a.q + head * HD, head_bytes);
-  const rsrc_t rd = make_rsrc(a.dout + head * HD, head_bytes);
+  const srd_t rq = make_srd(a.q + head * HD, head_bytes);
+  const srd_t rd = make_srd(a.dout + head * HD, head_bytes);
   unsigned ld_off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -314,9 +314,9 @@ __global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
     ld_off[i] = (unsigned)R * 256 + (unsigned)(((P & 15) ^ swz(R)) * 16);
   }
   {
-    const rsrc_t rv = make_rsrc(a.v + head * HD, head_bytes);
+    const srd_t rv = make_srd(a.v + head * HD, head_bytes);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) buf2lds16(rv, v_s + wv * 4096 + i * 1024, ld_off[i], (unsigned)kb * (BK * 256));
+    for (int i = 0; i < 4; ++i) dma16(rv, v_s + wv * 4096 + i * 1024, ld_off[i], (unsigned)kb * (BK * 256));
   }
   bf16x8 kreg[8];
   {
@@ -329,8 +329,8 @@ __global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
     const unsigned soff = (unsigned)i * (BK * 256);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      buf2lds16(rq, qd_s[sb][0] + wv * 4096 + r * 1024, ld_off[r], soff);
-      buf2lds16(rd, qd_s[sb][1] + wv * 4096 + r * 1024, ld_off[r], soff);
+      dma16(rq, qd_s[sb][0] + wv * 4096 + r * 1024, ld_off[r], soff);
+      dma16(rd, qd_s[sb][1] + wv * 4096 + r * 1024, ld_off[r], soff);
     }
     if (wv == 0) {
       const size_t t = head + (size_t)i * BK + l;
@@ -361,13 +361,13 @@ __global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
   int inext = nc > 1 ? sload(a.col_idx + beg + 1) : 0;
   if (nc > 0) {
     issue(sload(a.col_idx + beg), 0, ls, dl);
-    wait_vmem();
+    dma_wait();
     if (wv == 0) {
       st_s[0][0][l] = ls;
       st_s[0][1][l] = dl;
     }
   }
-  wait_vmem();
+  dma_wait();
   __syncthreads();
   // masked key columns: every row's lse2 becomes +inf for this lane, so P = 2^(s - inf) = 0 without a branch
   const float kmask = kvalid ? 0.0f : INFINITY;
@@ -406,7 +406,7 @@ __global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
       dk[db] = mfma32(cat_tr(lds_read_tr(qt, toff[0][db]), lds_read_tr(qt, toff[1][db])), sa, dk[db]);
       dk[db] = mfma32(cat_tr(lds_read_tr(qt + 4096, toff[0][db]), lds_read_tr(qt + 4096, toff[1][db])), sb8, dk[db]);
     }
-    wait_vmem();
+    dma_wait();
     if (j + 1 < nc && wv == 0) {
       st_s[sb ^ 1][0][l] = ls;
       st_s[sb ^ 1][1][l] = dl;
@@ -506,8 +506,8 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
   const float dl = a.delta[tok];
 
   const unsigned head_bytes = (unsigned)((size_t)a.L * HD * 2);
-  const rsrc_t rk = make_rsrc(a.k + head * HD, head_bytes);
-  const rsrc_t rv = make_rsrc(a.v + head * HD, head_bytes);
+  const srd_t rk = make_srd(a.k + head * HD, head_bytes);
+  const srd_t rv = make_srd(a.v + head * HD, head_bytes);
   unsigned ld_off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -518,8 +518,8 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
     const unsigned soff = (unsigned)b * (BK * 256);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      buf2lds16(rk, kv_s[sb][0] + wv * 4096 + i * 1024, ld_off[i], soff);
-      buf2lds16(rv, kv_s[sb][1] + wv * 4096 + i * 1024, ld_off[i], soff);
+      dma16(rk, kv_s[sb][0] + wv * 4096 + i * 1024, ld_off[i], soff);
+      dma16(rv, kv_s[sb][1] + wv * 4096 + i * 1024, ld_off[i], soff);
     }
   };
   int koff[8];
@@ -542,7 +542,7 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
   int ccur = nc > 0 ? sload(a.blk_cnt + bcur) : 0;
   int bnext = nc > 1 ? sload(a.col_idx + beg + 1) : 0;
   if (nc > 0) issue(bcur, 0);
-  wait_vmem();
+  dma_wait();
   __syncthreads();
   for (int j = 0; j < nc; ++j) {
     const int sb = j & 1;
@@ -572,7 +572,7 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
       dq[db] = mfma32(cat_tr(lds_read_tr(kt, toff[0][db]), lds_read_tr(kt, toff[1][db])), sa, dq[db]);
       dq[db] = mfma32(cat_tr(lds_read_tr(kt + 4096, toff[0][db]), lds_read_tr(kt + 4096, toff[1][db])), sb8, dq[db]);
     }
-    wait_vmem();
+    dma_wait();
     __syncthreads();
     bcur = bnext;
     ccur = cnext;

@@ -138,12 +138,12 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
   const int nc = st.cA + st.cB + st.cC;
 
   const unsigned head_bytes = (unsigned)((size_t)a.L * HD * 2);
-  const rsrc_t rk = make_rsrc(a.k + head * HD, head_bytes);
-  const rsrc_t rv = make_rsrc(a.v + head * HD, head_bytes);
-  const rsrc_t rkm = make_rsrc(a.k_mid + (size_t)bh * a.mid_rows * HD, (unsigned)((size_t)a.mid_rows * HD * 2));
-  const rsrc_t rvm = make_rsrc(a.v_mid + (size_t)bh * a.mid_rows * HD, (unsigned)((size_t)a.mid_rows * HD * 2));
-  const rsrc_t rkt = make_rsrc(a.k_tail + (size_t)bh * a.tail_rows * HD, (unsigned)((size_t)a.tail_rows * HD * 2));
-  const rsrc_t rvt = make_rsrc(a.v_tail + (size_t)bh * a.tail_rows * HD, (unsigned)((size_t)a.tail_rows * HD * 2));
+  const srd_t rk = make_srd(a.k + head * HD, head_bytes);
+  const srd_t rv = make_srd(a.v + head * HD, head_bytes);
+  const srd_t rkm = make_srd(a.k_mid + (size_t)bh * a.mid_rows * HD, (unsigned)((size_t)a.mid_rows * HD * 2));
+  const srd_t rvm = make_srd(a.v_mid + (size_t)bh * a.mid_rows * HD, (unsigned)((size_t)a.mid_rows * HD * 2));
+  const srd_t rkt = make_srd(a.k_tail + (size_t)bh * a.tail_rows * HD, (unsigned)((size_t)a.tail_rows * HD * 2));
+  const srd_t rvt = make_srd(a.v_tail + (size_t)bh * a.tail_rows * HD, (unsigned)((size_t)a.tail_rows * HD * 2));
   unsigned chb[4];
   int lrow[4];
 #pragma unroll
@@ -161,8 +161,8 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
       const unsigned soff = (unsigned)b * (BK * 256);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        buf2lds16(rk, kd + i * 1024, (unsigned)lrow[i] * 256 + chb[i], soff);
-        buf2lds16(rv, vd + i * 1024, (unsigned)lrow[i] * 256 + chb[i], soff);
+        dma16(rk, kd + i * 1024, (unsigned)lrow[i] * 256 + chb[i], soff);
+        dma16(rv, vd + i * 1024, (unsigned)lrow[i] * 256 + chb[i], soff);
       }
       return l < sload(a.blk_cnt + b) ? 0.0f : -INFINITY;
     }
@@ -173,13 +173,13 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
       if (p >= n) return -1;
       return tb ? (int)blist[p / a.RM] * a.RM + p % a.RM : (int)clist[p];
     };
-    const rsrc_t r1 = tb ? rkm : rkt, r2 = tb ? rvm : rvt;
+    const srd_t r1 = tb ? rkm : rkt, r2 = tb ? rvm : rvt;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = table_row(p0 + lrow[i]);
       const unsigned off = row < 0 ? 0x80000000u : (unsigned)row * 256 + chb[i];
-      buf2lds16(r1, kd + i * 1024, off, 0);
-      buf2lds16(r2, vd + i * 1024, off, 0);
+      dma16(r1, kd + i * 1024, off, 0);
+      dma16(r2, vd + i * 1024, off, 0);
     }
     const int row = table_row(p0 + l);
     return row < 0 ? -INFINITY : (tb ? a.lc_mid[row] : a.lc_tail[row]);
@@ -218,7 +218,7 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
     const float b0 = issue(0, 0);
     if (wv == 0) bias_s[0][l] = b0;
   }
-  wait_vmem();
+  dma_wait();
   __syncthreads();
   for (int j = 0; j < nc; ++j) {
     const int sb = j & 1;
@@ -277,7 +277,7 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
       }
     }
     if (j + 1 < nc && wv == 0) bias_s[sb ^ 1][l] = bn;
-    wait_vmem();
+    dma_wait();
     __syncthreads();
   }
 
@@ -376,8 +376,8 @@ __global__ __launch_bounds__(256, 1) void rep_bwd_tab_kernel(TabArgs a) {
   const size_t head = (size_t)bh * a.L;
 
   const unsigned head_bytes = (unsigned)((size_t)a.L * HD * 2);
-  const rsrc_t rq = make_rsrc(a.q + head * HD, head_bytes);
-  const rsrc_t rd = make_rsrc(a.dout + head * HD, head_bytes);
+  const srd_t rq = make_srd(a.q + head * HD, head_bytes);
+  const srd_t rd = make_srd(a.dout + head * HD, head_bytes);
   unsigned ld_off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -385,9 +385,9 @@ __global__ __launch_bounds__(256, 1) void rep_bwd_tab_kernel(TabArgs a) {
     ld_off[i] = (unsigned)R * 256 + (unsigned)(((P & 15) ^ swz(R)) * 16);
   }
   {
-    const rsrc_t rv = make_rsrc(a.v_tab + (size_t)bh * a.rows_pad * HD, (unsigned)((size_t)a.rows_pad * HD * 2));
+    const srd_t rv = make_srd(a.v_tab + (size_t)bh * a.rows_pad * HD, (unsigned)((size_t)a.rows_pad * HD * 2));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) buf2lds16(rv, v_s + wv * 4096 + i * 1024, ld_off[i], (unsigned)grp * (BK * 256));
+    for (int i = 0; i < 4; ++i) dma16(rv, v_s + wv * 4096 + i * 1024, ld_off[i], (unsigned)grp * (BK * 256));
   }
   bf16x8 kreg[8];
   {
@@ -399,8 +399,8 @@ __global__ __launch_bounds__(256, 1) void rep_bwd_tab_kernel(TabArgs a) {
     const unsigned soff = (unsigned)i * (BK * 256);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      buf2lds16(rq, qd_s[sb][0] + wv * 4096 + r * 1024, ld_off[r], soff);
-      buf2lds16(rd, qd_s[sb][1] + wv * 4096 + r * 1024, ld_off[r], soff);
+      dma16(rq, qd_s[sb][0] + wv * 4096 + r * 1024, ld_off[r], soff);
+      dma16(rd, qd_s[sb][1] + wv * 4096 + r * 1024, ld_off[r], soff);
     }
     if (wv == 0) {
       const size_t t = head + (size_t)i * BK + l;
@@ -442,13 +442,13 @@ __global__ __launch_bounds__(256, 1) void rep_bwd_tab_kernel(TabArgs a) {
   int inext = icur < a.NB ? next_active(icur + 1, mnext) : a.NB;
   if (icur < a.NB) {
     issue(icur, 0, ls, dl);
-    wait_vmem();
+    dma_wait();
     if (wv == 0) {
       st_s[0][0][l] = ls;
       st_s[0][1][l] = dl;
     }
   }
-  wait_vmem();
+  dma_wait();
   __syncthreads();
   for (int j = 0; icur < a.NB; ++j) {
     const int sb = j & 1;
@@ -488,7 +488,7 @@ __global__ __launch_bounds__(256, 1) void rep_bwd_tab_kernel(TabArgs a) {
       dk[db] = mfma32(cat_tr(lds_read_tr(qt, toff[0][db]), lds_read_tr(qt, toff[1][db])), sa, dk[db]);
       dk[db] = mfma32(cat_tr(lds_read_tr(qt + 4096, toff[0][db]), lds_read_tr(qt + 4096, toff[1][db])), sb8, dk[db]);
     }
-    wait_vmem();
+    dma_wait();
     if (inext < a.NB && wv == 0) {
       st_s[sb ^ 1][0][l] = ls;
       st_s[sb ^ 1][1][l] = dl;

@@ -483,7 +483,7 @@ __global__ __launch_bounds__(256) void psp_kernel(PspArgs a) {
   const int qrow = qt * 64 + 32 * rg + lq;
   const bool qvalid = group_valid(a, qrow);
   const bf16_t* kbase = a.kr + bh * a.Lr_pad * HD;
-  const rsrc_t rk = make_rsrc(kbase, (unsigned)((size_t)a.Lr_pad * HD * 2));
+  const srd_t rk = make_srd(kbase, (unsigned)((size_t)a.Lr_pad * HD * 2));
   unsigned ld_off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -492,7 +492,7 @@ __global__ __launch_bounds__(256) void psp_kernel(PspArgs a) {
   }
   auto issue = [&](int c, int sb) -> float {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) buf2lds16(rk, k_s[sb] + wv * 4096 + i * 1024, ld_off[i], (unsigned)c * (BK * 256));
+    for (int i = 0; i < 4; ++i) dma16(rk, k_s[sb] + wv * 4096 + i * 1024, ld_off[i], (unsigned)c * (BK * 256));
     return group_valid(a, c * 64 + l) ? 0.0f : -INFINITY;
   };
   bf16x8 qreg[8];
@@ -517,7 +517,7 @@ __global__ __launch_bounds__(256) void psp_kernel(PspArgs a) {
 
   float b0 = issue(0, 0);
   if (wv == 0) bias_s[0][l] = b0;
-  wait_vmem();
+  dma_wait();
   __syncthreads();
   for (int c = 0; c < nchunk; ++c) {
     const int sb = c & 1;
@@ -576,7 +576,7 @@ __global__ __launch_bounds__(256) void psp_kernel(PspArgs a) {
       }
     }
     if (c + 1 < nchunk && wv == 0) bias_s[sb ^ 1][l] = bn;
-    wait_vmem();
+    dma_wait();
     __syncthreads();
   }
   if (!SCORES) {
