@@ -181,25 +181,34 @@ __global__ __launch_bounds__(64) void probe_kernel(const bf16_t* __restrict__ q,
   p[1] = f2bf(b * scale / d);
 }
 
+// kmeans_kernel: one (block, head) per 256-thread workgroup; ~50 KB of LDS so three workgroups share a CU.
+//   LDS region A (33 KB): X (fp32, padded rows), then the K and V tiles for the final means
+//   LDS region B (16.6 KB): the K tile, then the probe logits, then the dot partials / centroids / weights
+// Thread (wave w, lane l) keeps X[l][32 w ..] in registers for the distances; the centroid sums (threads 0..127,
+// channel = tid) read X's columns from LDS.
 template <bool MEANS>
-__global__ __launch_bounds__(256) void kmeans_kernel(const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-                                                     const bf16_t* __restrict__ metric_t,
-                                                     const bf16_t* __restrict__ probes, bf16_t* __restrict__ k4,
-                                                     bf16_t* __restrict__ v4, float* __restrict__ lc4,
-                                                     bf16_t* __restrict__ km, bf16_t* __restrict__ vm, int L, int H,
-                                                     int NB, int iters) {
-  __shared__ __attribute__((aligned(16))) char kt[BK * 256];
-  __shared__ float X[BK][HD + 1];
-  __shared__ __attribute__((aligned(16))) float sp[NPROBE][BK + 1];  // probe logits, then the V tile
+__global__ __launch_bounds__(256, 3) void kmeans_kernel(const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+                                                        const bf16_t* __restrict__ metric_t,
+                                                        const bf16_t* __restrict__ probes, bf16_t* __restrict__ k4,
+                                                        bf16_t* __restrict__ v4, float* __restrict__ lc4,
+                                                        bf16_t* __restrict__ km, bf16_t* __restrict__ vm, int L,
+                                                        int H, int NB, int iters) {
+  __shared__ __attribute__((aligned(16))) float regA[BK * (HD + 1)];
+  __shared__ __attribute__((aligned(16))) float regB[NPROBE * (BK + 1)];
   __shared__ float wpart[4][BK];
   __shared__ float wgt[BK];
-  __shared__ float cen[4][HD];
-  __shared__ float cw[4];
-  __shared__ float part[4][BK][9];
-  char* vt = reinterpret_cast<char*>(&sp[0][0]);
   __shared__ int lab[BK];
-  __shared__ int red_i[4];
-  __shared__ float cnt_s[4];
+  __shared__ float cw[4];
+  __shared__ float nnp[2][4];
+  __shared__ int red_i[1];
+  float(*X)[HD + 1] = reinterpret_cast<float(*)[HD + 1]>(regA);
+  char* kt2 = reinterpret_cast<char*>(regA);  // K tile for the means (after the clustering)
+  char* vt2 = kt2 + BK * 256;                 // V tile for the means
+  char* kt = reinterpret_cast<char*>(regB);   // K tile for X and the probe logits
+  float(*sp)[BK + 1] = reinterpret_cast<float(*)[BK + 1]>(regB);
+  f32x4* part = reinterpret_cast<f32x4*>(regB);            // [4 waves][BK] partial dots
+  f32x4* cen = reinterpret_cast<f32x4*>(regB) + 4 * BK;    // [HD] centroids, (channel, cluster)
+  f32x4* aw = reinterpret_cast<f32x4*>(regB) + 4 * BK + HD;  // [BK] token weight per cluster
 
   const int j = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, hi = l >> 5, lq = l & 31;
@@ -208,10 +217,11 @@ __global__ __launch_bounds__(256) void kmeans_kernel(const bf16_t* __restrict__ 
   wait_vmem();
   __syncthreads();
 
-  // X = K Lchol: wave wv -> tokens 32 (wv & 1) .., channels 64 (wv >> 1) .. (two 32-wide C tiles)
+  // X = K Lchol: wave wv -> tokens 32 (wv & 1) .., channels 64 (wv >> 1) .. (two 32-wide C tiles); probe logits:
+  // wave wv -> probes 32 (wv & 1) .., tokens 32 (wv >> 1) ..
+  f32x16 ax[2] = {f32x16{}, f32x16{}}, ap = {};
   {
     const int tb = wv & 1, e0 = (wv >> 1) * 2;
-    f32x16 acc[2] = {f32x16{}, f32x16{}};
     const bf16_t* mt = metric_t + (size_t)h * HD * HD;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
@@ -219,29 +229,33 @@ __global__ __launch_bounds__(256) void kmeans_kernel(const bf16_t* __restrict__ 
 #pragma unroll
       for (int eb = 0; eb < 2; ++eb) {
         const bf16x8 b = *reinterpret_cast<const bf16x8*>(mt + (size_t)(32 * (e0 + eb) + lq) * HD + 16 * ks + 8 * hi);
-        acc[eb] = mfma32(a, b, acc[eb]);
+        ax[eb] = mfma32(a, b, ax[eb]);
       }
     }
-#pragma unroll
-    for (int eb = 0; eb < 2; ++eb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) X[32 * tb + 8 * (r / 4) + 4 * hi + (r % 4)][32 * (e0 + eb) + lq] = acc[eb][r];
-  }
-  // probe logits: wave wv -> probes 32 (wv & 1) .., tokens 32 (wv >> 1) ..
-  {
-    const int pb = wv & 1, tb = wv >> 1;
-    f32x16 acc = {};
+    const int pb = wv & 1, tk = wv >> 1;
     const bf16_t* pr = probes + ((size_t)h * NPROBE + 32 * pb + lq) * HD;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
       const bf16x8 a = *reinterpret_cast<const bf16x8*>(pr + 16 * ks + 8 * hi);
-      const bf16x8 b = lds_read16(kt, tile_off(32 * tb + lq, 2 * ks + hi));
-      acc = mfma32(a, b, acc);
+      const bf16x8 b = lds_read16(kt, tile_off(32 * tk + lq, 2 * ks + hi));
+      ap = mfma32(a, b, ap);
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sp[32 * pb + 8 * (r / 4) + 4 * hi + (r % 4)][32 * tb + lq] = acc[r];
+    for (int eb = 0; eb < 2; ++eb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) X[32 * tb + 8 * (r / 4) + 4 * hi + (r % 4)][32 * (e0 + eb) + lq] = ax[eb][r];
+  }
+  __syncthreads();  // every wave is done with the K tile: region B takes the probe logits
+  {
+    const int pb = wv & 1, tk = wv >> 1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sp[32 * pb + 8 * (r / 4) + 4 * hi + (r % 4)][32 * tk + lq] = ap[r];
   }
   __syncthreads();
+
+  float xd[32];  // X[l][32 wv + i]
+#pragma unroll
+  for (int i = 0; i < 32; ++i) xd[i] = X[l][32 * wv + i];
   // probe softmax weights: wave wv takes probes 16 wv .. 16 wv + 15, lane = token
   {
     const bool tv = l < nvalid;
@@ -254,84 +268,99 @@ __global__ __launch_bounds__(256) void kmeans_kernel(const bf16_t* __restrict__ 
     }
     wpart[wv][l] = wpart_l;
   }
-  __syncthreads();
-  stage_rows(v, j * BK, L, H, h, vt);  // the V tile lands while the clustering runs
-  if (tid < BK) {
-    const float s = wpart[0][tid] + wpart[1][tid] + wpart[2][tid] + wpart[3][tid];
-    wgt[tid] = tid < nvalid ? s * ((float)nvalid / (float)NPROBE) : 0.0f;
-    lab[tid] = tid / (BK / 4);
+  __syncthreads();  // the probe logits are consumed: region B is free
+  // token weights, the initial labels (four contiguous 16-token groups), per-cluster weights
+  auto set_weights = [&](int lb) {  // wave 0, lane = token: aw and cw of the labels lb
+    const float w = wgt[l];
+    f32x4 a4;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) a4[c] = lb == c ? w : 0.0f;
+    aw[l] = a4;
+    lab[l] = lb;
+    float s[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s[c] = wave_sum_dpp(a4[c]);
+    if (l == 0) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) cw[c] = s[c];
+    }
+  };
+  if (wv == 0) {
+    const float s = wpart[0][l] + wpart[1][l] + wpart[2][l] + wpart[3][l];
+    wgt[l] = l < nvalid ? s * ((float)nvalid / (float)NPROBE) : 0.0f;
+    set_weights(l / (BK / 4));
   }
   __syncthreads();
 
-  // weighted centroids of the current labels: thread -> channel tid % 128, clusters 2 (tid / 128) + {0, 1};
-  // a cluster with zero weight keeps its previous centroid unless `init`
+  // weighted centroids of the current labels (threads 0..127, channel = tid); a cluster with zero weight keeps
+  // its previous centroid unless `init`; also the squared centroid norms (per wave, nnp)
   auto centroids = [&](bool init) {
-    const int e = tid & (HD - 1), c0 = 2 * (tid >> 7);
-    float s0 = 0.f, s1 = 0.f, w0 = 0.f, w1 = 0.f;
-#pragma unroll 4
-    for (int t = 0; t < nvalid; ++t) {
-      const int lb = lab[t];
-      const float w = wgt[t], x = X[t][e];
-      const float a0 = lb == c0 ? w : 0.0f, a1 = lb == c0 + 1 ? w : 0.0f;
-      w0 += a0;
-      w1 += a1;
-      s0 = fmaf(a0, x, s0);
-      s1 = fmaf(a1, x, s1);
+    if (tid >= HD) return;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int t = 0; t < BK; ++t) {
+      const f32x4 a4 = aw[t];
+      const float x = X[t][tid];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) s[c] = fmaf(a4[c], x, s[c]);
     }
-    __syncthreads();
-    if (init || w0 > 0.0f) cen[c0][e] = s0 / fmaxf(w0, 1e-6f);
-    if (init || w1 > 0.0f) cen[c0 + 1][e] = s1 / fmaxf(w1, 1e-6f);
-    if (e == 0) {
-      cw[c0] = w0;
-      cw[c0 + 1] = w1;
+    f32x4 c4 = init ? f32x4{} : cen[tid];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float w = cw[c];
+      if (init || w > 0.0f) c4[c] = s[c] / fmaxf(w, 1e-6f);
     }
-    __syncthreads();
+    cen[tid] = c4;
+    float q[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) q[c] = wave_sum_dpp(c4[c] * c4[c]);
+    if (l == 0) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) nnp[wv][c] = q[c];
+    }
   };
   centroids(true);
+  __syncthreads();
   for (int it = 0; it < iters; ++it) {
     {  // partial dots over channels 32 wv .. 32 wv + 31 for token l
-      float d[4] = {0.f, 0.f, 0.f, 0.f}, nn[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-      for (int e = 32 * wv; e < 32 * wv + 32; ++e) {
-        const float x = X[l][e];
+      float d[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const float z = cen[c][e];
-          d[c] = fmaf(x, z, d[c]);
-          nn[c] = fmaf(z, z, nn[c]);
-        }
-      }
+      for (int i = 0; i < 32; ++i) {
+        const f32x4 c4 = cen[32 * wv + i];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        part[wv][l][c] = d[c];
-        part[wv][l][4 + c] = nn[c];
+        for (int c = 0; c < 4; ++c) d[c] = fmaf(xd[i], c4[c], d[c]);
       }
+      part[wv * BK + l] = f32x4{d[0], d[1], d[2], d[3]};
     }
     __syncthreads();
-    if (tid < BK) {
+    if (wv == 0) {
+      const f32x4 p0 = part[l], p1 = part[BK + l], p2 = part[2 * BK + l], p3 = part[3 * BK + l];
       int best = 0;
       float bd = INFINITY;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const float xc = part[0][tid][c] + part[1][tid][c] + part[2][tid][c] + part[3][tid][c];
-        const float cc = part[0][tid][4 + c] + part[1][tid][4 + c] + part[2][tid][4 + c] + part[3][tid][4 + c];
-        const float dc = cw[c] > 0.0f ? cc - 2.0f * xc : INFINITY;
+        const float xcd = p0[c] + p1[c] + p2[c] + p3[c];
+        const float nn = nnp[0][c] + nnp[1][c];
+        const float dc = cw[c] > 0.0f ? nn - 2.0f * xcd : INFINITY;
         if (c == 0 || dc < bd) {  // first minimum, like argmin
           bd = dc;
           best = c;
         }
       }
-      const int changed = wave_sum_i((tid < nvalid) && best != lab[tid]);
-      lab[tid] = best;
-      if (tid == 0) red_i[0] = changed;
+      const int changed = wave_sum_i((l < nvalid) && best != lab[l]);
+      set_weights(best);
+      if (l == 0) red_i[0] = changed;
     }
     __syncthreads();
     const int total = red_i[0];
     centroids(false);
+    __syncthreads();
     if (total == 0) break;
   }
 
-  // representatives: plain means of K and V over each cluster's valid tokens (both tiles in LDS)
+  // representatives: plain means of K and V over each cluster's valid tokens (both tiles in LDS, region A)
+  stage_rows(k, j * BK, L, H, h, kt2);
+  stage_rows(v, j * BK, L, H, h, vt2);
   wait_vmem();
   __syncthreads();
   {
@@ -341,8 +370,8 @@ __global__ __launch_bounds__(256) void kmeans_kernel(const bf16_t* __restrict__ 
 #pragma unroll 4
     for (int t = 0; t < nvalid; ++t) {
       const int off = tile_off(t, e / 8) + (e % 8) * 2;
-      const unsigned kw = *reinterpret_cast<const unsigned*>(kt + off);
-      const unsigned vw = *reinterpret_cast<const unsigned*>(vt + off);
+      const unsigned kw = *reinterpret_cast<const unsigned*>(kt2 + off);
+      const unsigned vw = *reinterpret_cast<const unsigned*>(vt2 + off);
       const float m = lab[t] == c ? 1.0f : 0.0f;
       n += lab[t] == c;
       k0 = fmaf(m, __uint_as_float(kw << 16), k0);
@@ -359,7 +388,7 @@ __global__ __launch_bounds__(256) void kmeans_kernel(const bf16_t* __restrict__ 
     if ((tid & 63) == 0) lc4[(size_t)h * (NB + 1) * 4 + (size_t)j * 4 + c] = n > 0 ? log2f((float)n) : -INFINITY;
   }
   if (MEANS && tid < 128) {  // block means: the same sequential fp32 sum and division as means_kernel
-    const char* src = tid < 64 ? kt : vt;
+    const char* src = tid < 64 ? kt2 : vt2;
     bf16_t* dst = tid < 64 ? km : vm;
     const int e = 2 * (tid & 63);
     float a = 0.f, b = 0.f;
