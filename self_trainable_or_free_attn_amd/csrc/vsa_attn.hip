@@ -117,20 +117,19 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
   float lsum = 0.0f, mref = -INFINITY;
   const float scale = a.scale;
 
-  int bcur = nc > 0 ? sload(a.col_idx + beg) : 0;
-  int ccur = nc > 0 ? sload(a.blk_cnt + bcur) : 0;
-  int bnext = nc > 1 ? sload(a.col_idx + beg + 1) : 0;
-  if (nc > 0) issue(bcur, 0);
+  ListWindow lw;
+  lw.init(a.col_idx + beg, a.blk_cnt, nc);
+  int ccur = nc > 0 ? lw.count(0) : 0;
+  if (nc > 0) issue(lw.id(0), 0);
   dma_wait();
   __syncthreads();
 
   for (int j = 0; j < nc; ++j) {
     const int sb = j & 1;
-    int cnext = 0, bnn = 0;
+    int cnext = 0;
     if (j + 1 < nc) {
-      issue(bnext, sb ^ 1);
-      cnext = sload(a.blk_cnt + bnext);
-      if (j + 2 < nc) bnn = sload(a.col_idx + beg + j + 2);
+      issue(lw.id(j + 1), sb ^ 1);
+      cnext = lw.count(j + 1);
     }
     const char* kb = kv_s[sb][0];
     const char* vb = kv_s[sb][1] + kh * 8192;
@@ -171,9 +170,8 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
     }
     dma_wait();
     __syncthreads();
-    bcur = bnext;
     ccur = cnext;
-    bnext = bnn;
+    lw.retire(j);
   }
 
   // merge the two key halves of each row group: kh = 1 waves hand (m, l, O) to the kh = 0 waves through LDS
@@ -358,9 +356,10 @@ __global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
   for (int db = 0; db < 4; ++db) dk[db] = dv[db] = f32x16{};
 
   float ls = 0.0f, dl = 0.0f;
-  int inext = nc > 1 ? sload(a.col_idx + beg + 1) : 0;
+  ListWindow lw;
+  lw.init(a.col_idx + beg, nullptr, nc);
   if (nc > 0) {
-    issue(sload(a.col_idx + beg), 0, ls, dl);
+    issue(lw.id(0), 0, ls, dl);
     dma_wait();
     if (wv == 0) {
       st_s[0][0][l] = ls;
@@ -373,11 +372,7 @@ __global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
   const float kmask = kvalid ? 0.0f : INFINITY;
   for (int j = 0; j < nc; ++j) {
     const int sb = j & 1;
-    int inn = 0;
-    if (j + 1 < nc) {
-      issue(inext, sb ^ 1, ls, dl);
-      if (j + 2 < nc) inn = sload(a.col_idx + beg + j + 2);
-    }
+    if (j + 1 < nc) issue(lw.id(j + 1), sb ^ 1, ls, dl);
     const char* qt = qd_s[sb][0];
     const char* dt = qd_s[sb][1];
     f32x16 s = {}, dp = {};
@@ -412,7 +407,7 @@ __global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
       st_s[sb ^ 1][1][l] = dl;
     }
     __syncthreads();
-    inext = inn;
+    lw.retire(j);
   }
 
   // sum the query-half partials: qh = 1 waves hand theirs to the qh = 0 waves of the same key half
@@ -538,19 +533,18 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
 #pragma unroll
   for (int db = 0; db < 4; ++db) dq[db] = f32x16{};
 
-  int bcur = nc > 0 ? sload(a.col_idx + beg) : 0;
-  int ccur = nc > 0 ? sload(a.blk_cnt + bcur) : 0;
-  int bnext = nc > 1 ? sload(a.col_idx + beg + 1) : 0;
-  if (nc > 0) issue(bcur, 0);
+  ListWindow lw;
+  lw.init(a.col_idx + beg, a.blk_cnt, nc);
+  int ccur = nc > 0 ? lw.count(0) : 0;
+  if (nc > 0) issue(lw.id(0), 0);
   dma_wait();
   __syncthreads();
   for (int j = 0; j < nc; ++j) {
     const int sb = j & 1;
-    int cnext = 0, bnn = 0;
+    int cnext = 0;
     if (j + 1 < nc) {
-      issue(bnext, sb ^ 1);
-      cnext = sload(a.blk_cnt + bnext);
-      if (j + 2 < nc) bnn = sload(a.col_idx + beg + j + 2);
+      issue(lw.id(j + 1), sb ^ 1);
+      cnext = lw.count(j + 1);
     }
     const char* kt = kv_s[sb][0];
     const char* vt = kv_s[sb][1];
@@ -574,9 +568,8 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
     }
     dma_wait();
     __syncthreads();
-    bcur = bnext;
     ccur = cnext;
-    bnext = bnn;
+    lw.retire(j);
   }
 
   float* xq = reinterpret_cast<float*>(&kv_s[0][0][0]) + rg * (64 * 64);
