@@ -136,31 +136,38 @@ __global__ __launch_bounds__(256) void chol_kernel(const float* __restrict__ gra
   __syncthreads();
   const float eps = (red[0] + red[1]) / (float)HD * 1e-12f;
   bf16_t* mt = metric_t + (size_t)h * HD * HD;
-  // Register-resident right-looking factorisation: thread (cc = tid % 128, r0 = tid / 128) holds column cc at
-  // rows r0, r0 + 2, ... Each step the owners of column j publish it, everyone reads the pivot and subtracts the
-  // rank-1 update from its own entries.
-  const int cc = tid & (HD - 1), r0 = tid >> 7;
-  float a[HD / 2];
+  // Register-resident right-looking factorisation: thread (cc = tid % 128, half = tid / 128) holds column cc at
+  // rows 64 half .. 64 half + 63. Step j: the owners of column j publish it into column buffer j % 2 (16-byte
+  // LDS writes), one barrier, then every thread reads the pivot column with 16-byte broadcast reads and subtracts
+  // the rank-1 update from its own entries. (Two buffers: step j+1 writes the other one while step j's readers
+  // may still be reading.)
+  const int cc = tid & (HD - 1), rb = 64 * (tid >> 7);
+  float a[64];
 #pragma unroll
-  for (int i = 0; i < HD / 2; ++i) a[i] = A[r0 + 2 * i][cc];
+  for (int i = 0; i < 64; ++i) a[i] = A[rb + i][cc];
   __syncthreads();
-  float* colbuf = &A[0][0];  // the matrix now lives in registers; reuse the LDS as the column buffer
+  float* colbuf = &A[0][0];  // the matrix now lives in registers; reuse the LDS as two column buffers
   for (int j = 0; j < HD; ++j) {
+    float* cb = colbuf + (j & 1) * HD;
     if (cc == j) {
 #pragma unroll
-      for (int i = 0; i < HD / 2; ++i) colbuf[r0 + 2 * i] = a[i];
+      for (int q4 = 0; q4 < 16; ++q4)
+        *reinterpret_cast<f32x4*>(cb + rb + 4 * q4) = f32x4{a[4 * q4], a[4 * q4 + 1], a[4 * q4 + 2], a[4 * q4 + 3]};
     }
     __syncthreads();
-    const float inv = 1.0f / sqrtf(fmaxf(colbuf[j], eps));
-    const float cv = cc >= j ? colbuf[cc] * inv : 0.0f;
-    if (tid < HD) mt[j * HD + tid] = f2bf(tid >= j ? colbuf[tid] * inv : 0.0f);  // metric_t[j][d] = Lchol[d][j]
+    const float inv = 1.0f / sqrtf(fmaxf(cb[j], eps));
+    const float cv = cc >= j ? cb[cc] * inv : 0.0f;
+    if (tid < HD) mt[j * HD + tid] = f2bf(tid >= j ? cb[tid] * inv : 0.0f);  // metric_t[j][d] = Lchol[d][j]
 #pragma unroll
-    for (int i = 0; i < HD / 2; ++i) {
-      const int r = r0 + 2 * i;
-      const float cr = r >= j ? colbuf[r] * inv : 0.0f;
-      a[i] = fmaf(-cr, cv, a[i]);
+    for (int q4 = 0; q4 < 16; ++q4) {
+      const f32x4 c4 = *reinterpret_cast<const f32x4*>(cb + rb + 4 * q4);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int r = rb + 4 * q4 + k;
+        const float cr = r >= j ? c4[k] * inv : 0.0f;
+        a[4 * q4 + k] = fmaf(-cr, cv, a[4 * q4 + k]);
+      }
     }
-    __syncthreads();
   }
 }
 
