@@ -80,16 +80,27 @@ __global__ __launch_bounds__(256) void estimate_kernel(const bf16_t* __restrict_
 
   float num[4] = {0.f, 0.f, 0.f, 0.f}, den[4] = {0.f, 0.f, 0.f, 0.f};
   const int nchunks = (NB + 31) / 32;
+  // B operands (the chunk's 32 block means) are fetched one chunk ahead of the MFMAs that use them
+  auto load_b = [&](int c, bf16x8 (&b)[8]) {
+    const int key = c * 32 + lq;
+    const bf16_t* kr = km + ((size_t)(key < NB ? key : 0) * H + h) * HD;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) b[ks] = *reinterpret_cast<const bf16x8*>(kr + 16 * ks + 8 * hi);
+  };
+  bf16x8 bn[8];
+  if (wv < nchunks) load_b(wv, bn);
   for (int c = wv; c < nchunks; c += 4) {
     const int key = c * 32 + lq;
     const bool kvalid = key < NB;
-    const bf16_t* kr = km + ((size_t)(kvalid ? key : 0) * H + h) * HD;
+    bf16x8 bc[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) bc[ks] = bn[ks];
+    if (c + 4 < nchunks) load_b(c + 4, bn);
     f32x16 acc[2] = {f32x16{}, f32x16{}};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-      const bf16x8 b = *reinterpret_cast<const bf16x8*>(kr + 16 * ks + 8 * hi);
-      acc[0] = mfma32(qa[0][ks], b, acc[0]);
-      acc[1] = mfma32(qa[1][ks], b, acc[1]);
+      acc[0] = mfma32(qa[0][ks], bc[ks], acc[0]);
+      acc[1] = mfma32(qa[1][ks], bc[ks], acc[1]);
     }
     const float lb = key == NB - 1 ? lb_last : 6.0f;
     float est[4] = {0.f, 0.f, 0.f, 0.f};

@@ -16,14 +16,6 @@ namespace es {
 constexpr int SEL_THREADS = 256;
 constexpr int SEL_MAXE = 16;  // elements per thread: next_pow2(nb) <= 4096
 
-__device__ __forceinline__ int block_count(int local, int* red, int parity) {
-  const int wv = threadIdx.x >> 6;
-  int s = wave_sum_i(local);
-  if ((threadIdx.x & 63) == 0) red[parity * 4 + wv] = s;
-  __syncthreads();
-  return red[parity * 4 + 0] + red[parity * 4 + 1] + red[parity * 4 + 2] + red[parity * 4 + 3];
-}
-
 // exclusive prefix over the workgroup of one int per thread; returns (prefix, total)
 __device__ __forceinline__ int2 block_scan(int x, int* scan_s) {
   const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -46,17 +38,42 @@ __device__ __forceinline__ int2 block_scan(int x, int* scan_s) {
   return make_int2(before + inc - x, total);
 }
 
+// The reference's 31-step bisection, two steps per workgroup exchange: one round counts at the midpoint m of
+// [lo, hi) and at the midpoints of both halves, then takes the step at m and the step the original would take
+// next. Wave counts are popcounts of ballots (no cross-lane arithmetic); 16 rounds = 32 steps, and a step on a
+// converged interval (hi - lo <= 1) leaves lo as it is, so the result equals the 31-step search.
 template <int E>
 __device__ int kth_largest(const int (&bits)[E], int K, int* red, int& parity) {
+  const int wv = threadIdx.x >> 6;
   int lo = 0, hi = 0x7F800001;
-  for (int it = 0; it < 31; ++it) {
-    const int mid = lo + (hi - lo) / 2;
-    int c = 0;
+  for (int it = 0; it < 16; ++it) {
+    const int m = lo + (hi - lo) / 2;
+    const int ml = lo + (m - lo) / 2, mh = m + (hi - m) / 2;
+    int c[3] = {0, 0, 0};
 #pragma unroll
-    for (int e = 0; e < E; ++e) c += bits[e] >= mid;
-    const int cnt = block_count(c, red, parity);
+    for (int e = 0; e < E; ++e) {
+      c[0] += __builtin_popcountll(__builtin_amdgcn_ballot_w64(bits[e] >= ml));
+      c[1] += __builtin_popcountll(__builtin_amdgcn_ballot_w64(bits[e] >= m));
+      c[2] += __builtin_popcountll(__builtin_amdgcn_ballot_w64(bits[e] >= mh));
+    }
+    int* r = red + parity * 12;
+    if ((threadIdx.x & 63) == 0) {
+      r[wv * 3 + 0] = c[0];
+      r[wv * 3 + 1] = c[1];
+      r[wv * 3 + 2] = c[2];
+    }
+    __syncthreads();
+    int t[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) t[k] = r[k] + r[3 + k] + r[6 + k] + r[9 + k];
     parity ^= 1;
-    if (cnt >= K) lo = mid; else hi = mid;
+    if (t[1] >= K) {
+      lo = m;
+      if (t[2] >= K) lo = mh; else hi = mh;
+    } else {
+      hi = m;
+      if (t[0] >= K) lo = ml; else hi = ml;
+    }
   }
   return lo;
 }
@@ -71,7 +88,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(const float* __rest
                                                               int* __restrict__ bits_out, int nw, int* __restrict__ ridx,
                                                               int rw, int K, int R, int NB, int L, int H, int nq,
                                                               int sink, int nwords) {
-  __shared__ int red[8];
+  __shared__ int red[24];
   __shared__ int scan_s[4];
   const int t = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x;
