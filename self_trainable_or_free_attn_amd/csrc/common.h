@@ -126,46 +126,6 @@ __device__ __forceinline__ void dma4(srd_t r, const void* lds_base, unsigned vof
 // every vector memory operation of this wave (dma16 / dma4 included) has completed; also a compiler memory barrier
 __device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// The entries e = 0 .. n-1 of a list (list[e], and cnt[list[e]] when cnt is given) read 64 at a time into VGPRs
-// (lane i holds entry 64 w + i of window w) and handed out with v_readlane. A loop over the list then holds no
-// scalar loads, whose lgkmcnt wait would also drain the LDS reads in flight. Windows w and w + 1 are resident;
-// the one after is fetched when the loop moves past window w.
-struct ListWindow {
-  const int* list;
-  const int* cnt;
-  int n, w;
-  int id0, c0, id1, c1;  // windows w and w + 1
-  __device__ __forceinline__ void fetch(int win, int& id, int& c) const {
-    const int e = 64 * win + (int)(threadIdx.x & 63);
-    id = e < n ? list[e] : 0;
-    c = (cnt != nullptr && e < n) ? cnt[id] : 0;
-  }
-  __device__ __forceinline__ void init(const int* list_, const int* cnt_, int n_) {
-    list = list_;
-    cnt = cnt_;
-    n = n_;
-    w = 0;
-    fetch(0, id0, c0);
-    fetch(1, id1, c1);
-  }
-  // entry e of window w or w + 1 (wave-uniform)
-  __device__ __forceinline__ int id(int e) const {
-    return __builtin_amdgcn_readlane((e >> 6) == w ? id0 : id1, e & 63);
-  }
-  __device__ __forceinline__ int count(int e) const {
-    return __builtin_amdgcn_readlane((e >> 6) == w ? c0 : c1, e & 63);
-  }
-  // entry e is done with: past the end of window w, shift and fetch window w + 2
-  __device__ __forceinline__ void retire(int e) {
-    if ((e & 63) == 63) {
-      id0 = id1;
-      c0 = c1;
-      ++w;
-      fetch(w + 1, id1, c1);
-    }
-  }
-};
-
 // uniform load through the scalar cache (the value must not change during the kernel)
 template <typename T>
 __device__ __forceinline__ T sload(const T* p) {
