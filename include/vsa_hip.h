@@ -3,10 +3,13 @@
  * Conventions as in echosparse_hip.h: caller-owned device pointers, plain sizes, the HIP stream last, no
  * allocation and no synchronisation inside, an es_status return and es_last_error_string() on failure.
  * Layouts (row-major):
- *   tokens q, k, v, o, gate, dO      [BH, L, D] bf16, L = NB * 64, valid-first 64-token blocks, D = 128
+ *   tokens q, k, v, o, gate, dO      [BH, L, 128] bf16, L = NB * 64, valid-first 64-token blocks
+ *   D (every entry point)            the logical head dim, 64 or 128: rows are always 128 columns wide and a
+ *                                    D = 64 caller zero-fills columns 64..127 (they add exact zeros to every dot
+ *                                    product and come out zero); D sets the softmax scale 1 / sqrt(D)
  *   blk_cnt                          [NB] int32, valid tokens per block (1..64)
- *   router pools qr, kr, vr          [BH, Lr_pad, D] bf16, Lr_pad = ceil64(NB * 64 / R)
- *   block means qc, kc, vc           [BH, NBc_pad, D] bf16, NBc_pad = ceil64(NB)
+ *   router pools qr, kr, vr          [BH, Lr_pad, 128] bf16, Lr_pad = ceil64(NB * 64 / R)
+ *   block means qc, kc, vc           [BH, NBc_pad, 128] bf16, NBc_pad = ceil64(NB)
  *   lse                              [BH, L] float32, natural log; -inf on rows with nothing to attend
  *   CSR selection                    ptr [BH, NB + 1] int32 absolute offsets into idx [nnz] int32;
  *                                    q2k rows list kv blocks ascending, k2q columns list query blocks ascending
