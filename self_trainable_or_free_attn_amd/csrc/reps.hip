@@ -203,6 +203,7 @@ __global__ __launch_bounds__(256, 3) void kmeans_kernel(const bf16_t* __restrict
   __shared__ __attribute__((aligned(16))) float regA[BK * (HD + 1)];
   __shared__ __attribute__((aligned(16))) float regB[NPROBE * (BK + 1)];
   __shared__ float wpart[4][BK];
+  __shared__ float pmax[NPROBE], pinv[NPROBE];
   __shared__ float wgt[BK];
   __shared__ int lab[BK];
   __shared__ float cw[4];
@@ -263,17 +264,40 @@ __global__ __launch_bounds__(256, 3) void kmeans_kernel(const bf16_t* __restrict
   float xd[32];  // X[l][32 wv + i]
 #pragma unroll
   for (int i = 0; i < 32; ++i) xd[i] = X[l][32 * wv + i];
-  // probe softmax weights: wave wv takes probes 16 wv .. 16 wv + 15, lane = token
+  // probe softmax weights w_t = sum_p softmax_p(t). (a) thread (probe tid % 64, token quarter tid / 64): row max
+  // and row sum over its 16 tokens, combined through LDS; (b) wave wv, lane = token: its 16 probes. Plain loops
+  // and LDS instead of one cross-lane reduction per probe.
   {
-    const bool tv = l < nvalid;
-    float wpart_l = 0.0f;
-    for (int p = 16 * wv; p < 16 * wv + 16; ++p) {
-      const float x = tv ? sp[p][l] : -INFINITY;
-      const float m = wave_max_dpp(x);
-      const float e = tv ? exp2f_fast((x - m) * LOG2E) : 0.0f;
-      wpart_l += e / wave_sum_dpp(e);
+    const int pp = tid & 63, q4 = tid >> 6;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int tk = 16 * q4 + i;
+      mx = fmaxf(mx, tk < nvalid ? sp[pp][tk] : -INFINITY);
     }
-    wpart[wv][l] = wpart_l;
+    wpart[q4][pp] = mx;
+    __syncthreads();
+    const float m = fmaxf(fmaxf(wpart[0][pp], wpart[1][pp]), fmaxf(wpart[2][pp], wpart[3][pp]));
+    float sm = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int tk = 16 * q4 + i;
+      sm += tk < nvalid ? exp2f_fast((sp[pp][tk] - m) * LOG2E) : 0.0f;
+    }
+    __syncthreads();  // the maxima are read
+    wpart[q4][pp] = sm;
+    __syncthreads();
+    if (tid < NPROBE) {
+      pmax[tid] = m;
+      pinv[tid] = 1.0f / (wpart[0][tid] + wpart[1][tid] + wpart[2][tid] + wpart[3][tid]);
+    }
+    __syncthreads();
+    float wsum = 0.0f;
+    if (l < nvalid) {
+#pragma unroll 4
+      for (int p = 16 * wv; p < 16 * wv + 16; ++p) wsum = fmaf(exp2f_fast((sp[p][l] - pmax[p]) * LOG2E), pinv[p], wsum);
+    }
+    wpart[wv][l] = wsum;  // (every read of wpart above precedes the last barrier)
   }
   __syncthreads();  // the probe logits are consumed: region B is free
   // token weights, the initial labels (four contiguous 16-token groups), per-cluster weights
