@@ -336,3 +336,42 @@ def test_fallback_and_compensation(data, plan, reps, dev):
     ref.compensate_fallback(f32(data["q"]), f32(km), f32(vm), p["lists"][0], rl, ro, fl)
     check_close("compensated O", f32(out), ro)
     check_close("compensated LSE", f32(lse)[:L], rl[:L])
+
+
+def test_sparse_attention_stream_edges(data, plan, reps, dev):
+    """Column streams that start with representative or mean chunks, a stream of 65 exact blocks (mass flush
+    after block 63 and at the end), one chunk of each kind, against the oracle on the same lists: exercises the
+    kernel's staged list ring and its first-chunk bias paths."""
+    p = plan
+    R, km, vm = reps
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    keep, counts, blocks, refine, rc, means, mc = (np.array(x, copy=True) for x in p["lists"])
+    counts[0, 0], mc[0, 0], rc[0, 0] = 0, 0, 3            # representatives only
+    refine[0, 0, :3] = [3, 10, NB - 1]
+    counts[1, 0], mc[1, 0], rc[1, 0] = 0, NB, 0           # block means only, two chunks
+    means[1, 0, :NB] = np.arange(NB)
+    counts[2, 0], mc[2, 0], rc[2, 0] = NB, 0, 0           # every block exact
+    blocks[2, 0, :NB] = np.arange(NB)
+    counts[3, 1], mc[3, 1], rc[3, 1] = 1, 1, 1            # one chunk of each kind, the tail block exact
+    blocks[3, 1, 0], means[3, 1, 0], refine[3, 1, 0] = NB - 1, 0, 2
+    offset = t(p["lse"])
+    out = torch.full_like(data["qd"], 7.0)
+    lse = torch.full((NQ * 128, H), 7.0, device=dev)
+    flags = torch.full((NQ, H), 7, device=dev, dtype=torch.int32)
+    mass = torch.zeros(H, NQ, NB, device=dev)
+    K().sparse_attention(data["qd"], data["kd"], data["vd"], km, vm, t(means), t(mc), out, t(counts), t(blocks),
+                         offset, lse, flags, t(refine), t(rc), R.k, R.v, R.log_counts, mass=mass)
+    torch.cuda.synchronize()
+    comp = dict(k_mean=f32(km), v_mean=f32(vm), means=means, mean_counts=mc, refine=refine, refine_counts=rc,
+                k_rep=f32(R.k), v_rep=f32(R.v), log_counts=f32(R.log_counts))
+    ro, rl, rf, rm = ref.fixed_offset_attention(f32(data["q"]), f32(data["k"]), f32(data["v"]), counts, blocks,
+                                                p["lse"], comp=comp, write_mass=True)
+    check_close("edge O", f32(out), ro)
+    check_close("edge LSE", f32(lse)[:L], rl[:L])
+    assert np.array_equal(flags.cpu().numpy(), rf)
+    ex = np.zeros((H, NQ, NB), bool)
+    for qt in range(NQ):
+        for hh in range(H):
+            ex[hh, qt, blocks[qt, hh, :counts[qt, hh]]] = True
+    check_close("edge mass", f32(mass)[ex], rm[ex], max_abs=2e-2 * max(1.0, float(np.abs(rm).max())))
+    assert (f32(mass)[~ex] == 0).all()
