@@ -204,43 +204,33 @@ __global__ __launch_bounds__(64) void rebuild_kernel(const int* __restrict__ exa
   const size_t pb = ((size_t)h * nq + t) * nw;
   const size_t lb = ((size_t)t * H + h) * NB;
   const size_t rbase = ((size_t)t * H + h) * rw;
+  // lane l takes block j0 + l: one ballot per list gives every set bit its position among the lanes below it, so
+  // the three lists come out in ascending block order with coalesced stores, 64 blocks per step
+  (void)nwords;
   int off_e = 0, off_m = 0, off_r = 0;
-  for (int w0 = 0; w0 < nwords; w0 += 64) {
-    const int word = w0 + l;
-    unsigned ex = 0, sk = 0, vm = 0;
-    if (word < nwords) {
-      ex = (unsigned)exact_bits[pb + word];
-      sk = (unsigned)skip_bits[pb + word];
-      const int rem = NB - word * 32;
-      vm = rem >= 32 ? 0xffffffffu : rem <= 0 ? 0u : ((1u << rem) - 1u);
+  for (int j0 = 0; j0 < NB; j0 += 64) {
+    const int j = j0 + l;
+    const bool valid = j < NB;
+    const unsigned ex = valid ? (unsigned)exact_bits[pb + (j >> 5)] : 0u;
+    const unsigned sk = valid ? (unsigned)skip_bits[pb + (j >> 5)] : 0u;
+    const bool e = valid && ((ex >> (j & 31)) & 1u);
+    const bool sbit = (sk >> (j & 31)) & 1u;
+    const bool r = valid && sbit && !e, m = valid && !sbit;
+    const unsigned long long be = __builtin_amdgcn_ballot_w64(e), br = __builtin_amdgcn_ballot_w64(r),
+                             bm = __builtin_amdgcn_ballot_w64(m);
+    auto below = [&](unsigned long long b) {
+      return (int)__builtin_amdgcn_mbcnt_hi((unsigned)(b >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)b, 0u));
+    };
+    if (e) idx[lb + off_e + below(be)] = j;
+    if (m) midx[lb + off_m + below(bm)] = j;
+    if (r) {
+      const int pr = off_r + below(br);
+      if (pr < rw) ridx[rbase + pr] = j;
     }
-    const unsigned e = ex & vm, r = sk & ~ex & vm, m = ~sk & vm;
-    const int ce = __popc(e), cr = __popc(r), cmn = __popc(m);
-    // inclusive scans over the wave
-    int ie = ce, ir = cr, im = cmn;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      int a = __shfl_up(ie, d, 64), b = __shfl_up(ir, d, 64), c = __shfl_up(im, d, 64);
-      if (l >= d) {
-        ie += a;
-        ir += b;
-        im += c;
-      }
-    }
-    int pe = off_e + ie - ce, pr = off_r + ir - cr, pm = off_m + im - cmn;
-    for (int i = 0; i < 32; ++i) {
-      const int j = word * 32 + i;
-      if ((e >> i) & 1u) idx[lb + pe++] = j;
-      if ((m >> i) & 1u) midx[lb + pm++] = j;
-      if ((r >> i) & 1u) {
-        if (pr < rw) ridx[rbase + pr] = j;
-        ++pr;
-      }
-      if ((vm >> i) & 1u) keep[((size_t)h * nq + t) * NB + j] = (e >> i) & 1u;
-    }
-    off_e += __shfl(ie, 63, 64);
-    off_r += __shfl(ir, 63, 64);
-    off_m += __shfl(im, 63, 64);
+    if (valid) keep[((size_t)h * nq + t) * NB + j] = e ? 1 : 0;
+    off_e += __builtin_popcountll(be);
+    off_r += __builtin_popcountll(br);
+    off_m += __builtin_popcountll(bm);
   }
   for (int p = off_r + l; p < rw; p += 64) ridx[rbase + p] = NB;
   if (l == 0) {
