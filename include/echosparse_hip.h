@@ -77,6 +77,13 @@ int es_compensate_fallback(const void* q, const void* k_mean, const void* v_mean
 int es_dense_attention(const void* q, const void* k, const void* v, void* out, float* lse2, int L, int H, int D,
                        hipStream_t stream);
 
+/* Dense attention of Lq query rows (q, out: (Lq, H, 128)) over Lk key rows (k, v: (Lk, H, 128)); log2 LSE as
+ * above over the query rows. The other FlashAttention-4 calls of the pipeline integrations: Wan cross-attention
+ * (echosparse/models/wan.py:26-28), the text query rows of HunyuanVideo (models/hunyuan_video.py:71) and the
+ * prefix rows of MiniMax-H3 (models/minimax_h3.py:85, 92). */
+int es_dense_attention_kv(const void* q, const void* k, const void* v, void* out, float* lse2, int Lq, int Lk,
+                          int H, int D, hipStream_t stream);
+
 /* ---------------------------------------------------------------- EchoSparse map, scales and plans */
 
 /* Mean key and value of every 64-token block (tail divided by its token count), bf16.

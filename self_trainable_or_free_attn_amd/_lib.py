@@ -24,6 +24,7 @@ SIGNATURES = {
     "es_exact_fallback": [P, P, P, P, P, P, I, P, P, I, I, I],
     "es_compensate_fallback": [P, P, P, P, P, P, P, I, I, I],
     "es_dense_attention": [P, P, P, P, P, I, I, I],
+    "es_dense_attention_kv": [P, P, P, P, P, I, I, I, I],
     "es_block_means": [P, P, P, P, I, I, I],
     "es_estimate_skipped": [P, P, P, P, P, P, P, P, I, I, I],
     "es_full_step_scales": [P, P, P, P, I, I],

@@ -34,14 +34,23 @@ def _next_pow2(n):
 
 
 def dense_attention(q, k, v, return_lse=False):
-    """Dense attention on [1, L, H, D] bf16 tensors with the native kernel. With return_lse also the natural-log
-    LSE [1, H, L] (the FlashAttention-4 contract the reference calls, attention.py:33-35)."""
+    """Dense attention on [B, Lq, H, D] queries over [B, Lk, H, D] keys / values (bf16, D = 128) with the native
+    kernel; Lk may differ from Lq (cross-attention, text rows). With return_lse also the natural-log LSE [B, H, Lq]
+    (the FlashAttention-4 contract the reference calls, attention.py:33-35)."""
     from .kernels import gfx950
-    out, lse2 = gfx950.dense_attention(q[0], k[0], v[0])
+    B, Lq = q.shape[:2]
+    outs, lses = [], []
+    for b in range(B):
+        if k.shape[1] == Lq:
+            out, lse2 = gfx950.dense_attention(q[b], k[b], v[b])
+        else:
+            out, lse2 = gfx950.dense_attention_kv(q[b], k[b], v[b])
+        outs.append(out)
+        lses.append(lse2[:Lq].t() / LOG2E)
+    out = outs[0][None] if B == 1 else torch.stack(outs)
     if not return_lse:
-        return out[None]
-    L = q.shape[1]
-    return out[None], (lse2[:L].t() / LOG2E)[None]
+        return out
+    return out, (lses[0][None] if B == 1 else torch.stack(lses))
 
 
 class _CompactState:

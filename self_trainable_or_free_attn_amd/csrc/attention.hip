@@ -46,7 +46,7 @@ struct AttnArgs {
   float* lse;
   int* flags;  // FIXED: written; ONLINE / COMPENSATE: read (nullptr = every tile)
   float* mass;
-  int L, H, nq, nb, NK, RW, tiles, per_xcd;
+  int L, Lk, H, nq, nb, NK, RW, tiles, per_xcd;  // L query rows, Lk key rows (Lk == L but in dense_kv)
   float threshold, tail_log2, scale;
 };
 
@@ -104,13 +104,13 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   }
   const int cm = (nm + BK - 1) / BK, cr = (4 * nr + BK - 1) / BK;
   const int nc = MODE == COMPENSATE ? (nb + BK - 1) / BK : n + (COMP ? cm + cr : 0);
-  const bool tail_block = (L & (BK - 1)) != 0;
+  const bool tail_block = (a.Lk & (BK - 1)) != 0;
 
   // Loads go through buffer resources (32-bit offsets; offsets past the end read as zero). Token tensors and the
   // mean table are row-strided by H * 256 bytes from this head's first row; representatives are contiguous rows.
   const unsigned hstride = (unsigned)H * HD * 2;
-  const srd_t rk = make_srd(a.k + (size_t)h * HD, (unsigned)(((size_t)L * H - h) * HD * 2));
-  const srd_t rv = make_srd(a.v + (size_t)h * HD, (unsigned)(((size_t)L * H - h) * HD * 2));
+  const srd_t rk = make_srd(a.k + (size_t)h * HD, (unsigned)(((size_t)a.Lk * H - h) * HD * 2));
+  const srd_t rv = make_srd(a.v + (size_t)h * HD, (unsigned)(((size_t)a.Lk * H - h) * HD * 2));
   srd_t rkm = rk, rvm = rv, rkr = rk, rvr = rv;
   if (COMP || MODE == COMPENSATE) {
     rkm = make_srd(a.k_mean + (size_t)h * HD, (unsigned)(((size_t)nb * H - h) * HD * 2));
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
           bias = (b < nb && a.keep[((size_t)h * a.nq + t) * nb + b] == 0) ? (b == nb - 1 ? a.tail_log2 : 6.0f)
                                                                            : -INFINITY;
         } else {
-          bias = b0 + l < L ? 0.0f : -INFINITY;
+          bias = b0 + l < a.Lk ? 0.0f : -INFINITY;
         }
       }
     } else {
@@ -477,6 +477,7 @@ static AttnArgs base_args(const void* q, const void* k, const void* v, int L, in
   a.k = (const bf16_t*)k;
   a.v = (const bf16_t*)v;
   a.L = L;
+  a.Lk = L;
   a.H = H;
   a.nq = (L + BM - 1) / BM;
   a.nb = (L + BK - 1) / BK;
@@ -592,4 +593,19 @@ extern "C" int es_compensate_fallback(const void* q, const void* k_mean, const v
   a.out = (bf16_t*)out;
   a.flags = (int*)flags;
   return launch<COMPENSATE, false, false>(a, stream, "es_compensate_fallback");
+}
+
+extern "C" int es_dense_attention_kv(const void* q, const void* k, const void* v, void* out, float* lse2, int Lq,
+                                     int Lk, int H, int D, hipStream_t stream) {
+  int st = check_common(q, k, v, Lq, H, D);
+  if (st) return st;
+  ES_REQUIRE(Lk > 0, ES_ERR_INVALID, "Lk must be positive");
+  ES_REQUIRE((size_t)Lk * H * D * 2 < (1ull << 31), ES_ERR_UNSUPPORTED, "k / v larger than 2 GiB (32-bit buffer offsets)");
+  ES_REQUIRE(out && lse2, ES_ERR_INVALID, "null tensor pointer");
+  AttnArgs a = base_args(q, k, v, Lq, H);
+  a.Lk = Lk;
+  a.nb = (Lk + BK - 1) / BK;
+  a.out = (bf16_t*)out;
+  a.lse = lse2;
+  return launch<ONLINE, false, false>(a, stream, "es_dense_attention_kv");
 }

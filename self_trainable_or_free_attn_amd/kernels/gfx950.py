@@ -138,6 +138,18 @@ def dense_attention(q, k, v):
     return out, lse
 
 
+def dense_attention_kv(q, k, v):
+    """Dense attention of q (Lq, H, D) over k / v (Lk, H, D), any Lk: returns (out (Lq, H, D) bf16, lse (nq * 128,
+    H) float32 log2 with 1e30 past Lq). The cross-attention / text-row calls of the pipeline integrations."""
+    Lq, H, D = _check_qkv(q, k, v)
+    Lk = k.shape[0]
+    assert k.shape == v.shape == (Lk, H, D), "k and v must be (Lk, H, 128) with q's heads"
+    out = torch.empty_like(q)
+    lse = torch.empty(_cdiv(Lq, BM) * BM, H, device=q.device, dtype=torch.float32)
+    _lib.call("es_dense_attention_kv", q, k, v, out, lse, Lq, Lk, H, D)
+    return out, lse
+
+
 class Representatives:
     """Four representatives per 64-token kv block, clustered in the query metric; buffers are reused across calls.
     Reference representatives.py:131-166 (same outputs: k / v (H, (nb + 1) * 4, D) bf16 and log_counts
