@@ -61,7 +61,7 @@ template <int MODE, bool COMP, bool MASS>
 __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char kv_s[2][2][BK * 256];
   __shared__ __attribute__((aligned(16))) float bias_s[2][BK];
-  __shared__ float mass_s[4][128];
+  __shared__ float mass_s[16][128];  // [wave * 4 + row of 16 lanes][chunk % 128]
   // list entries of chunks j, j+1, j+2 (ring slot j % 3), staged from global memory straight into LDS two chunks
   // ahead, so the loop holds no global->register or scalar loads whose waits would also drain the K / V loads
   __shared__ int ids_s[3][64];
@@ -310,8 +310,12 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
       pv(vb, 3, pk3);
       lsum += csum;
       if (MODE == FIXED && MASS && j < n) {
-        const float bs = wave_sum_dpp(csum);
-        if (l == 0) mass_s[wv][j & 127] = bs;
+        float bs = csum;
+        bs += dpp_f<0x111>(bs);
+        bs += dpp_f<0x112>(bs);
+        bs += dpp_f<0x114>(bs);
+        bs += dpp_f<0x118>(bs);
+        if ((l & 15) == 15) mass_s[wv * 4 + (l >> 4)][j & 127] = bs;
       }
       return;
     }
@@ -394,7 +398,9 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
     if (MODE == FIXED && MASS && j < n && ((j & 63) == 63 || j == n - 1) && tid < 64) {
       const int idx = (j & ~63) + tid;
       if (idx <= j) {
-        const float m = mass_s[0][idx & 127] + mass_s[1][idx & 127] + mass_s[2][idx & 127] + mass_s[3][idx & 127];
+        float m = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) m += mass_s[r][idx & 127];
         const int b = g_ex == nullptr ? idx : g_ex[idx];
         a.mass[((size_t)h * a.nq + t) * nb + b] = m;
       }
