@@ -188,22 +188,21 @@ __global__ __launch_bounds__(64) void probe_kernel(const bf16_t* __restrict__ q,
   p[1] = f2bf(b * scale / d);
 }
 
-// kmeans_kernel: one (block, head) per 256-thread workgroup; ~50 KB of LDS so three workgroups share a CU.
-//   LDS region A (33 KB): X (fp32, padded rows), then the K and V tiles for the final means
-//   LDS region B (16.6 KB): the K tile, then the probe logits, then the dot partials / centroids / weights
+// kmeans_kernel: one (block, head) per 256-thread workgroup; under 40 KB of LDS so four workgroups share a CU.
+//   LDS region A (33 KB): the K tile, then the probe logits, then X (fp32, padded rows), then the K and V tiles
+//                         for the final means (X waits in registers while the probe softmax reads the logits)
+//   LDS region B (7 KB):  the softmax partials, then the dot partials / centroids / weights
 // Thread (wave w, lane l) keeps X[l][32 w ..] in registers for the distances; the centroid sums (threads 0..127,
 // channel = tid) read X's columns from LDS.
 template <bool MEANS>
-__global__ __launch_bounds__(256, 3) void kmeans_kernel(const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+__global__ __launch_bounds__(256, 4) void kmeans_kernel(const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
                                                         const bf16_t* __restrict__ metric_t,
                                                         const bf16_t* __restrict__ probes, bf16_t* __restrict__ k4,
                                                         bf16_t* __restrict__ v4, float* __restrict__ lc4,
                                                         bf16_t* __restrict__ km, bf16_t* __restrict__ vm, int L,
                                                         int H, int NB, int iters) {
   __shared__ __attribute__((aligned(16))) float regA[BK * (HD + 1)];
-  __shared__ __attribute__((aligned(16))) float regB[NPROBE * (BK + 1)];
-  __shared__ float wpart[4][BK];
-  __shared__ float pmax[NPROBE], pinv[NPROBE];
+  __shared__ __attribute__((aligned(16))) float regB[(4 * BK + HD + BK) * 4];
   __shared__ float wgt[BK];
   __shared__ int lab[BK];
   __shared__ float cw[4];
@@ -212,8 +211,11 @@ __global__ __launch_bounds__(256, 3) void kmeans_kernel(const bf16_t* __restrict
   float(*X)[HD + 1] = reinterpret_cast<float(*)[HD + 1]>(regA);
   char* kt2 = reinterpret_cast<char*>(regA);  // K tile for the means (after the clustering)
   char* vt2 = kt2 + BK * 256;                 // V tile for the means
-  char* kt = reinterpret_cast<char*>(regB);   // K tile for X and the probe logits
-  float(*sp)[BK + 1] = reinterpret_cast<float(*)[BK + 1]>(regB);
+  char* kt = reinterpret_cast<char*>(regA);   // K tile for X and the probe logits
+  float(*sp)[BK + 1] = reinterpret_cast<float(*)[BK + 1]>(regA);
+  float(*wpart)[BK] = reinterpret_cast<float(*)[BK]>(regB);  // softmax partials [4][BK]
+  float* pmax = regB + 4 * BK;
+  float* pinv = pmax + NPROBE;
   f32x4* part = reinterpret_cast<f32x4*>(regB);            // [4 waves][BK] partial dots
   f32x4* cen = reinterpret_cast<f32x4*>(regB) + 4 * BK;    // [HD] centroids, (channel, cluster)
   f32x4* aw = reinterpret_cast<f32x4*>(regB) + 4 * BK + HD;  // [BK] token weight per cluster
@@ -248,12 +250,8 @@ __global__ __launch_bounds__(256, 3) void kmeans_kernel(const bf16_t* __restrict
       const bf16x8 b = lds_read16(kt, tile_off(32 * tk + lq, 2 * ks + hi));
       ap = mfma32(a, b, ap);
     }
-#pragma unroll
-    for (int eb = 0; eb < 2; ++eb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) X[32 * tb + 8 * (r / 4) + 4 * hi + (r % 4)][32 * (e0 + eb) + lq] = ax[eb][r];
   }
-  __syncthreads();  // every wave is done with the K tile: region B takes the probe logits
+  __syncthreads();  // every wave is done with the K tile: region A takes the probe logits
   {
     const int pb = wv & 1, tk = wv >> 1;
 #pragma unroll
@@ -261,9 +259,6 @@ __global__ __launch_bounds__(256, 3) void kmeans_kernel(const bf16_t* __restrict
   }
   __syncthreads();
 
-  float xd[32];  // X[l][32 wv + i]
-#pragma unroll
-  for (int i = 0; i < 32; ++i) xd[i] = X[l][32 * wv + i];
   // probe softmax weights w_t = sum_p softmax_p(t). (a) thread (probe tid % 64, token quarter tid / 64): row max
   // and row sum over its 16 tokens, combined through LDS; (b) wave wv, lane = token: its 16 probes. Plain loops
   // and LDS instead of one cross-lane reduction per probe.
@@ -299,7 +294,14 @@ __global__ __launch_bounds__(256, 3) void kmeans_kernel(const bf16_t* __restrict
     }
     wpart[wv][l] = wsum;  // (every read of wpart above precedes the last barrier)
   }
-  __syncthreads();  // the probe logits are consumed: region B is free
+  __syncthreads();  // the probe logits are consumed: region A takes X
+  {
+    const int tb = wv & 1, e0 = (wv >> 1) * 2;
+#pragma unroll
+    for (int eb = 0; eb < 2; ++eb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) X[32 * tb + 8 * (r / 4) + 4 * hi + (r % 4)][32 * (e0 + eb) + lq] = ax[eb][r];
+  }
   // token weights, the initial labels (four contiguous 16-token groups), per-cluster weights
   auto set_weights = [&](int lb) {  // wave 0, lane = token: aw and cw of the labels lb
     const float w = wgt[l];
@@ -322,6 +324,9 @@ __global__ __launch_bounds__(256, 3) void kmeans_kernel(const bf16_t* __restrict
     set_weights(l / (BK / 4));
   }
   __syncthreads();
+  float xd[32];  // X[l][32 wv + i]
+#pragma unroll
+  for (int i = 0; i < 32; ++i) xd[i] = X[l][32 * wv + i];
 
   // weighted centroids of the current labels (threads 0..127, channel = tid); a cluster with zero weight keeps
   // its previous centroid unless `init`; also the squared centroid norms (per wave, nnp)
