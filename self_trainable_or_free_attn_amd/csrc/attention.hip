@@ -61,7 +61,7 @@ template <int MODE, bool COMP, bool MASS>
 __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char kv_s[2][2][BK * 256];
   __shared__ __attribute__((aligned(16))) float bias_s[2][BK];
-  __shared__ float mass_s[16][128];  // [wave * 4 + row of 16 lanes][chunk % 128]
+  __shared__ float mass_s[16][129];  // [wave * 4 + row of 16 lanes][chunk % 128], rows padded against bank conflicts
   // list entries of chunks j, j+1, j+2 (ring slot j % 3), staged from global memory straight into LDS two chunks
   // ahead, so the loop holds no global->register or scalar loads whose waits would also drain the K / V loads
   __shared__ int ids_s[3][64];
