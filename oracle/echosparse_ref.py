@@ -9,7 +9,7 @@ blocks have BK = 64 tokens (nb = cdiv(L, 64)); offsets / LSEs are log2 values st
 1e30 past L; the block-mass map is (H, nq, nb) float32; block lists are (nq, H, NK) int32; bit plans are
 (H, nq, NW) int32 (bit j % 32 of word j // 32 is block j).
 
-Pinning (what checks each function independently of this file; the tests live in tests/test_oracle_*.py):
+Pinning (what checks each function independently of this file; the tests live in tests/test_cpu_oracle.py):
   block_means           closed form; test compares with torch mean + bf16 rounding
   fixed_offset_attention
                         density-1.0 identity with dense softmax attention (torch), offset invariance of O,
@@ -18,14 +18,16 @@ Pinning (what checks each function independently of this file; the tests live in
   exact_fallback        equals torch.softmax attention over the listed blocks (textbook logsumexp)
   compensate_fallback   closed form: appending mean columns to one softmax (derivation in its docstring),
                         checked against torch.softmax over [exact tokens ++ means]
-  estimate_skipped      brute-force per-element loops on tiny inputs (tests/test_oracle_plans.py)
+  estimate_skipped      brute-force per-element loops on tiny inputs
   full_step_scales      brute force on tiny inputs
   select_blocks         hand-made maps with ties, forced and sink blocks, fell-back tiles, NaN (known answers);
                         pack -> rebuild round trip (reference tests/test_sm120.py:109-140)
   pack_plan / rebuild_plan
                         round trip + known answers
   representatives       invariants of reference tests/test_sm120.py:65-83 (weighted sum of reps = block sum,
-                        counts sum to block length), Lloyd fixed point, -inf for empty clusters
+                        counts sum to block length), Lloyd fixed point, -inf for empty clusters; the exact float
+                        values beyond these invariants are parity unpinned (the reference's own clustering uses
+                        TF32 dot products)
 """
 import math
 
