@@ -190,3 +190,72 @@ def test_minimax_hooks_packed_sequence(monkeypatch):
     perm, _ = grid_morton_order(*grid, torch.device("cpu"))
     assert torch.equal(impl.layout.packed_to_original[:nv], perm + prefix)
     assert torch.equal(impl.layout.packed_to_original[nv:], torch.arange(prefix))
+
+
+def test_morton_known_answer():
+    """Reference tests/test_attention.py:152-155: the first tokens of a 5 x 6 x 7 grid in Morton order."""
+    from self_trainable_or_free_attn_amd.models.common import grid_morton_order
+    perm, inv = grid_morton_order(5, 6, 7, torch.device("cpu"))
+    assert torch.equal(perm[inv], torch.arange(5 * 6 * 7))
+    assert perm[:8].tolist() == [0, 1, 7, 8, 42, 43, 49, 50]
+
+
+def test_h3_layout_strided_time_axis():
+    """Reference tests/test_api.py:146-166 (the layout part): a prefix of text, conditioning-video and audio tokens,
+    then a 2 x 3 x 4 target video whose rotary t coordinate steps by 2; the packed order is the video in the Morton
+    order of the ranked coordinates, then the prefix in its own order."""
+    fd.install()
+    from self_trainable_or_free_attn_amd.models.common import morton_order
+    from self_trainable_or_free_attn_amd.models.minimax_h3 import _Layout
+    t, y, x = torch.meshgrid(torch.arange(0, 4, 2), torch.arange(3), torch.arange(4), indexing="ij")
+    video = torch.stack([t.flatten(), y.flatten(), x.flatten()], 1)
+    pos = torch.cat([torch.zeros(9, 3, dtype=torch.long), video])
+    L, vs = pos.shape[0], 9
+    layout = _Layout(pos, torch.cat([torch.arange(3, 7), torch.arange(vs, L)]))
+    perm, _ = morton_order(video[:, 0] // 2, video[:, 1], video[:, 2])
+    assert layout.video == L - vs and layout.video_start == vs
+    assert torch.equal(layout.packed_to_original[:L - vs], perm + vs)
+    assert torch.equal(layout.packed_to_original[L - vs:], torch.arange(vs))
+    assert torch.equal(layout.packed_to_original[layout.original_to_packed], torch.arange(L))
+
+
+def test_enable_and_attention_agree(monkeypatch):
+    """Reference tests/test_api.py:86-99: the package-level enable builds the attention from the named preset and
+    hands that same object to the family's hooks."""
+    import sys
+    import types
+    import self_trainable_or_free_attn_amd as pkg
+    from self_trainable_or_free_attn_amd import models
+    seen = {}
+    fake = types.ModuleType("self_trainable_or_free_attn_amd.models.minimax_h3")
+    fake.enable = lambda pipe, attention: seen.update(attention=attention)
+    monkeypatch.setitem(sys.modules, fake.__name__, fake)
+    monkeypatch.setattr(models, "minimax_h3", fake, raising=False)
+    pipe = types.SimpleNamespace(transformer=type("MiniMaxH3Transformer", (), {})())
+    attn = pkg.enable(pipe, preset="minimax_h3_rtx5090", gpu="mi355x", refine_iters=6)
+    assert seen["attention"] is attn
+    assert (attn.density, attn.dense_steps, attn.dense_layers, attn.gpu) == (0.24, 10, {0}, "mi355x")
+    with pytest.raises(ValueError, match="gpu must be"):
+        pkg.enable(pipe, gpu="sm120")
+
+
+def test_device_change_releases_old_history(monkeypatch):
+    """Reference tests/test_api.py:64-83: state and scratch survive calls on one device and are dropped when the
+    inputs move to another."""
+    import types
+    from self_trainable_or_free_attn_amd import EchoSparseAttention, attention, backends
+    monkeypatch.setattr(backends, "resolve", lambda gpu, device: "mi355x")
+    monkeypatch.setattr(backends, "kernels", lambda name: None)
+    monkeypatch.setattr(attention, "dense_attention", lambda q, k, v: q)
+    attn = EchoSparseAttention()
+    q = types.SimpleNamespace(shape=(1, 128, 1, 128), device=torch.device("cuda:0"))
+    attn(q, q, q, step=0, branch=0, layer=0)
+    previous = object()
+    attn._states[1] = previous
+    attn._buffers = attn._plan_scratch = previous
+    attn(q, q, q, step=0, branch=0, layer=0)
+    assert attn._states[1] is previous and attn._buffers is previous
+    q.device = torch.device("cuda:1")
+    attn(q, q, q, step=0, branch=0, layer=0)
+    assert not attn._states
+    assert attn._buffers is None and attn._plan_scratch is None
