@@ -3,7 +3,8 @@
  * Conventions as in echosparse_hip.h: caller-owned device pointers, plain sizes, the HIP stream last, no
  * allocation and no synchronisation inside, an es_status return and es_last_error_string() on failure.
  * Layouts (row-major):
- *   tokens q, k, v, o, gate, dO      [BH, L, 128] bf16, L = NB * 64, valid-first 64-token blocks
+ *   tokens q, k, v, o, gate, dO      [BH, L, 128] bf16 (fp16: the _f16 twins), L = NB * 64, valid-first
+ *                                    64-token blocks
  *   D (every entry point)            the logical head dim, 64 or 128: rows are always 128 columns wide and a
  *                                    D = 64 caller zero-fills columns 64..127 (they add exact zeros to every dot
  *                                    product and come out zero); D sets the softmax scale 1 / sqrt(D)
@@ -214,6 +215,82 @@ int vsa_row_dot(const void* x, const void* y, const int* blk_cnt, float* out, in
  * rep_pool.cu:114-140 tier_b_lists. */
 int vsa_tier_b_lists(const int* ab_ptr, const int* ab_idx, const int* a_ptr, const unsigned* bits_a, int* b_ptr,
                      int* b_idx, int BH, int NB, hipStream_t stream);
+
+/* ---------------------------------------------------------------- fp16 token tensors
+ * Every entry point above that reads or writes token tensors (q, k, v, o, gate, dO, pools, block means, scores,
+ * tier tables, gradients) has an fp16 twin with the suffix _f16 and the same arguments: the same kernels built for
+ * fp16 storage and v_mfma_f32_32x32x16_f16 (fp32 accumulation), as the reference dispatches its kernels on the
+ * tensor dtype (csrc/vsa/vsa2_api.cpp:51). Entry points without token tensors (vsa_topk_workspace,
+ * vsa_global_topk, vsa_csr_transpose, vsa_split_plan, vsa_tier_b_lists) serve both. */
+int vsa_pool_f16(const void* q, const void* k, const void* v, const int* blk_cnt, void* qr, void* kr, void* vr,
+                 void* qc, void* kc, void* vc, int BH, int L, int D, int R, hipStream_t stream);
+int vsa_fuse_fwd_f16(const void* of, const void* oc, const void* gate, void* o, const int* blk_cnt, int BH, int L,
+                     int D, int NBc_pad, int gate_mode, int gate_act, hipStream_t stream);
+int vsa_fuse_bwd_f16(const void* dout, const void* of, const void* oc, const void* gate, void* dout_f, float* delta_f,
+                     void* dout_c, float* delta_c, void* dgate, const int* blk_cnt, int BH, int L, int D, int NBc_pad,
+                     int gate_mode, int gate_act, hipStream_t stream);
+int vsa_finalize_f16(const float* acc, const float* add, int add_nb, void* out, const int* blk_cnt, int BH, int L,
+                     int D, hipStream_t stream);
+int vsa_attn_fwd_f16(const void* q, const void* k, const void* v, const int* row_ptr, const int* col_idx,
+                     const int* blk_cnt, void* out, float* lse, int BH, int L, int D, hipStream_t stream);
+int vsa_attn_fwd_tasks_f16(const void* q, const void* k, const void* v, const int* col_idx, const int* blk_cnt,
+                           const int* tasks, const int* info, int max_tasks, void* out, float* lse, float* part_o,
+                           float* part_lse, int BH, int L, int D, hipStream_t stream);
+int vsa_attn_bwd_kv_f16(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                        const float* delta, const int* k2q_ptr, const int* k2q_idx, const int* blk_cnt,
+                        const float* add_dk, const float* add_dv, int add_nb, void* dk, void* dv, int out_fp32, int BH,
+                        int L, int D, hipStream_t stream);
+int vsa_attn_bwd_kv_tasks_f16(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                              const float* delta, const int* k2q_idx, const int* blk_cnt, const int* tasks,
+                              const int* info, int max_tasks, const float* add_dk, const float* add_dv, int add_nb,
+                              void* dk, void* dv, float* part_dk, float* part_dv, int BH, int L, int D,
+                              hipStream_t stream);
+int vsa_attn_bwd_q_f16(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                       const float* delta, const int* q2k_ptr, const int* q2k_idx, const int* blk_cnt,
+                       const float* add_dq, int add_nb, void* dq, float* dq_acc, int BH, int L, int D,
+                       hipStream_t stream);
+int vsa_attn_bwd_q_tasks_f16(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                             const float* delta, const int* q2k_idx, const int* blk_cnt, const int* tasks,
+                             const int* info, int max_tasks, const float* add_dq, int add_nb, void* dq, float* part_dq,
+                             int BH, int L, int D, hipStream_t stream);
+int vsa_block_scores_f16(const void* qc, const void* kc, void* scores, int NB, int NBc_pad, int bh0, int bh_count, int D,
+                         hipStream_t stream);
+int vsa_route_rows_f16(const void* qc, const void* kc, int NB, int NBc_pad, int bh0, int bh_count, int K, int D,
+                       int* q2k_ptr, int* q2k_idx, int* k2q_ptr, int* k2q_idx, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream);
+int vsa_row_topk_f16(const void* scores, int NB, int bh0, int bh_count, int K, int* q2k_ptr, int* q2k_idx,
+                     int* k2q_ptr, int* k2q_idx, void* workspace, size_t workspace_bytes, hipStream_t stream);
+int vsa_router_lse_f16(const void* qr, const void* kr, const int* blk_cnt, float* lse2, int NB, int R, int BH, int D,
+                       hipStream_t stream);
+int vsa_router_scores_f16(const void* qr, const void* kr, const float* lse2, const int* blk_cnt, float* scores, int NB,
+                          int R, int row_norm, int bh0, int bh_count, int D, hipStream_t stream);
+int vsa_split_merge_fwd_f16(const float* part_o, const float* part_lse, const int* merges, const int* info,
+                            int max_merges, const int* blk_cnt, void* o, float* lse, int BH, int L, int D, int mask_rows,
+                            hipStream_t stream);
+int vsa_split_merge_sum_f16(const float* part, const int* merges, const int* info, int max_merges, const float* add,
+                            int add_nb, const int* blk_cnt, void* out, float* out_f32, int BH, int L, int D,
+                            hipStream_t stream);
+int vsa_rep_build_f16(const void* k, const void* v, const int* blk_cnt, void* k_mid, void* v_mid, float* lc_mid,
+                      void* k_tail, void* v_tail, float* lc_tail, int BH, int L, int D, int RM, hipStream_t stream);
+int vsa_rep_attn_fwd_f16(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
+                         const float* lc_mid, const void* k_tail, const void* v_tail, const float* lc_tail,
+                         const int* q2k_ptr, const int* q2k_idx, const unsigned* bits_a, const unsigned* bits_ab,
+                         const int* blk_cnt, void* out, float* lse, int BH, int L, int D, int RM, int phases,
+                         hipStream_t stream);
+int vsa_rep_attn_bwd_q_f16(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
+                           const float* lc_mid, const void* k_tail, const void* v_tail, const float* lc_tail,
+                           const void* dout, const float* lse, const float* delta, const int* q2k_ptr,
+                           const int* q2k_idx, const unsigned* bits_a, const unsigned* bits_ab, const int* blk_cnt,
+                           const float* add_dq, int add_nb, const float* dq_acc, void* dq, int BH, int L, int D, int RM,
+                           int phases, hipStream_t stream);
+int vsa_rep_bwd_tables_f16(const void* q, const void* dout, const void* k_tab, const void* v_tab, const float* lc,
+                           const float* lse, const float* delta, const unsigned* bits_a, const unsigned* bits_ab,
+                           float* dk_tab, float* dv_tab, int BH, int L, int D, int RM, int tier, hipStream_t stream);
+int vsa_rep_unpool_f16(const float* acc_k, const float* acc_v, const float* dk_mid, const float* dv_mid,
+                       const float* dk_tail, const float* dv_tail, const int* blk_cnt, void* dk, void* dv, int BH, int L,
+                       int D, int RM, hipStream_t stream);
+int vsa_row_dot_f16(const void* x, const void* y, const int* blk_cnt, float* out, int BH, int L, int D,
+                    hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -42,10 +42,10 @@ def token_valid(blk_cnt, L):
     return (pos % BLOCK) < np.asarray(blk_cnt, np.int64)[pos // BLOCK]
 
 
-def pool(x, blk_cnt, R):
-    """(group means [B, H, NB * G, D], block means [B, H, NB, D]) as bf16 values in float32, restating
-    csrc/vsa/router/pool.cu:16-51: per column, float32 sums of a group's valid rows in order, the group sums added in
-    order, times 1 / count; empty groups give 0."""
+def pool(x, blk_cnt, R, rnd=round_bf16):
+    """(group means [B, H, NB * G, D], block means [B, H, NB, D]) as 16-bit values in float32 (rnd: round_bf16 or
+    round_f16, the token dtype), restating csrc/vsa/router/pool.cu:16-51: per column, float32 sums of a group's
+    valid rows in order, the group sums added in order, times 1 / count; empty groups give 0."""
     x = np.asarray(x, np.float32)
     B, H, L, D = x.shape
     NB, G = L // BLOCK, BLOCK // R
@@ -60,18 +60,19 @@ def pool(x, blk_cnt, R):
             for r in range(r0, r1):
                 s = (s + x[:, :, b * BLOCK + r]).astype(np.float32)
             inv = np.float32(1.0) / np.float32(r1 - r0) if r1 > r0 else np.float32(0.0)
-            grp[:, :, b * G + g] = round_bf16(s * inv)
+            grp[:, :, b * G + g] = rnd(s * inv)
             tot = (tot + s).astype(np.float32)
-        blk[:, :, b] = round_bf16(tot * (np.float32(1.0) / np.float32(cnt[b])))
+        blk[:, :, b] = rnd(tot * (np.float32(1.0) / np.float32(cnt[b])))
     return grp, blk
 
 
-def block_scores(qc, kc):
-    """rnd(rnd(qc . kc) / sqrt(D)) with rnd = bf16, float64 dot (reference tests/vsa_reference.py:148-151)."""
+def block_scores(qc, kc, rnd=round_bf16):
+    """rnd(rnd(qc . kc) / sqrt(D)) with rnd the token dtype's rounding (bf16 default), float64 dot (reference
+    tests/vsa_reference.py:148-151)."""
     qc, kc = np.asarray(qc, np.float64), np.asarray(kc, np.float64)
     D = qc.shape[-1]
-    s = round_bf16(np.einsum("...id,...jd->...ij", qc, kc).astype(np.float32))
-    return round_bf16((s * np.float32(1.0 / math.sqrt(D))).astype(np.float32))
+    s = rnd(np.einsum("...id,...jd->...ij", qc, kc).astype(np.float32))
+    return rnd((s * np.float32(1.0 / math.sqrt(D))).astype(np.float32))
 
 
 def _desc_order(values):
@@ -287,12 +288,13 @@ def merge_fwd(part_o, part_lse2):
 
 
 # --------------------------------------------------------------------------- VSA2 three-tier representatives
-def rep_tables(k, v, blk_cnt, RM):
+def rep_tables(k, v, blk_cnt, RM, rnd=round_bf16):
     """(k_mid, v_mid [B, H, NB * RM, D], k_tail, v_tail [B, H, NB, D], lc_mid [NB * RM], lc_tail [NB]): the pooled
     group / block means of the kernels' float32 order (see `pool`, groups of 64 / RM tokens) and log2 counts, -inf
-    for an empty group (reference experiments/vsa2_representative/vsa2_rep/reference.py:23-50)."""
-    km, kt = pool(k, blk_cnt, BLOCK // RM)
-    vm, vt = pool(v, blk_cnt, BLOCK // RM)
+    for an empty group (reference experiments/vsa2_representative/vsa2_rep/reference.py:23-50); rnd = the token
+    dtype's rounding."""
+    km, kt = pool(k, blk_cnt, BLOCK // RM, rnd)
+    vm, vt = pool(v, blk_cnt, BLOCK // RM, rnd)
     cnt = np.asarray(blk_cnt, np.int64)
     gs = BLOCK // RM
     n = np.clip(cnt[:, None] - np.arange(RM)[None, :] * gs, 0, gs).reshape(-1)

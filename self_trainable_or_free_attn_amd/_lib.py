@@ -61,6 +61,13 @@ SIGNATURES = {
     "vsa_row_dot": [P, P, P, P, I, I, I],
     "vsa_tier_b_lists": [P, P, P, P, P, P, I, I],
 }
+# include/vsa_hip.h: the fp16 twins (suffix _f16) of the entry points that take token tensors, same arguments
+F16_TWINS = ("vsa_pool", "vsa_fuse_fwd", "vsa_fuse_bwd", "vsa_finalize", "vsa_attn_fwd", "vsa_attn_fwd_tasks",
+             "vsa_attn_bwd_kv", "vsa_attn_bwd_kv_tasks", "vsa_attn_bwd_q", "vsa_attn_bwd_q_tasks", "vsa_block_scores",
+             "vsa_route_rows", "vsa_row_topk", "vsa_router_lse", "vsa_router_scores", "vsa_split_merge_fwd",
+             "vsa_split_merge_sum", "vsa_rep_build", "vsa_rep_attn_fwd", "vsa_rep_attn_bwd_q", "vsa_rep_bwd_tables",
+             "vsa_rep_unpool", "vsa_row_dot")
+SIGNATURES.update({n + "_f16": SIGNATURES[n] for n in F16_TWINS})
 NO_STREAM = {"es_representatives_workspace": ([I, I, I], Z), "es_last_error_string": ([], ctypes.c_char_p),
              "es_abi_version": ([], I), "vsa_topk_workspace": ([I, I], Z)}
 

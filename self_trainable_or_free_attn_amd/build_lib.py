@@ -1,7 +1,8 @@
 """Build libechosparse_hip.so in-tree with hipcc for gfx950 (python -m self_trainable_or_free_attn_amd.build_lib).
 
-Every HIP source under csrc/ is compiled to an object in parallel and linked into lib/libechosparse_hip.so. Flags:
--O3, gfx950 only, and packed FP32 instructions disabled (-Xclang -target-feature -Xclang -packed-fp32-ops).
+Every HIP source under csrc/ is compiled to an object in parallel and linked into lib/libechosparse_hip.so; the
+VSA sources (vsa_*.hip) are compiled a second time with -DES_ELEM_F16 for their fp16 entry points (suffix _f16).
+Flags: -O3, gfx950 only, and packed FP32 instructions disabled (-Xclang -target-feature -Xclang -packed-fp32-ops).
 """
 import os
 import subprocess
@@ -22,10 +23,21 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 
 
-def _compile(src, obj_dir):
-    obj = os.path.join(obj_dir, os.path.basename(src) + ".o")
+def units():
+    """(source, extra flags, object suffix) for every compilation: each source once, the VSA ones also for fp16."""
+    out = []
+    for src in sources():
+        out.append((src, [], ""))
+        if os.path.basename(src).startswith("vsa_"):
+            out.append((src, ["-DES_ELEM_F16"], ".f16"))
+    return out
+
+
+def _compile(unit, obj_dir):
+    src, extra, suffix = unit
+    obj = os.path.join(obj_dir, os.path.basename(src) + suffix + ".o")
     lang = ["-x", "hip"] if src.endswith(".hip") else []
-    cmd = [HIPCC, *FLAGS, *lang, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *extra, *lang, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")
@@ -39,9 +51,9 @@ def build(verbose=False, out=None):
     obj_dir = os.path.join(HERE, "_build", os.path.basename(lib_path))
     os.makedirs(obj_dir, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
-    srcs = sources()
+    srcs = units()
     with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(lambda s: _compile(s, obj_dir), srcs))
+        objs = list(ex.map(lambda u: _compile(u, obj_dir), srcs))
     os.makedirs(os.path.dirname(lib_path), exist_ok=True)
     tmp = lib_path + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
@@ -50,7 +62,7 @@ def build(verbose=False, out=None):
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, lib_path)
     if verbose:
-        print(f"built {lib_path} from {len(srcs)} sources")
+        print(f"built {lib_path} from {len(srcs)} compilations")
     return lib_path
 
 

@@ -16,6 +16,7 @@
 // writes an fp32 normalized partial O and its log2 lse to part_o / part_lse, slot < 0 the final O / lse.
 #include "../../include/vsa_hip.h"
 #include "common.h"
+#include "elem.h"
 
 namespace es {
 
@@ -25,8 +26,8 @@ constexpr float LN2 = 0.6931471805599453f;
 constexpr float RESCALE_SLACK = 8.0f;
 
 struct VsaFwdArgs {
-  const bf16_t *q, *k, *v;
-  bf16_t* out;
+  const e16_t *q, *k, *v;
+  e16_t* out;
   float* lse;
   const int *row_ptr, *col_idx, *blk_cnt;
   const int4* tasks;
@@ -94,11 +95,11 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
     }
   };
 
-  bf16x8 qreg[8];
+  ev8 qreg[8];
   {
-    const bf16_t* qp = a.q + (head + (size_t)qb * BK + qrow) * HD;
+    const e16_t* qp = a.q + (head + (size_t)qb * BK + qrow) * HD;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qreg[ks] = *reinterpret_cast<const bf16x8*>(qp + 16 * ks + 8 * hi);
+    for (int ks = 0; ks < 8; ++ks) qreg[ks] = *reinterpret_cast<const ev8*>(qp + 16 * ks + 8 * hi);
   }
   int koff[8];
 #pragma unroll
@@ -138,7 +139,7 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
     const char* vb = kv_s[sb][1] + kh * 8192;
     f32x16 s = {};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) s = mfma32(lds_read16(kb, koff[ks]), qreg[ks], s);
+    for (int ks = 0; ks < 8; ++ks) s = emfma(elds16(kb, koff[ks]), qreg[ks], s);
     float p[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) p[r] = s[r] * scale;
@@ -164,12 +165,12 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
     const float msub = mref == -INFINITY ? 0.0f : mref;
 #pragma unroll
     for (int r = 0; r < 16; ++r) p[r] = exp2f_fast(p[r] - msub);
-    const bf16x8 pa = pack8(&p[0]), pb = pack8(&p[8]);
-    lsum += sum8_bf16(pb, sum8_bf16(pa, 0.0f));
+    const ev8 pa = epack8(&p[0]), pb = epack8(&p[8]);
+    lsum += esum8(pb, esum8(pa, 0.0f));
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      o[db] = mfma32(cat_tr(lds_read_tr(vb, voff[0][db]), lds_read_tr(vb, voff[1][db])), pa, o[db]);
-      o[db] = mfma32(cat_tr(lds_read_tr(vb + 4096, voff[0][db]), lds_read_tr(vb + 4096, voff[1][db])), pb, o[db]);
+      o[db] = emfma(ecat_tr(lds_read_tr(vb, voff[0][db]), lds_read_tr(vb, voff[1][db])), pa, o[db]);
+      o[db] = emfma(ecat_tr(lds_read_tr(vb + 4096, voff[0][db]), lds_read_tr(vb + 4096, voff[1][db])), pb, o[db]);
     }
     wait_vmem();
     __syncthreads();
@@ -202,16 +203,16 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
   const size_t tok = head + (size_t)qb * BK + qrow;
   const float lse2 = live ? M + log2f(lt) : -INFINITY;
   if (!TASKS || slot < 0) {
-    bf16_t* orow = a.out + tok * HD;
+    e16_t* orow = a.out + tok * HD;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         ushort4 v4;
-        v4.x = f2bf((a0 * o[db][4 * i + 0] + a1 * xo[(db * 16 + 4 * i + 0) * 64 + l]) * inv);
-        v4.y = f2bf((a0 * o[db][4 * i + 1] + a1 * xo[(db * 16 + 4 * i + 1) * 64 + l]) * inv);
-        v4.z = f2bf((a0 * o[db][4 * i + 2] + a1 * xo[(db * 16 + 4 * i + 2) * 64 + l]) * inv);
-        v4.w = f2bf((a0 * o[db][4 * i + 3] + a1 * xo[(db * 16 + 4 * i + 3) * 64 + l]) * inv);
+        v4.x = f2e((a0 * o[db][4 * i + 0] + a1 * xo[(db * 16 + 4 * i + 0) * 64 + l]) * inv);
+        v4.y = f2e((a0 * o[db][4 * i + 1] + a1 * xo[(db * 16 + 4 * i + 1) * 64 + l]) * inv);
+        v4.z = f2e((a0 * o[db][4 * i + 2] + a1 * xo[(db * 16 + 4 * i + 2) * 64 + l]) * inv);
+        v4.w = f2e((a0 * o[db][4 * i + 3] + a1 * xo[(db * 16 + 4 * i + 3) * 64 + l]) * inv);
         *reinterpret_cast<ushort4*>(orow + 32 * db + 8 * i + 4 * hi) = v4;
       }
     if (hi == 0) a.lse[tok] = live ? lse2 * LN2 : -INFINITY;
@@ -244,14 +245,14 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
 //     transposed LDS reads. 3 products per pair; dQ is deterministic (no atomics).
 // The two partial accumulators of a workgroup (query halves, or key halves) are summed once at the end in LDS.
 struct VsaBwdArgs {
-  const bf16_t *q, *k, *v, *dout;
+  const e16_t *q, *k, *v, *dout;
   const float *lse, *delta;
   const int *row_ptr, *col_idx, *blk_cnt;
   const int4* tasks;
   const int* info;
   const float *add_a, *add_b;  // per-block gradients distributed as add / cnt (KV owner: dK, dV; Q owner: dQ)
   int add_nb;
-  bf16_t *out_a, *out_b;       // bf16 outputs
+  e16_t *out_a, *out_b;       // bf16 outputs
   float *out_a32, *out_b32;    // fp32 outputs (KV owner) / accumulator dq_acc += dQ (Q owner)
   float *part_a, *part_b;      // split partials [slot, 64, D]
   int L, NB, BH, per_xcd;
@@ -320,11 +321,11 @@ __global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) dma16(rv, v_s + wv * 4096 + i * 1024, ld_off[i], (unsigned)kb * (BK * 256));
   }
-  bf16x8 kreg[8];
+  ev8 kreg[8];
   {
     const size_t off = (head + (size_t)kb * BK + key) * HD + 8 * hi;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) kreg[ks] = *reinterpret_cast<const bf16x8*>(a.k + off + 16 * ks);
+    for (int ks = 0; ks < 8; ++ks) kreg[ks] = *reinterpret_cast<const ev8*>(a.k + off + 16 * ks);
   }
   // stage query block i (Q, dO); wave 0 returns lane l's lse2 / delta of row i * 64 + l
   auto issue = [&](int i, int sb, float& ls, float& dl) {
@@ -384,9 +385,9 @@ __global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
     const char* dt = qd_s[sb][1];
     f32x16 s = {}, dp = {};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) s = mfma32(lds_read16(qt, aoff[ks]), kreg[ks], s);
+    for (int ks = 0; ks < 8; ++ks) s = emfma(elds16(qt, aoff[ks]), kreg[ks], s);
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) dp = mfma32(lds_read16(dt, aoff[ks]), lds_read16(v_s, boff[ks]), dp);
+    for (int ks = 0; ks < 8; ++ks) dp = emfma(elds16(dt, aoff[ks]), elds16(v_s, boff[ks]), dp);
     float p[16], ds[16];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -399,14 +400,14 @@ __global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
         ds[r] = p[r] * (dp[r] - d4[e]) * a.scale;
       }
     }
-    const bf16x8 pa = pack8(&p[0]), pb = pack8(&p[8]);
-    const bf16x8 sa = pack8(&ds[0]), sb8 = pack8(&ds[8]);
+    const ev8 pa = epack8(&p[0]), pb = epack8(&p[8]);
+    const ev8 sa = epack8(&ds[0]), sb8 = epack8(&ds[8]);
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      dv[db] = mfma32(cat_tr(lds_read_tr(dt, toff[0][db]), lds_read_tr(dt, toff[1][db])), pa, dv[db]);
-      dv[db] = mfma32(cat_tr(lds_read_tr(dt + 4096, toff[0][db]), lds_read_tr(dt + 4096, toff[1][db])), pb, dv[db]);
-      dk[db] = mfma32(cat_tr(lds_read_tr(qt, toff[0][db]), lds_read_tr(qt, toff[1][db])), sa, dk[db]);
-      dk[db] = mfma32(cat_tr(lds_read_tr(qt + 4096, toff[0][db]), lds_read_tr(qt + 4096, toff[1][db])), sb8, dk[db]);
+      dv[db] = emfma(ecat_tr(lds_read_tr(dt, toff[0][db]), lds_read_tr(dt, toff[1][db])), pa, dv[db]);
+      dv[db] = emfma(ecat_tr(lds_read_tr(dt + 4096, toff[0][db]), lds_read_tr(dt + 4096, toff[1][db])), pb, dv[db]);
+      dk[db] = emfma(ecat_tr(lds_read_tr(qt, toff[0][db]), lds_read_tr(qt, toff[1][db])), sa, dk[db]);
+      dk[db] = emfma(ecat_tr(lds_read_tr(qt + 4096, toff[0][db]), lds_read_tr(qt + 4096, toff[1][db])), sb8, dk[db]);
     }
     dma_wait();
     if (j + 1 < nc && wv == 0) {
@@ -475,8 +476,8 @@ __global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
         *reinterpret_cast<f32x4*>(a.out_b32 + tok * HD + c) = xv4;
       } else {
         ushort4 k4, v4;
-        k4.x = f2bf(xk4[0]); k4.y = f2bf(xk4[1]); k4.z = f2bf(xk4[2]); k4.w = f2bf(xk4[3]);
-        v4.x = f2bf(xv4[0]); v4.y = f2bf(xv4[1]); v4.z = f2bf(xv4[2]); v4.w = f2bf(xv4[3]);
+        k4.x = f2e(xk4[0]); k4.y = f2e(xk4[1]); k4.z = f2e(xk4[2]); k4.w = f2e(xk4[3]);
+        v4.x = f2e(xv4[0]); v4.y = f2e(xv4[1]); v4.z = f2e(xv4[2]); v4.w = f2e(xv4[3]);
         *reinterpret_cast<ushort4*>(a.out_a + tok * HD + c) = k4;
         *reinterpret_cast<ushort4*>(a.out_b + tok * HD + c) = v4;
       }
@@ -498,11 +499,11 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
   const size_t head = (size_t)bh * a.L;
   const size_t tok = head + (size_t)qb * BK + qrow;
 
-  bf16x8 qreg[8], dreg[8];
+  ev8 qreg[8], dreg[8];
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
-    qreg[ks] = *reinterpret_cast<const bf16x8*>(a.q + tok * HD + 16 * ks + 8 * hi);
-    dreg[ks] = *reinterpret_cast<const bf16x8*>(a.dout + tok * HD + 16 * ks + 8 * hi);
+    qreg[ks] = *reinterpret_cast<const ev8*>(a.q + tok * HD + 16 * ks + 8 * hi);
+    dreg[ks] = *reinterpret_cast<const ev8*>(a.dout + tok * HD + 16 * ks + 8 * hi);
   }
   const float ls = qvalid ? lse_to_log2(a.lse[tok]) : INFINITY;
   const float dl = a.delta[tok];
@@ -558,9 +559,9 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
     const char* vt = kv_s[sb][1];
     f32x16 s = {}, dp = {};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) s = mfma32(lds_read16(kt, koff[ks]), qreg[ks], s);
+    for (int ks = 0; ks < 8; ++ks) s = emfma(elds16(kt, koff[ks]), qreg[ks], s);
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) dp = mfma32(lds_read16(vt, koff[ks]), dreg[ks], dp);
+    for (int ks = 0; ks < 8; ++ks) dp = emfma(elds16(vt, koff[ks]), dreg[ks], dp);
     float ds[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -568,11 +569,11 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
       const float p = exp2f_fast(fmaf(s[r], a.scale_log2, -(ls + kill)));
       ds[r] = p * (dp[r] - dl) * a.scale;
     }
-    const bf16x8 sa = pack8(&ds[0]), sb8 = pack8(&ds[8]);
+    const ev8 sa = epack8(&ds[0]), sb8 = epack8(&ds[8]);
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      dq[db] = mfma32(cat_tr(lds_read_tr(kt, toff[0][db]), lds_read_tr(kt, toff[1][db])), sa, dq[db]);
-      dq[db] = mfma32(cat_tr(lds_read_tr(kt + 4096, toff[0][db]), lds_read_tr(kt + 4096, toff[1][db])), sb8, dq[db]);
+      dq[db] = emfma(ecat_tr(lds_read_tr(kt, toff[0][db]), lds_read_tr(kt, toff[1][db])), sa, dq[db]);
+      dq[db] = emfma(ecat_tr(lds_read_tr(kt + 4096, toff[0][db]), lds_read_tr(kt + 4096, toff[1][db])), sb8, dq[db]);
     }
     dma_wait();
     __syncthreads();
@@ -621,7 +622,7 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
       } else {
         if (a.add_a != nullptr) x += *reinterpret_cast<const f32x4*>(adq + c) * inv;
         ushort4 q4;
-        q4.x = f2bf(x[0]); q4.y = f2bf(x[1]); q4.z = f2bf(x[2]); q4.w = f2bf(x[3]);
+        q4.x = f2e(x[0]); q4.y = f2e(x[1]); q4.z = f2e(x[2]); q4.w = f2e(x[3]);
         *reinterpret_cast<ushort4*>(a.out_a + tok * HD + c) = q4;
       }
     }
@@ -643,9 +644,9 @@ static int vsa_check_qkv(const void* q, const void* k, const void* v, int BH, in
 
 static VsaFwdArgs fwd_args(const void* q, const void* k, const void* v, const int* blk_cnt, int BH, int L, int D) {
   VsaFwdArgs a = {};
-  a.q = (const bf16_t*)q;
-  a.k = (const bf16_t*)k;
-  a.v = (const bf16_t*)v;
+  a.q = (const e16_t*)q;
+  a.k = (const e16_t*)k;
+  a.v = (const e16_t*)v;
   a.blk_cnt = blk_cnt;
   a.L = L;
   a.NB = L / BK;
@@ -654,14 +655,14 @@ static VsaFwdArgs fwd_args(const void* q, const void* k, const void* v, const in
   return a;
 }
 
-extern "C" int vsa_attn_fwd(const void* q, const void* k, const void* v, const int* row_ptr, const int* col_idx,
+extern "C" int ES_VSA_API(vsa_attn_fwd)(const void* q, const void* k, const void* v, const int* row_ptr, const int* col_idx,
                             const int* blk_cnt, void* out, float* lse, int BH, int L, int D, hipStream_t stream) {
   if (int st = vsa_check_qkv(q, k, v, BH, L, D)) return st;
   ES_REQUIRE(row_ptr && blk_cnt && out && lse, ES_ERR_INVALID, "VSA: null tensor pointer");
   VsaFwdArgs a = fwd_args(q, k, v, blk_cnt, BH, L, D);
   a.row_ptr = row_ptr;
   a.col_idx = col_idx;
-  a.out = (bf16_t*)out;
+  a.out = (e16_t*)out;
   a.lse = lse;
   a.per_xcd = (a.NB + 7) / 8;
   const long long grid = 8LL * BH * a.per_xcd;
@@ -670,7 +671,7 @@ extern "C" int vsa_attn_fwd(const void* q, const void* k, const void* v, const i
   return check_launch("vsa_attn_fwd");
 }
 
-extern "C" int vsa_attn_fwd_tasks(const void* q, const void* k, const void* v, const int* col_idx,
+extern "C" int ES_VSA_API(vsa_attn_fwd_tasks)(const void* q, const void* k, const void* v, const int* col_idx,
                                   const int* blk_cnt, const int* tasks, const int* info, int max_tasks, void* out,
                                   float* lse, float* part_o, float* part_lse, int BH, int L, int D,
                                   hipStream_t stream) {
@@ -683,7 +684,7 @@ extern "C" int vsa_attn_fwd_tasks(const void* q, const void* k, const void* v, c
   a.col_idx = col_idx;
   a.tasks = (const int4*)tasks;
   a.info = info;
-  a.out = (bf16_t*)out;
+  a.out = (e16_t*)out;
   a.lse = lse;
   a.part_o = part_o;
   a.part_lse = part_lse;
@@ -695,10 +696,10 @@ extern "C" int vsa_attn_fwd_tasks(const void* q, const void* k, const void* v, c
 static VsaBwdArgs bwd_args(const void* q, const void* k, const void* v, const void* dout, const float* lse,
                            const float* delta, const int* blk_cnt, int BH, int L, int D) {
   VsaBwdArgs a = {};
-  a.q = (const bf16_t*)q;
-  a.k = (const bf16_t*)k;
-  a.v = (const bf16_t*)v;
-  a.dout = (const bf16_t*)dout;
+  a.q = (const e16_t*)q;
+  a.k = (const e16_t*)k;
+  a.v = (const e16_t*)v;
+  a.dout = (const e16_t*)dout;
   a.lse = lse;
   a.delta = delta;
   a.blk_cnt = blk_cnt;
@@ -711,7 +712,7 @@ static VsaBwdArgs bwd_args(const void* q, const void* k, const void* v, const vo
   return a;
 }
 
-extern "C" int vsa_attn_bwd_kv(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+extern "C" int ES_VSA_API(vsa_attn_bwd_kv)(const void* q, const void* k, const void* v, const void* dout, const float* lse,
                                const float* delta, const int* k2q_ptr, const int* k2q_idx, const int* blk_cnt,
                                const float* add_dk, const float* add_dv, int add_nb, void* dk, void* dv,
                                int out_fp32, int BH, int L, int D, hipStream_t stream) {
@@ -729,8 +730,8 @@ extern "C" int vsa_attn_bwd_kv(const void* q, const void* k, const void* v, cons
     a.out_a32 = (float*)dk;
     a.out_b32 = (float*)dv;
   } else {
-    a.out_a = (bf16_t*)dk;
-    a.out_b = (bf16_t*)dv;
+    a.out_a = (e16_t*)dk;
+    a.out_b = (e16_t*)dv;
   }
   const long long grid = 8LL * BH * a.per_xcd;
   ES_REQUIRE(grid < (1LL << 31), ES_ERR_UNSUPPORTED, "VSA: grid too large");
@@ -738,7 +739,7 @@ extern "C" int vsa_attn_bwd_kv(const void* q, const void* k, const void* v, cons
   return check_launch("vsa_attn_bwd_kv");
 }
 
-extern "C" int vsa_attn_bwd_kv_tasks(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+extern "C" int ES_VSA_API(vsa_attn_bwd_kv_tasks)(const void* q, const void* k, const void* v, const void* dout, const float* lse,
                                      const float* delta, const int* k2q_idx, const int* blk_cnt, const int* tasks,
                                      const int* info, int max_tasks, const float* add_dk, const float* add_dv,
                                      int add_nb, void* dk, void* dv, float* part_dk, float* part_dv, int BH, int L,
@@ -754,15 +755,15 @@ extern "C" int vsa_attn_bwd_kv_tasks(const void* q, const void* k, const void* v
   a.add_a = add_dk;
   a.add_b = add_dv;
   a.add_nb = add_nb;
-  a.out_a = (bf16_t*)dk;
-  a.out_b = (bf16_t*)dv;
+  a.out_a = (e16_t*)dk;
+  a.out_b = (e16_t*)dv;
   a.part_a = part_dk;
   a.part_b = part_dv;
   hipLaunchKernelGGL(vsa_bwd_kv_kernel<true>, dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
   return check_launch("vsa_attn_bwd_kv_tasks");
 }
 
-extern "C" int vsa_attn_bwd_q(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+extern "C" int ES_VSA_API(vsa_attn_bwd_q)(const void* q, const void* k, const void* v, const void* dout, const float* lse,
                               const float* delta, const int* q2k_ptr, const int* q2k_idx, const int* blk_cnt,
                               const float* add_dq, int add_nb, void* dq, float* dq_acc, int BH, int L, int D,
                               hipStream_t stream) {
@@ -774,7 +775,7 @@ extern "C" int vsa_attn_bwd_q(const void* q, const void* k, const void* v, const
   a.col_idx = q2k_idx;
   a.add_a = add_dq;
   a.add_nb = add_nb;
-  a.out_a = (bf16_t*)dq;
+  a.out_a = (e16_t*)dq;
   a.out_a32 = dq_acc;
   const long long grid = 8LL * BH * a.per_xcd;
   ES_REQUIRE(grid < (1LL << 31), ES_ERR_UNSUPPORTED, "VSA: grid too large");
@@ -782,7 +783,7 @@ extern "C" int vsa_attn_bwd_q(const void* q, const void* k, const void* v, const
   return check_launch("vsa_attn_bwd_q");
 }
 
-extern "C" int vsa_attn_bwd_q_tasks(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+extern "C" int ES_VSA_API(vsa_attn_bwd_q_tasks)(const void* q, const void* k, const void* v, const void* dout, const float* lse,
                                     const float* delta, const int* q2k_idx, const int* blk_cnt, const int* tasks,
                                     const int* info, int max_tasks, const float* add_dq, int add_nb, void* dq,
                                     float* part_dq, int BH, int L, int D, hipStream_t stream) {
@@ -796,7 +797,7 @@ extern "C" int vsa_attn_bwd_q_tasks(const void* q, const void* k, const void* v,
   a.info = info;
   a.add_a = add_dq;
   a.add_nb = add_nb;
-  a.out_a = (bf16_t*)dq;
+  a.out_a = (e16_t*)dq;
   a.part_a = part_dq;
   hipLaunchKernelGGL(vsa_bwd_q_kernel<true>, dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
   return check_launch("vsa_attn_bwd_q_tasks");

@@ -14,27 +14,28 @@
 //   finalize_kernel  reference csrc/vsa/fuse.cu:9 (dX = acc + add[blk] / cnt on valid rows, 0 elsewhere)
 #include "../../include/vsa_hip.h"
 #include "common.h"
+#include "elem.h"
 
 namespace es {
 
 namespace {
 
-__device__ __forceinline__ void ld8(const bf16_t* p, float* x) {
+__device__ __forceinline__ void ld8(const e16_t* p, float* x) {
   const uint4 u = *reinterpret_cast<const uint4*>(p);
   const unsigned w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    x[2 * i] = __uint_as_float(w[i] << 16);
-    x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    x[2 * i] = e2f((e16_t)(w[i] & 0xffffu));
+    x[2 * i + 1] = e2f((e16_t)(w[i] >> 16));
   }
 }
 
-__device__ __forceinline__ void st8(bf16_t* p, const float* x) {
+__device__ __forceinline__ void st8(e16_t* p, const float* x) {
   uint4 u;
-  u.x = (unsigned)f2bf(x[0]) | ((unsigned)f2bf(x[1]) << 16);
-  u.y = (unsigned)f2bf(x[2]) | ((unsigned)f2bf(x[3]) << 16);
-  u.z = (unsigned)f2bf(x[4]) | ((unsigned)f2bf(x[5]) << 16);
-  u.w = (unsigned)f2bf(x[6]) | ((unsigned)f2bf(x[7]) << 16);
+  u.x = (unsigned)f2e(x[0]) | ((unsigned)f2e(x[1]) << 16);
+  u.y = (unsigned)f2e(x[2]) | ((unsigned)f2e(x[3]) << 16);
+  u.z = (unsigned)f2e(x[4]) | ((unsigned)f2e(x[5]) << 16);
+  u.w = (unsigned)f2e(x[6]) | ((unsigned)f2e(x[7]) << 16);
   *reinterpret_cast<uint4*>(p) = u;
 }
 
@@ -50,9 +51,9 @@ __device__ __forceinline__ float row16_sum(float x) {
 }
 
 struct PoolArgs {
-  const bf16_t* src[3];  // q, k, v
-  bf16_t* grp[3];        // qr, kr, vr (any may be null)
-  bf16_t* blk[3];        // qc, kc, vc
+  const e16_t* src[3];  // q, k, v
+  e16_t* grp[3];        // qr, kr, vr (any may be null)
+  e16_t* blk[3];        // qc, kc, vc
   const int* blk_cnt;
   int NB, L, R, G, Lr_pad, NBc_pad;
 };
@@ -68,8 +69,8 @@ __global__ __launch_bounds__(192) void pool_kernel(PoolArgs a) {
   if (blk >= a.NB || a.src[which] == nullptr) return;  // a null source: that tensor is not pooled
   const size_t bh = blockIdx.y;
   const int n = a.blk_cnt[blk];
-  const bf16_t* src = a.src[which] + (bh * a.L + (size_t)blk * BK) * HD + c8;
-  bf16_t* grp = a.grp[which];
+  const e16_t* src = a.src[which] + (bh * a.L + (size_t)blk * BK) * HD + c8;
+  e16_t* grp = a.grp[which];
   float tot[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int g = 0; g < a.G; ++g) {
     const int r0 = g * a.R, r1 = min(r0 + a.R, n);
@@ -84,7 +85,7 @@ __global__ __launch_bounds__(192) void pool_kernel(PoolArgs a) {
       const float inv = r1 > r0 ? 1.f / (float)(r1 - r0) : 0.f;
       float m[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) m[e] = s[e] * inv;
+      for (int e = 0; e < 8; ++e) m[e] = mul_rn(s[e], inv);
       st8(grp + (bh * a.Lr_pad + (size_t)blk * a.G + g) * HD + c8, m);
     }
 #pragma unroll
@@ -92,14 +93,14 @@ __global__ __launch_bounds__(192) void pool_kernel(PoolArgs a) {
   }
   const float inv = 1.f / (float)n;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) tot[e] *= inv;
+  for (int e = 0; e < 8; ++e) tot[e] = mul_rn(tot[e], inv);
   st8(a.blk[which] + (bh * a.NBc_pad + blk) * HD + c8, tot);
 }
 
 // lane -> (row slot s = lane / 16, column chunk c8 = 8 * (lane % 16)); the slot walks rows s, s + 4, ..., s + 60
 struct FuseArgs {
-  const bf16_t *dout, *of, *oc, *gate;
-  bf16_t *o, *dout_f, *dout_c, *dgate;
+  const e16_t *dout, *of, *oc, *gate;
+  e16_t *o, *dout_f, *dout_c, *dgate;
   float *delta_f, *delta_c;
   const int* blk_cnt;
   int NB, L, NBc_pad, gate_mode, gate_act;
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(256) void fuse_fwd_kernel(FuseArgs a) {
     if (r < n) {
       ld8(a.of + tok * HD + c8, x);
       if (a.gate_mode == 1) {
-        const float g = gact(bf2f(a.gate[tok]), a.gate_act);
+        const float g = gact(e2f(a.gate[tok]), a.gate_act);
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] += g * c[e];
       } else if (a.gate_mode == 2) {
@@ -162,7 +163,7 @@ __global__ __launch_bounds__(256) void fuse_bwd_kernel(FuseArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) dot_f += d[e] * f[e];
     if (a.gate_mode == 1) {
-      const float g = valid ? gact(bf2f(a.gate[tok]), a.gate_act) : 0.f;
+      const float g = valid ? gact(e2f(a.gate[tok]), a.gate_act) : 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         dot_c += d[e] * c[e];
@@ -187,7 +188,7 @@ __global__ __launch_bounds__(256) void fuse_bwd_kernel(FuseArgs a) {
     dot_c = row16_sum(dot_c);
     if ((l & 15) == 0) {
       a.delta_f[tok] = valid ? dot_f : 0.f;
-      if (a.gate_mode == 1) a.dgate[tok] = f2bf(valid ? dot_c : 0.f);
+      if (a.gate_mode == 1) a.dgate[tok] = f2e(valid ? dot_c : 0.f);
     }
   }
   // dO_c = the four row slots' column sums (fixed order), rounded; delta_c = <dO_c (rounded), O_c>
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(256) void fuse_bwd_kernel(FuseArgs a) {
   if (s == 0) {
     st8(a.dout_c + crow + c8, dc);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) part += bf2f(f2bf(dc[e])) * c[e];
+    for (int e = 0; e < 8; ++e) part += e2f(f2e(dc[e])) * c[e];
   }
   part = row16_sum(part);
   if (l == 0) a.delta_c[bh * a.NBc_pad + blk] = part;
@@ -209,7 +210,7 @@ __global__ __launch_bounds__(256) void fuse_bwd_kernel(FuseArgs a) {
 // grid (cdiv(NB, 4), BH), 256 threads: one wave per 64-token block; acc fp32 [BH, L, D] (optional), add fp32
 // [BH, add_nb, D] (optional)
 __global__ __launch_bounds__(256) void finalize_kernel(const float* __restrict__ acc, const float* __restrict__ add,
-                                                       bf16_t* __restrict__ out, const int* __restrict__ blk_cnt,
+                                                       e16_t* __restrict__ out, const int* __restrict__ blk_cnt,
                                                        int NB, int L, int add_nb) {
   const int blk = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (blk >= NB) return;
@@ -267,21 +268,21 @@ static int check_tokens(int BH, int L, int D) {
   return ES_OK;
 }
 
-extern "C" int vsa_pool(const void* q, const void* k, const void* v, const int* blk_cnt, void* qr, void* kr, void* vr,
+extern "C" int ES_VSA_API(vsa_pool)(const void* q, const void* k, const void* v, const int* blk_cnt, void* qr, void* kr, void* vr,
                         void* qc, void* kc, void* vc, int BH, int L, int D, int R, hipStream_t stream) {
   if (int st = check_tokens(BH, L, D)) return st;
   ES_REQUIRE(q && k && v && blk_cnt && qc && kc && vc, ES_ERR_INVALID, "VSA: null tensor pointer");
   ES_REQUIRE(R == 4 || R == 8 || R == 16 || R == 32, ES_ERR_INVALID, "VSA2: router pool size R must be 4, 8, 16 or 32");
   const int NB = L / BK, G = BK / R;
-  PoolArgs a{{(const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v},
-             {(bf16_t*)qr, (bf16_t*)kr, (bf16_t*)vr},
-             {(bf16_t*)qc, (bf16_t*)kc, (bf16_t*)vc},
+  PoolArgs a{{(const e16_t*)q, (const e16_t*)k, (const e16_t*)v},
+             {(e16_t*)qr, (e16_t*)kr, (e16_t*)vr},
+             {(e16_t*)qc, (e16_t*)kc, (e16_t*)vc},
              blk_cnt, NB, L, R, G, (NB * G + 63) / 64 * 64, (NB + 63) / 64 * 64};
   hipLaunchKernelGGL(pool_kernel, dim3((NB + POOL_BLOCKS - 1) / POOL_BLOCKS, BH), dim3(192), 0, stream, a);
   return check_launch("vsa_pool");
 }
 
-extern "C" int vsa_fuse_fwd(const void* of, const void* oc, const void* gate, void* o, const int* blk_cnt, int BH,
+extern "C" int ES_VSA_API(vsa_fuse_fwd)(const void* of, const void* oc, const void* gate, void* o, const int* blk_cnt, int BH,
                             int L, int D, int NBc_pad, int gate_mode, int gate_act, hipStream_t stream) {
   if (int st = check_tokens(BH, L, D)) return st;
   ES_REQUIRE(of && oc && o && blk_cnt && (gate_mode == 0 || gate), ES_ERR_INVALID, "VSA: null tensor pointer");
@@ -289,13 +290,13 @@ extern "C" int vsa_fuse_fwd(const void* of, const void* oc, const void* gate, vo
              "VSA: gate_mode must be 0 (none), 1 (per token) or 2 (elementwise), gate_act 0 (tanh) or 1 (identity)");
   const int NB = L / BK;
   ES_REQUIRE(NBc_pad >= NB, ES_ERR_INVALID, "VSA: coarse output has fewer rows than blocks");
-  FuseArgs a{nullptr, (const bf16_t*)of, (const bf16_t*)oc, (const bf16_t*)gate, (bf16_t*)o, nullptr, nullptr, nullptr,
+  FuseArgs a{nullptr, (const e16_t*)of, (const e16_t*)oc, (const e16_t*)gate, (e16_t*)o, nullptr, nullptr, nullptr,
              nullptr, nullptr, blk_cnt, NB, L, NBc_pad, gate_mode, gate_act};
   hipLaunchKernelGGL(fuse_fwd_kernel, dim3((NB + 3) / 4, BH), dim3(256), 0, stream, a);
   return check_launch("vsa_fuse_fwd");
 }
 
-extern "C" int vsa_fuse_bwd(const void* dout, const void* of, const void* oc, const void* gate, void* dout_f,
+extern "C" int ES_VSA_API(vsa_fuse_bwd)(const void* dout, const void* of, const void* oc, const void* gate, void* dout_f,
                             float* delta_f, void* dout_c, float* delta_c, void* dgate, const int* blk_cnt, int BH,
                             int L, int D, int NBc_pad, int gate_mode, int gate_act, hipStream_t stream) {
   if (int st = check_tokens(BH, L, D)) return st;
@@ -305,24 +306,24 @@ extern "C" int vsa_fuse_bwd(const void* dout, const void* of, const void* oc, co
   ES_REQUIRE(gate_mode == 0 || (gate && dgate), ES_ERR_INVALID, "VSA: a gated fusion needs gate and dgate");
   const int NB = L / BK;
   ES_REQUIRE(NBc_pad >= NB, ES_ERR_INVALID, "VSA: coarse output has fewer rows than blocks");
-  FuseArgs a{(const bf16_t*)dout, (const bf16_t*)of, (const bf16_t*)oc, (const bf16_t*)gate, nullptr, (bf16_t*)dout_f,
-             (bf16_t*)dout_c, (bf16_t*)dgate, delta_f, delta_c, blk_cnt, NB, L, NBc_pad, gate_mode, gate_act};
+  FuseArgs a{(const e16_t*)dout, (const e16_t*)of, (const e16_t*)oc, (const e16_t*)gate, nullptr, (e16_t*)dout_f,
+             (e16_t*)dout_c, (e16_t*)dgate, delta_f, delta_c, blk_cnt, NB, L, NBc_pad, gate_mode, gate_act};
   hipLaunchKernelGGL(fuse_bwd_kernel, dim3((NB + 3) / 4, BH), dim3(256), 0, stream, a);
   return check_launch("vsa_fuse_bwd");
 }
 
-extern "C" int vsa_finalize(const float* acc, const float* add, int add_nb, void* out, const int* blk_cnt, int BH,
+extern "C" int ES_VSA_API(vsa_finalize)(const float* acc, const float* add, int add_nb, void* out, const int* blk_cnt, int BH,
                             int L, int D, hipStream_t stream) {
   if (int st = check_tokens(BH, L, D)) return st;
   ES_REQUIRE(out && blk_cnt, ES_ERR_INVALID, "VSA: null tensor pointer");
   const int NB = L / BK;
   ES_REQUIRE(add == nullptr || add_nb >= NB, ES_ERR_INVALID, "VSA: finalize add has fewer rows than blocks");
-  hipLaunchKernelGGL(finalize_kernel, dim3((NB + 3) / 4, BH), dim3(256), 0, stream, acc, add, (bf16_t*)out, blk_cnt,
+  hipLaunchKernelGGL(finalize_kernel, dim3((NB + 3) / 4, BH), dim3(256), 0, stream, acc, add, (e16_t*)out, blk_cnt,
                      NB, L, add_nb);
   return check_launch("vsa_finalize");
 }
 
-extern "C" int vsa_rep_build(const void* k, const void* v, const int* blk_cnt, void* k_mid, void* v_mid,
+extern "C" int ES_VSA_API(vsa_rep_build)(const void* k, const void* v, const int* blk_cnt, void* k_mid, void* v_mid,
                              float* lc_mid, void* k_tail, void* v_tail, float* lc_tail, int BH, int L, int D, int RM,
                              hipStream_t stream) {
   if (int st = check_tokens(BH, L, D)) return st;
@@ -332,9 +333,9 @@ extern "C" int vsa_rep_build(const void* k, const void* v, const int* blk_cnt, v
              "RepTiers.mid_reps must be one of (1, 2, 4, 8, 16)");
   const int NB = L / BK, R = BK / RM;
   // the mid table is the pooled groups of R = 64 / RM tokens, the tail table the block means
-  PoolArgs a{{nullptr, (const bf16_t*)k, (const bf16_t*)v},
-             {nullptr, (bf16_t*)k_mid, (bf16_t*)v_mid},
-             {nullptr, (bf16_t*)k_tail, (bf16_t*)v_tail},
+  PoolArgs a{{nullptr, (const e16_t*)k, (const e16_t*)v},
+             {nullptr, (e16_t*)k_mid, (e16_t*)v_mid},
+             {nullptr, (e16_t*)k_tail, (e16_t*)v_tail},
              blk_cnt, NB, L, R, RM, (NB * RM + 63) / 64 * 64, (NB + 63) / 64 * 64};
   hipLaunchKernelGGL(pool_kernel, dim3((NB + POOL_BLOCKS - 1) / POOL_BLOCKS, BH), dim3(192), 0, stream, a);
   hipLaunchKernelGGL(rep_counts_kernel, dim3((NB * RM + 255) / 256), dim3(256), 0, stream, blk_cnt, lc_mid, lc_tail,

@@ -20,6 +20,7 @@
 //                       means), tier_b_lists_kernel (A|B lists minus tier A), row_dot_kernel (delta).
 #include "../../include/vsa_hip.h"
 #include "common.h"
+#include "elem.h"
 
 namespace es {
 
@@ -31,11 +32,11 @@ constexpr int REP_MAX_NB = 2048;
 enum { PH_A = 1, PH_B = 2, PH_C = 4 };
 
 struct RepArgs {
-  const bf16_t *q, *k, *v, *dout;
-  const bf16_t *k_mid, *v_mid, *k_tail, *v_tail;
+  const e16_t *q, *k, *v, *dout;
+  const e16_t *k_mid, *v_mid, *k_tail, *v_tail;
   const float *lc_mid, *lc_tail;
   const float *lse, *delta;
-  bf16_t* out;
+  e16_t* out;
   float* lse_out;
   const int *row_ptr, *col_idx, *blk_cnt;
   const unsigned *bits_a, *bits_ab;
@@ -185,11 +186,11 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
     return row < 0 ? -INFINITY : (tb ? a.lc_mid[row] : a.lc_tail[row]);
   };
 
-  bf16x8 qreg[8], dreg[8];
+  ev8 qreg[8], dreg[8];
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
-    qreg[ks] = *reinterpret_cast<const bf16x8*>(a.q + tok * HD + 16 * ks + 8 * hi);
-    if (BWD) dreg[ks] = *reinterpret_cast<const bf16x8*>(a.dout + tok * HD + 16 * ks + 8 * hi);
+    qreg[ks] = *reinterpret_cast<const ev8*>(a.q + tok * HD + 16 * ks + 8 * hi);
+    if (BWD) dreg[ks] = *reinterpret_cast<const ev8*>(a.dout + tok * HD + 16 * ks + 8 * hi);
   }
   float ls = 0.0f, dl = 0.0f;
   if (BWD) {
@@ -228,7 +229,7 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
     const char* vt = kv_s[sb][1];
     f32x16 s = {};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) s = mfma32(lds_read16(kt, koff[ks]), qreg[ks], s);
+    for (int ks = 0; ks < 8; ++ks) s = emfma(elds16(kt, koff[ks]), qreg[ks], s);
     float x[16];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -254,25 +255,25 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
       const float msub = mref == -INFINITY ? 0.0f : mref;
 #pragma unroll
       for (int r = 0; r < 16; ++r) x[r] = exp2f_fast(x[r] - msub);
-      const bf16x8 pa = pack8(&x[0]), pb = pack8(&x[8]);
-      lsum += sum8_bf16(pb, sum8_bf16(pa, 0.0f));
+      const ev8 pa = epack8(&x[0]), pb = epack8(&x[8]);
+      lsum += esum8(pb, esum8(pa, 0.0f));
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        acc[db] = mfma32(cat_tr(lds_read_tr(vt, toff[0][db]), lds_read_tr(vt, toff[1][db])), pa, acc[db]);
-        acc[db] = mfma32(cat_tr(lds_read_tr(vt + 4096, toff[0][db]), lds_read_tr(vt + 4096, toff[1][db])), pb, acc[db]);
+        acc[db] = emfma(ecat_tr(lds_read_tr(vt, toff[0][db]), lds_read_tr(vt, toff[1][db])), pa, acc[db]);
+        acc[db] = emfma(ecat_tr(lds_read_tr(vt + 4096, toff[0][db]), lds_read_tr(vt + 4096, toff[1][db])), pb, acc[db]);
       }
     } else {
       f32x16 dp = {};
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) dp = mfma32(lds_read16(vt, koff[ks]), dreg[ks], dp);
+      for (int ks = 0; ks < 8; ++ks) dp = emfma(elds16(vt, koff[ks]), dreg[ks], dp);
       float ds[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) ds[r] = exp2f_fast(x[r] - ls) * (dp[r] - dl) * a.scale;
-      const bf16x8 sa = pack8(&ds[0]), sb8 = pack8(&ds[8]);
+      const ev8 sa = epack8(&ds[0]), sb8 = epack8(&ds[8]);
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        acc[db] = mfma32(cat_tr(lds_read_tr(kt, toff[0][db]), lds_read_tr(kt, toff[1][db])), sa, acc[db]);
-        acc[db] = mfma32(cat_tr(lds_read_tr(kt + 4096, toff[0][db]), lds_read_tr(kt + 4096, toff[1][db])), sb8,
+        acc[db] = emfma(ecat_tr(lds_read_tr(kt, toff[0][db]), lds_read_tr(kt, toff[1][db])), sa, acc[db]);
+        acc[db] = emfma(ecat_tr(lds_read_tr(kt + 4096, toff[0][db]), lds_read_tr(kt + 4096, toff[1][db])), sb8,
                          acc[db]);
       }
     }
@@ -324,7 +325,7 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
       }
       if (BWD && adq != nullptr) x += *reinterpret_cast<const f32x4*>(adq + c) * inv_cnt;
       ushort4 u;
-      u.x = f2bf(x[0]); u.y = f2bf(x[1]); u.z = f2bf(x[2]); u.w = f2bf(x[3]);
+      u.x = f2e(x[0]); u.y = f2e(x[1]); u.z = f2e(x[2]); u.w = f2e(x[3]);
       *reinterpret_cast<ushort4*>(a.out + tok * HD + c) = u;
     }
   if (!BWD && hi == 0) a.lse_out[tok] = live ? lse2 * LN2_F : -INFINITY;
@@ -332,8 +333,8 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
 
 // ------------------------------------------------------------------------------------------------ table dK / dV
 struct TabArgs {
-  const bf16_t *q, *dout;
-  const bf16_t *k_tab, *v_tab;  // [BH, rows_pad, D]
+  const e16_t *q, *dout;
+  const e16_t *k_tab, *v_tab;  // [BH, rows_pad, D]
   const float* lc;              // [rows]
   const float *lse, *delta;
   const unsigned *bits_a, *bits_ab;
@@ -389,11 +390,11 @@ __global__ __launch_bounds__(256, 1) void rep_bwd_tab_kernel(TabArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) dma16(rv, v_s + wv * 4096 + i * 1024, ld_off[i], (unsigned)grp * (BK * 256));
   }
-  bf16x8 kreg[8];
+  ev8 kreg[8];
   {
-    const bf16_t* kp = a.k_tab + ((size_t)bh * a.rows_pad + trow) * HD + 8 * hi;
+    const e16_t* kp = a.k_tab + ((size_t)bh * a.rows_pad + trow) * HD + 8 * hi;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) kreg[ks] = *reinterpret_cast<const bf16x8*>(kp + 16 * ks);
+    for (int ks = 0; ks < 8; ++ks) kreg[ks] = *reinterpret_cast<const ev8*>(kp + 16 * ks);
   }
   auto issue = [&](int i, int sb, float& ls, float& dl) {
     const unsigned soff = (unsigned)i * (BK * 256);
@@ -464,9 +465,9 @@ __global__ __launch_bounds__(256, 1) void rep_bwd_tab_kernel(TabArgs a) {
     const char* dt = qd_s[sb][1];
     f32x16 s = {}, dp = {};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) s = mfma32(lds_read16(qt, aoff[ks]), kreg[ks], s);
+    for (int ks = 0; ks < 8; ++ks) s = emfma(elds16(qt, aoff[ks]), kreg[ks], s);
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) dp = mfma32(lds_read16(dt, aoff[ks]), lds_read16(v_s, boff[ks]), dp);
+    for (int ks = 0; ks < 8; ++ks) dp = emfma(elds16(dt, aoff[ks]), elds16(v_s, boff[ks]), dp);
     float p[16], ds[16];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -479,14 +480,14 @@ __global__ __launch_bounds__(256, 1) void rep_bwd_tab_kernel(TabArgs a) {
         ds[r] = p[r] * (dp[r] - d4[e]) * a.scale;
       }
     }
-    const bf16x8 pa = pack8(&p[0]), pb = pack8(&p[8]);
-    const bf16x8 sa = pack8(&ds[0]), sb8 = pack8(&ds[8]);
+    const ev8 pa = epack8(&p[0]), pb = epack8(&p[8]);
+    const ev8 sa = epack8(&ds[0]), sb8 = epack8(&ds[8]);
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      dv[db] = mfma32(cat_tr(lds_read_tr(dt, toff[0][db]), lds_read_tr(dt, toff[1][db])), pa, dv[db]);
-      dv[db] = mfma32(cat_tr(lds_read_tr(dt + 4096, toff[0][db]), lds_read_tr(dt + 4096, toff[1][db])), pb, dv[db]);
-      dk[db] = mfma32(cat_tr(lds_read_tr(qt, toff[0][db]), lds_read_tr(qt, toff[1][db])), sa, dk[db]);
-      dk[db] = mfma32(cat_tr(lds_read_tr(qt + 4096, toff[0][db]), lds_read_tr(qt + 4096, toff[1][db])), sb8, dk[db]);
+      dv[db] = emfma(ecat_tr(lds_read_tr(dt, toff[0][db]), lds_read_tr(dt, toff[1][db])), pa, dv[db]);
+      dv[db] = emfma(ecat_tr(lds_read_tr(dt + 4096, toff[0][db]), lds_read_tr(dt + 4096, toff[1][db])), pb, dv[db]);
+      dk[db] = emfma(ecat_tr(lds_read_tr(qt, toff[0][db]), lds_read_tr(qt, toff[1][db])), sa, dk[db]);
+      dk[db] = emfma(ecat_tr(lds_read_tr(qt + 4096, toff[0][db]), lds_read_tr(qt + 4096, toff[1][db])), sb8, dk[db]);
     }
     dma_wait();
     if (inext < a.NB && wv == 0) {
@@ -536,8 +537,8 @@ __global__ __launch_bounds__(256, 1) void rep_bwd_tab_kernel(TabArgs a) {
 __global__ __launch_bounds__(256) void rep_unpool_kernel(const float* __restrict__ acc_k, const float* __restrict__ acc_v,
                                                          const float* __restrict__ dk_mid, const float* __restrict__ dv_mid,
                                                          const float* __restrict__ dk_tail,
-                                                         const float* __restrict__ dv_tail, bf16_t* __restrict__ dk,
-                                                         bf16_t* __restrict__ dv, const int* __restrict__ blk_cnt,
+                                                         const float* __restrict__ dv_tail, e16_t* __restrict__ dk,
+                                                         e16_t* __restrict__ dv, const int* __restrict__ blk_cnt,
                                                          int L, int NB, int RM, int mid_rows, int tail_rows) {
   const int blk = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (blk >= NB) return;
@@ -566,21 +567,21 @@ __global__ __launch_bounds__(256) void rep_unpool_kernel(const float* __restrict
       }
     }
     uint4 uk, uv;
-    uk.x = (unsigned)f2bf(xk[0]) | ((unsigned)f2bf(xk[1]) << 16);
-    uk.y = (unsigned)f2bf(xk[2]) | ((unsigned)f2bf(xk[3]) << 16);
-    uk.z = (unsigned)f2bf(xk[4]) | ((unsigned)f2bf(xk[5]) << 16);
-    uk.w = (unsigned)f2bf(xk[6]) | ((unsigned)f2bf(xk[7]) << 16);
-    uv.x = (unsigned)f2bf(xv[0]) | ((unsigned)f2bf(xv[1]) << 16);
-    uv.y = (unsigned)f2bf(xv[2]) | ((unsigned)f2bf(xv[3]) << 16);
-    uv.z = (unsigned)f2bf(xv[4]) | ((unsigned)f2bf(xv[5]) << 16);
-    uv.w = (unsigned)f2bf(xv[6]) | ((unsigned)f2bf(xv[7]) << 16);
+    uk.x = (unsigned)f2e(xk[0]) | ((unsigned)f2e(xk[1]) << 16);
+    uk.y = (unsigned)f2e(xk[2]) | ((unsigned)f2e(xk[3]) << 16);
+    uk.z = (unsigned)f2e(xk[4]) | ((unsigned)f2e(xk[5]) << 16);
+    uk.w = (unsigned)f2e(xk[6]) | ((unsigned)f2e(xk[7]) << 16);
+    uv.x = (unsigned)f2e(xv[0]) | ((unsigned)f2e(xv[1]) << 16);
+    uv.y = (unsigned)f2e(xv[2]) | ((unsigned)f2e(xv[3]) << 16);
+    uv.z = (unsigned)f2e(xv[4]) | ((unsigned)f2e(xv[5]) << 16);
+    uv.w = (unsigned)f2e(xv[6]) | ((unsigned)f2e(xv[7]) << 16);
     *reinterpret_cast<uint4*>(dk + tok) = uk;
     *reinterpret_cast<uint4*>(dv + tok) = uv;
   }
 }
 
 // delta[row] = <dO, O> on valid rows, 0 on padding; one wave per block, 16 lanes per token row
-__global__ __launch_bounds__(256) void row_dot_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ y,
+__global__ __launch_bounds__(256) void row_dot_kernel(const e16_t* __restrict__ x, const e16_t* __restrict__ y,
                                                       float* __restrict__ out, const int* __restrict__ blk_cnt, int L,
                                                       int NB) {
   const int blk = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -597,8 +598,8 @@ __global__ __launch_bounds__(256) void row_dot_kernel(const bf16_t* __restrict__
       const unsigned wx[4] = {ux.x, ux.y, ux.z, ux.w}, wy[4] = {uy.x, uy.y, uy.z, uy.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        acc += __uint_as_float(wx[i] << 16) * __uint_as_float(wy[i] << 16) +
-               __uint_as_float(wx[i] & 0xffff0000u) * __uint_as_float(wy[i] & 0xffff0000u);
+        acc += e2f((e16_t)(wx[i] & 0xffffu)) * e2f((e16_t)(wy[i] & 0xffffu)) +
+               e2f((e16_t)(wx[i] >> 16)) * e2f((e16_t)(wy[i] >> 16));
     }
 #pragma unroll
     for (int m = 1; m < 16; m <<= 1) acc += __shfl_xor(acc, m, 16);
@@ -657,14 +658,14 @@ static RepArgs rep_args(const void* q, const void* k, const void* v, const void*
                         const int* q2k_ptr, const int* q2k_idx, const unsigned* bits_a, const unsigned* bits_ab,
                         const int* blk_cnt, int BH, int L, int D, int RM, int phases) {
   RepArgs a = {};
-  a.q = (const bf16_t*)q;
-  a.k = (const bf16_t*)k;
-  a.v = (const bf16_t*)v;
-  a.k_mid = (const bf16_t*)k_mid;
-  a.v_mid = (const bf16_t*)v_mid;
+  a.q = (const e16_t*)q;
+  a.k = (const e16_t*)k;
+  a.v = (const e16_t*)v;
+  a.k_mid = (const e16_t*)k_mid;
+  a.v_mid = (const e16_t*)v_mid;
   a.lc_mid = lc_mid;
-  a.k_tail = (const bf16_t*)k_tail;
-  a.v_tail = (const bf16_t*)v_tail;
+  a.k_tail = (const e16_t*)k_tail;
+  a.v_tail = (const e16_t*)v_tail;
   a.lc_tail = lc_tail;
   a.row_ptr = q2k_ptr;
   a.col_idx = q2k_idx;
@@ -685,7 +686,7 @@ static RepArgs rep_args(const void* q, const void* k, const void* v, const void*
   return a;
 }
 
-extern "C" int vsa_rep_attn_fwd(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
+extern "C" int ES_VSA_API(vsa_rep_attn_fwd)(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
                                 const float* lc_mid, const void* k_tail, const void* v_tail, const float* lc_tail,
                                 const int* q2k_ptr, const int* q2k_idx, const unsigned* bits_a,
                                 const unsigned* bits_ab, const int* blk_cnt, void* out, float* lse, int BH, int L,
@@ -697,13 +698,13 @@ extern "C" int vsa_rep_attn_fwd(const void* q, const void* k, const void* v, con
   ES_REQUIRE(phases >= 0 && phases <= 7, ES_ERR_INVALID, "VSA2-rep: phases must be a mask of 1 | 2 | 4");
   RepArgs a = rep_args(q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, q2k_ptr, q2k_idx, bits_a, bits_ab,
                        blk_cnt, BH, L, D, RM, phases);
-  a.out = (bf16_t*)out;
+  a.out = (e16_t*)out;
   a.lse_out = lse;
   hipLaunchKernelGGL(rep_q_kernel<false>, dim3(8 * BH * a.per_xcd), dim3(256), 0, stream, a);
   return check_launch("vsa_rep_attn_fwd");
 }
 
-extern "C" int vsa_rep_attn_bwd_q(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
+extern "C" int ES_VSA_API(vsa_rep_attn_bwd_q)(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
                                   const float* lc_mid, const void* k_tail, const void* v_tail, const float* lc_tail,
                                   const void* dout, const float* lse, const float* delta, const int* q2k_ptr,
                                   const int* q2k_idx, const unsigned* bits_a, const unsigned* bits_ab,
@@ -716,18 +717,18 @@ extern "C" int vsa_rep_attn_bwd_q(const void* q, const void* k, const void* v, c
   ES_REQUIRE(add_dq == nullptr || add_nb >= L / BK, ES_ERR_INVALID, "VSA2-rep: add_dq has fewer rows than blocks");
   RepArgs a = rep_args(q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, q2k_ptr, q2k_idx, bits_a, bits_ab,
                        blk_cnt, BH, L, D, RM, phases);
-  a.dout = (const bf16_t*)dout;
+  a.dout = (const e16_t*)dout;
   a.lse = lse;
   a.delta = delta;
   a.add_dq = add_dq;
   a.add_nb = add_nb;
   a.dq_acc = (float*)dq_acc;
-  a.out = (bf16_t*)dq;
+  a.out = (e16_t*)dq;
   hipLaunchKernelGGL(rep_q_kernel<true>, dim3(8 * BH * a.per_xcd), dim3(256), 0, stream, a);
   return check_launch("vsa_rep_attn_bwd_q");
 }
 
-extern "C" int vsa_rep_bwd_tables(const void* q, const void* dout, const void* k_tab, const void* v_tab,
+extern "C" int ES_VSA_API(vsa_rep_bwd_tables)(const void* q, const void* dout, const void* k_tab, const void* v_tab,
                                   const float* lc, const float* lse, const float* delta, const unsigned* bits_a,
                                   const unsigned* bits_ab, float* dk_tab, float* dv_tab, int BH, int L, int D, int RM,
                                   int tier, hipStream_t stream) {
@@ -736,10 +737,10 @@ extern "C" int vsa_rep_bwd_tables(const void* q, const void* dout, const void* k
              ES_ERR_INVALID, "VSA2-rep: null tensor pointer");
   ES_REQUIRE(tier == 2 || tier == 4, ES_ERR_INVALID, "VSA2-rep: tier must be 2 (B, mid table) or 4 (C, tail table)");
   TabArgs a = {};
-  a.q = (const bf16_t*)q;
-  a.dout = (const bf16_t*)dout;
-  a.k_tab = (const bf16_t*)k_tab;
-  a.v_tab = (const bf16_t*)v_tab;
+  a.q = (const e16_t*)q;
+  a.dout = (const e16_t*)dout;
+  a.k_tab = (const e16_t*)k_tab;
+  a.v_tab = (const e16_t*)v_tab;
   a.lc = lc;
   a.lse = lse;
   a.delta = delta;
@@ -760,7 +761,7 @@ extern "C" int vsa_rep_bwd_tables(const void* q, const void* dout, const void* k
   return check_launch("vsa_rep_bwd_tables");
 }
 
-extern "C" int vsa_rep_unpool(const float* acc_k, const float* acc_v, const float* dk_mid, const float* dv_mid,
+extern "C" int ES_VSA_API(vsa_rep_unpool)(const float* acc_k, const float* acc_v, const float* dk_mid, const float* dv_mid,
                               const float* dk_tail, const float* dv_tail, const int* blk_cnt, void* dk, void* dv,
                               int BH, int L, int D, int RM, hipStream_t stream) {
   if (int st = rep_check(BH, L, D, RM)) return st;
@@ -768,22 +769,23 @@ extern "C" int vsa_rep_unpool(const float* acc_k, const float* acc_v, const floa
              "VSA2-rep: null tensor pointer");
   const int NB = L / BK;
   hipLaunchKernelGGL(rep_unpool_kernel, dim3((NB + 3) / 4, BH), dim3(256), 0, stream, acc_k, acc_v, dk_mid, dv_mid,
-                     dk_tail, dv_tail, (bf16_t*)dk, (bf16_t*)dv, blk_cnt, L, NB, RM, (NB * RM + 63) / 64 * 64,
+                     dk_tail, dv_tail, (e16_t*)dk, (e16_t*)dv, blk_cnt, L, NB, RM, (NB * RM + 63) / 64 * 64,
                      (NB + 63) / 64 * 64);
   return check_launch("vsa_rep_unpool");
 }
 
-extern "C" int vsa_row_dot(const void* x, const void* y, const int* blk_cnt, float* out, int BH, int L, int D,
+extern "C" int ES_VSA_API(vsa_row_dot)(const void* x, const void* y, const int* blk_cnt, float* out, int BH, int L, int D,
                            hipStream_t stream) {
   ES_REQUIRE(x && y && blk_cnt && out, ES_ERR_INVALID, "VSA: null tensor pointer");
   ES_REQUIRE(BH > 0 && BH <= 65535 && L > 0 && L % BK == 0, ES_ERR_INVALID, "VSA: tokens must be [BH, L = NB * 64, D]");
   ES_REQUIRE(D == 64 || D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 64 or 128 (rows stored with 128 columns)");
   const int NB = L / BK;
-  hipLaunchKernelGGL(row_dot_kernel, dim3((NB + 3) / 4, BH), dim3(256), 0, stream, (const bf16_t*)x, (const bf16_t*)y,
+  hipLaunchKernelGGL(row_dot_kernel, dim3((NB + 3) / 4, BH), dim3(256), 0, stream, (const e16_t*)x, (const e16_t*)y,
                      out, blk_cnt, L, NB);
   return check_launch("vsa_row_dot");
 }
 
+#ifndef ES_ELEM_F16  // no token tensors: built once
 extern "C" int vsa_tier_b_lists(const int* ab_ptr, const int* ab_idx, const int* a_ptr, const unsigned* bits_a,
                                 int* b_ptr, int* b_idx, int BH, int NB, hipStream_t stream) {
   ES_REQUIRE(ab_ptr && a_ptr && bits_a && b_ptr, ES_ERR_INVALID, "VSA2-rep: null tensor pointer");
@@ -792,3 +794,4 @@ extern "C" int vsa_tier_b_lists(const int* ab_ptr, const int* ab_idx, const int*
                      b_ptr, b_idx, NB, (NB + 31) / 32);
   return check_launch("vsa_tier_b_lists");
 }
+#endif

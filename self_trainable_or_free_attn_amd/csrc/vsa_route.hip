@@ -19,6 +19,7 @@
 // scan into k2q_ptr (base (bh0 + b) * keff), and an emission that lists each column's query blocks ascending.
 #include "../../include/vsa_hip.h"
 #include "common.h"
+#include "elem.h"
 
 #include <algorithm>
 
@@ -46,9 +47,9 @@ __device__ __forceinline__ unsigned long long lanes_below() {
 
 // ------------------------------------------------------------------------------------ original-VSA rows
 struct RowsArgs {
-  const bf16_t *qc, *kc;      // [BH, NBc_pad, D]
-  const bf16_t* scores_in;    // [bh_count, NB, NB] (FROM_SCORES)
-  bf16_t* scores_out;         // optional [bh_count, NB, NB]
+  const e16_t *qc, *kc;      // [BH, NBc_pad, D]
+  const e16_t* scores_in;    // [bh_count, NB, NB] (FROM_SCORES)
+  e16_t* scores_out;         // optional [bh_count, NB, NB]
   int *q2k_ptr, *q2k_idx;
   unsigned* selbits;          // [bh_count, ceil32(NB), W]
   int NB, NBc_pad, bh0, K, W;
@@ -74,20 +75,20 @@ __global__ __launch_bounds__(256) void rows_select_kernel(RowsArgs a) {
     }
   } else {
     // S strip: A = qc rows r0 .. r0 + 31 (registers), B = kc rows of each 32-column tile (L2)
-    bf16x8 qa[8];
-    const bf16_t* qp = a.qc + (bh * a.NBc_pad + r0 + lq) * HD + 8 * hi;
+    ev8 qa[8];
+    const e16_t* qp = a.qc + (bh * a.NBc_pad + r0 + lq) * HD + 8 * hi;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qa[ks] = *reinterpret_cast<const bf16x8*>(qp + 16 * ks);
+    for (int ks = 0; ks < 8; ++ks) qa[ks] = *reinterpret_cast<const ev8*>(qp + 16 * ks);
     for (int ct = wv; ct < NBp / 32; ct += 4) {
-      const bf16_t* kp = a.kc + (bh * a.NBc_pad + ct * 32 + lq) * HD + 8 * hi;
+      const e16_t* kp = a.kc + (bh * a.NBc_pad + ct * 32 + lq) * HD + 8 * hi;
       f32x16 acc = {};
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) acc = mfma32(qa[ks], *reinterpret_cast<const bf16x8*>(kp + 16 * ks), acc);
+      for (int ks = 0; ks < 8; ++ks) acc = emfma(qa[ks], *reinterpret_cast<const ev8*>(kp + 16 * ks), acc);
       const int col = ct * 32 + lq;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int rr = 8 * (r / 4) + 4 * hi + (r % 4);
-        const bf16_t s = f2bf(bf2f(f2bf(acc[r])) * a.scale);
+        const e16_t s = f2e(mul_rn(e2f(f2e(acc[r])), a.scale));
         const bool in = r0 + rr < NB && col < NB;
         keys_s[rr * NBp + col] = in ? (unsigned short)key16(s) : 0;
         if (a.scores_out != nullptr && in) a.scores_out[((size_t)bhl * NB + r0 + rr) * NB + col] = s;
@@ -455,7 +456,7 @@ __global__ __launch_bounds__(256) void csr_bits_kernel(const int* __restrict__ p
 
 // ------------------------------------------------------------------------------------ VSA2 PSP router
 struct PspArgs {
-  const bf16_t *qr, *kr;  // [BH, Lr_pad, D]
+  const e16_t *qr, *kr;  // [BH, Lr_pad, D]
   const int* blk_cnt;
   float* lse2;            // [BH, Lr_pad]
   float* scores;          // [bh_count, NB, NB]
@@ -482,7 +483,7 @@ __global__ __launch_bounds__(256) void psp_kernel(PspArgs a) {
   const int rg = wv & 1, kh = wv >> 1;
   const int qrow = qt * 64 + 32 * rg + lq;
   const bool qvalid = group_valid(a, qrow);
-  const bf16_t* kbase = a.kr + bh * a.Lr_pad * HD;
+  const e16_t* kbase = a.kr + bh * a.Lr_pad * HD;
   const srd_t rk = make_srd(kbase, (unsigned)((size_t)a.Lr_pad * HD * 2));
   unsigned ld_off[4];
 #pragma unroll
@@ -495,11 +496,11 @@ __global__ __launch_bounds__(256) void psp_kernel(PspArgs a) {
     for (int i = 0; i < 4; ++i) dma16(rk, k_s[sb] + wv * 4096 + i * 1024, ld_off[i], (unsigned)c * (BK * 256));
     return group_valid(a, c * 64 + l) ? 0.0f : -INFINITY;
   };
-  bf16x8 qreg[8];
+  ev8 qreg[8];
   {
-    const bf16_t* qp = a.qr + (bh * a.Lr_pad + qrow) * HD + 8 * hi;
+    const e16_t* qp = a.qr + (bh * a.Lr_pad + qrow) * HD + 8 * hi;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qreg[ks] = *reinterpret_cast<const bf16x8*>(qp + 16 * ks);
+    for (int ks = 0; ks < 8; ++ks) qreg[ks] = *reinterpret_cast<const ev8*>(qp + 16 * ks);
   }
   int koff[8];
 #pragma unroll
@@ -525,7 +526,7 @@ __global__ __launch_bounds__(256) void psp_kernel(PspArgs a) {
     if (c + 1 < nchunk) bn = issue(c + 1, sb ^ 1);
     f32x16 s = {};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) s = mfma32(lds_read16(k_s[sb], koff[ks]), qreg[ks], s);
+    for (int ks = 0; ks < 8; ++ks) s = emfma(elds16(k_s[sb], koff[ks]), qreg[ks], s);
     float x[16];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -643,10 +644,12 @@ static size_t carve(void* base, int bh_count, int NB, TopkCarve* c) {
   return off;
 }
 
+#ifndef ES_ELEM_F16  // no token tensors: built once
 extern "C" size_t vsa_topk_workspace(int bh_count, int NB) {
   if (bh_count <= 0 || NB <= 0) return 0;
   return carve(nullptr, bh_count, NB, nullptr);
 }
+#endif
 
 static int invert(const TopkCarve& c, int* k2q_ptr, int* k2q_idx, int NB, int bh0, int bh_count, hipStream_t stream) {
   const int W = (NB + 31) / 32, NG = (NB + ROWS - 1) / ROWS;
@@ -662,10 +665,10 @@ static int rows_common(const void* qc, const void* kc, const void* scores_in, vo
   ES_REQUIRE(NB >= 1 && NB <= MAX_NB, ES_ERR_UNSUPPORTED, "VSA: route_rows supports 1 <= NB <= 2048 blocks");
   ES_REQUIRE(bh0 >= 0 && bh_count >= 1 && bh_count <= 65535, ES_ERR_INVALID, "VSA: bad (b,h) range");
   RowsArgs a = {};
-  a.qc = (const bf16_t*)qc;
-  a.kc = (const bf16_t*)kc;
-  a.scores_in = (const bf16_t*)scores_in;
-  a.scores_out = (bf16_t*)scores_out;
+  a.qc = (const e16_t*)qc;
+  a.kc = (const e16_t*)kc;
+  a.scores_in = (const e16_t*)scores_in;
+  a.scores_out = (e16_t*)scores_out;
   a.NB = NB;
   a.NBc_pad = NBc_pad;
   a.bh0 = bh0;
@@ -703,7 +706,7 @@ static int rows_common(const void* qc, const void* kc, const void* scores_in, vo
   return check_launch(what);
 }
 
-extern "C" int vsa_block_scores(const void* qc, const void* kc, void* scores, int NB, int NBc_pad, int bh0,
+extern "C" int ES_VSA_API(vsa_block_scores)(const void* qc, const void* kc, void* scores, int NB, int NBc_pad, int bh0,
                                 int bh_count, int D, hipStream_t stream) {
   ES_REQUIRE(qc && kc && scores, ES_ERR_INVALID, "VSA: null tensor pointer");
   ES_REQUIRE(D == 64 || D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 64 or 128 (rows stored with 128 columns)");
@@ -712,7 +715,7 @@ extern "C" int vsa_block_scores(const void* qc, const void* kc, void* scores, in
                      nullptr, 0, D, stream, "vsa_block_scores");
 }
 
-extern "C" int vsa_route_rows(const void* qc, const void* kc, int NB, int NBc_pad, int bh0, int bh_count, int K,
+extern "C" int ES_VSA_API(vsa_route_rows)(const void* qc, const void* kc, int NB, int NBc_pad, int bh0, int bh_count, int K,
                               int D, int* q2k_ptr, int* q2k_idx, int* k2q_ptr, int* k2q_idx, void* workspace,
                               size_t workspace_bytes, hipStream_t stream) {
   ES_REQUIRE(qc && kc, ES_ERR_INVALID, "VSA: null tensor pointer");
@@ -723,7 +726,7 @@ extern "C" int vsa_route_rows(const void* qc, const void* kc, int NB, int NBc_pa
                      workspace, workspace_bytes, D, stream, "vsa_route_rows");
 }
 
-extern "C" int vsa_row_topk(const void* scores, int NB, int bh0, int bh_count, int K, int* q2k_ptr, int* q2k_idx,
+extern "C" int ES_VSA_API(vsa_row_topk)(const void* scores, int NB, int bh0, int bh_count, int K, int* q2k_ptr, int* q2k_idx,
                             int* k2q_ptr, int* k2q_idx, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   ES_REQUIRE(scores, ES_ERR_INVALID, "VSA: null tensor pointer");
   ES_REQUIRE(K >= 0 && K <= NB, ES_ERR_INVALID, "VSA: K must be in [0, NB]");
@@ -731,6 +734,7 @@ extern "C" int vsa_row_topk(const void* scores, int NB, int bh0, int bh_count, i
                      workspace, workspace_bytes, HD, stream, "vsa_row_topk");
 }
 
+#ifndef ES_ELEM_F16  // no token tensors: built once
 extern "C" int vsa_global_topk(const float* scores, int NB, int bh0, int bh_count, long long budget, int* q2k_ptr,
                                int* q2k_idx, int* k2q_ptr, int* k2q_idx, unsigned* bits_out, void* workspace,
                                size_t workspace_bytes, hipStream_t stream) {
@@ -770,6 +774,7 @@ extern "C" int vsa_global_topk(const float* scores, int NB, int bh0, int bh_coun
                        bits_out, NB, W, bh0, bh_count);
   return check_launch("vsa_global_topk");
 }
+#endif
 
 template <int G>
 static void launch_psp(const PspArgs& a, bool scores, int bh_count, hipStream_t stream) {
@@ -789,8 +794,8 @@ static int psp(const void* qr, const void* kr, const int* blk_cnt, float* lse2, 
   ES_REQUIRE(NB >= 1 && bh0 >= 0 && bh_count >= 1 && bh_count <= 65535, ES_ERR_INVALID, "VSA: bad (b,h) range");
   const int G = BK / R;
   PspArgs a = {};
-  a.qr = (const bf16_t*)qr;
-  a.kr = (const bf16_t*)kr;
+  a.qr = (const e16_t*)qr;
+  a.kr = (const e16_t*)kr;
   a.blk_cnt = blk_cnt;
   a.lse2 = lse2;
   a.scores = scores;
@@ -811,17 +816,18 @@ static int psp(const void* qr, const void* kr, const int* blk_cnt, float* lse2, 
   return check_launch(what);
 }
 
-extern "C" int vsa_router_lse(const void* qr, const void* kr, const int* blk_cnt, float* lse2, int NB, int R, int BH,
+extern "C" int ES_VSA_API(vsa_router_lse)(const void* qr, const void* kr, const int* blk_cnt, float* lse2, int NB, int R, int BH,
                               int D, hipStream_t stream) {
   return psp(qr, kr, blk_cnt, lse2, nullptr, NB, R, 0, 0, BH, D, false, stream, "vsa_router_lse");
 }
 
-extern "C" int vsa_router_scores(const void* qr, const void* kr, const float* lse2, const int* blk_cnt, float* scores,
+extern "C" int ES_VSA_API(vsa_router_scores)(const void* qr, const void* kr, const float* lse2, const int* blk_cnt, float* scores,
                                  int NB, int R, int row_norm, int bh0, int bh_count, int D, hipStream_t stream) {
   return psp(qr, kr, blk_cnt, (float*)lse2, scores, NB, R, row_norm, bh0, bh_count, D, true, stream,
              "vsa_router_scores");
 }
 
+#ifndef ES_ELEM_F16  // no token tensors: built once
 extern "C" int vsa_csr_transpose(const int* ptr, const int* idx, int NB, int bh0, int bh_count, int* out_ptr,
                                  int* out_idx, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   ES_REQUIRE(ptr && out_ptr && workspace, ES_ERR_INVALID, "VSA: null tensor pointer");
@@ -841,3 +847,4 @@ extern "C" int vsa_csr_transpose(const int* ptr, const int* idx, int NB, int bh0
   invert(c, out_ptr, out_idx, NB, bh0, bh_count, stream);
   return check_launch("vsa_csr_transpose");
 }
+#endif

@@ -20,6 +20,7 @@
 //   sum     : out = valid ? sum_i part_i + add[blk] / cnt : 0 (reference split.cu:157-200)
 #include "../../include/vsa_hip.h"
 #include "common.h"
+#include "elem.h"
 
 #include <cmath>
 
@@ -138,7 +139,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void plan_kernel(PlanArgs a) {
 __global__ __launch_bounds__(256) void merge_fwd_kernel(const float* __restrict__ part_o,
                                                         const float* __restrict__ part_lse,
                                                         const int4* __restrict__ merges, const int* __restrict__ info,
-                                                        const int* __restrict__ blk_cnt, bf16_t* __restrict__ o,
+                                                        const int* __restrict__ blk_cnt, e16_t* __restrict__ o,
                                                         float* __restrict__ lse, int L, int NB, int mask_rows) {
   if ((int)blockIdx.x >= info[1]) return;
   const int4 mg = merges[blockIdx.x];
@@ -175,10 +176,10 @@ __global__ __launch_bounds__(256) void merge_fwd_kernel(const float* __restrict_
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     uint4 u;
-    u.x = (unsigned)f2bf(acc[8 * q + 0]) | ((unsigned)f2bf(acc[8 * q + 1]) << 16);
-    u.y = (unsigned)f2bf(acc[8 * q + 2]) | ((unsigned)f2bf(acc[8 * q + 3]) << 16);
-    u.z = (unsigned)f2bf(acc[8 * q + 4]) | ((unsigned)f2bf(acc[8 * q + 5]) << 16);
-    u.w = (unsigned)f2bf(acc[8 * q + 6]) | ((unsigned)f2bf(acc[8 * q + 7]) << 16);
+    u.x = (unsigned)f2e(acc[8 * q + 0]) | ((unsigned)f2e(acc[8 * q + 1]) << 16);
+    u.y = (unsigned)f2e(acc[8 * q + 2]) | ((unsigned)f2e(acc[8 * q + 3]) << 16);
+    u.z = (unsigned)f2e(acc[8 * q + 4]) | ((unsigned)f2e(acc[8 * q + 5]) << 16);
+    u.w = (unsigned)f2e(acc[8 * q + 6]) | ((unsigned)f2e(acc[8 * q + 7]) << 16);
     dst[q] = u;
   }
   if ((threadIdx.x & 3) == 0) lse[tok] = out_lse;
@@ -187,7 +188,7 @@ __global__ __launch_bounds__(256) void merge_fwd_kernel(const float* __restrict_
 __global__ __launch_bounds__(256) void merge_sum_kernel(const float* __restrict__ part, const int4* __restrict__ merges,
                                                         const int* __restrict__ info, const float* __restrict__ add,
                                                         int add_nb, const int* __restrict__ blk_cnt,
-                                                        bf16_t* __restrict__ out, float* __restrict__ out_f32, int L,
+                                                        e16_t* __restrict__ out, float* __restrict__ out_f32, int L,
                                                         int NB) {
   if ((int)blockIdx.x >= info[1]) return;
   const int4 mg = merges[blockIdx.x];
@@ -228,10 +229,10 @@ __global__ __launch_bounds__(256) void merge_sum_kernel(const float* __restrict_
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       uint4 u;
-      u.x = (unsigned)f2bf(acc[8 * q + 0]) | ((unsigned)f2bf(acc[8 * q + 1]) << 16);
-      u.y = (unsigned)f2bf(acc[8 * q + 2]) | ((unsigned)f2bf(acc[8 * q + 3]) << 16);
-      u.z = (unsigned)f2bf(acc[8 * q + 4]) | ((unsigned)f2bf(acc[8 * q + 5]) << 16);
-      u.w = (unsigned)f2bf(acc[8 * q + 6]) | ((unsigned)f2bf(acc[8 * q + 7]) << 16);
+      u.x = (unsigned)f2e(acc[8 * q + 0]) | ((unsigned)f2e(acc[8 * q + 1]) << 16);
+      u.y = (unsigned)f2e(acc[8 * q + 2]) | ((unsigned)f2e(acc[8 * q + 3]) << 16);
+      u.z = (unsigned)f2e(acc[8 * q + 4]) | ((unsigned)f2e(acc[8 * q + 5]) << 16);
+      u.w = (unsigned)f2e(acc[8 * q + 6]) | ((unsigned)f2e(acc[8 * q + 7]) << 16);
       dst[q] = u;
     }
   }
@@ -243,6 +244,7 @@ __global__ __launch_bounds__(256) void merge_sum_kernel(const float* __restrict_
 
 using namespace es;
 
+#ifndef ES_ELEM_F16  // no token tensors: built once
 extern "C" int vsa_split_plan(const int* ptr, int BH, int NB, int chunk, int max_slots, int min_len, double rel_mean,
                               double tail_frac, int resident, int budget, int* tasks, int* merges, int* info,
                               hipStream_t stream) {
@@ -268,8 +270,9 @@ extern "C" int vsa_split_plan(const int* ptr, int BH, int NB, int chunk, int max
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, a);
   return check_launch("vsa_split_plan");
 }
+#endif
 
-extern "C" int vsa_split_merge_fwd(const float* part_o, const float* part_lse, const int* merges, const int* info,
+extern "C" int ES_VSA_API(vsa_split_merge_fwd)(const float* part_o, const float* part_lse, const int* merges, const int* info,
                                    int max_merges, const int* blk_cnt, void* o, float* lse, int BH, int L, int D,
                                    int mask_rows, hipStream_t stream) {
   ES_REQUIRE(D == 64 || D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 64 or 128 (rows stored with 128 columns)");
@@ -277,11 +280,11 @@ extern "C" int vsa_split_merge_fwd(const float* part_o, const float* part_lse, c
   if (max_merges <= 0) return ES_OK;
   ES_REQUIRE(part_o && part_lse && merges && info && blk_cnt && o && lse, ES_ERR_INVALID, "VSA2: null tensor pointer");
   hipLaunchKernelGGL(merge_fwd_kernel, dim3(max_merges), dim3(256), 0, stream, part_o, part_lse, (const int4*)merges,
-                     info, blk_cnt, (bf16_t*)o, lse, L, L / BK, mask_rows);
+                     info, blk_cnt, (e16_t*)o, lse, L, L / BK, mask_rows);
   return check_launch("vsa_split_merge_fwd");
 }
 
-extern "C" int vsa_split_merge_sum(const float* part, const int* merges, const int* info, int max_merges,
+extern "C" int ES_VSA_API(vsa_split_merge_sum)(const float* part, const int* merges, const int* info, int max_merges,
                                    const float* add, int add_nb, const int* blk_cnt, void* out, float* out_f32, int BH,
                                    int L, int D, hipStream_t stream) {
   ES_REQUIRE(D == 64 || D == HD, ES_ERR_UNSUPPORTED, "VSA: head dim must be 64 or 128 (rows stored with 128 columns)");
@@ -289,6 +292,6 @@ extern "C" int vsa_split_merge_sum(const float* part, const int* merges, const i
   if (max_merges <= 0) return ES_OK;
   ES_REQUIRE(part && merges && info && blk_cnt && (out || out_f32), ES_ERR_INVALID, "VSA2: null tensor pointer");
   hipLaunchKernelGGL(merge_sum_kernel, dim3(max_merges), dim3(256), 0, stream, part, (const int4*)merges, info, add,
-                     add_nb, blk_cnt, (bf16_t*)out, out_f32, L, L / BK);
+                     add_nb, blk_cnt, (e16_t*)out, out_f32, L, L / BK);
   return check_launch("vsa_split_merge_sum");
 }

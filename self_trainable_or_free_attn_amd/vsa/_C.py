@@ -30,9 +30,19 @@ def _check(cond, msg):
 def _tokens(x, name):
     _check(isinstance(x, torch.Tensor) and x.is_cuda, f"{name} must be a CUDA tensor")
     _check(x.dim() == 4 and x.is_contiguous(), f"{name} must be contiguous [B, H, L, D]")
-    _check(x.dtype == torch.bfloat16, f"{name} must be bf16 (this build computes in bf16)")
+    _check(x.dtype in (torch.bfloat16, torch.float16), f"{name} must be bf16 or fp16")
     _check(x.shape[3] in (64, HD), f"{name}: head dim must be 64 or 128 (this build)")
     _check(x.shape[2] % BLOCK == 0, f"{name}: L must be a multiple of 64")
+
+
+def _call(name, *args):
+    """Call entry point `name`, or its fp16 twin when the token tensors among the arguments are fp16 (the reference
+    dispatches its kernels on the tensor dtype, vsa2_api.cpp:51); token tensors of mixed dtypes are refused."""
+    dts = {a.dtype for a in args if isinstance(a, torch.Tensor) and a.dtype in (torch.bfloat16, torch.float16)}
+    _check(len(dts) <= 1, f"{name}: token tensors must share one dtype (bf16 or fp16), got {sorted(map(str, dts))}")
+    if dts == {torch.float16} and name in _lib.F16_TWINS:
+        name += "_f16"
+    _lib.call(name, *args)
 
 
 def _i32(x, name):
@@ -108,7 +118,7 @@ def pool_fwd(q, k, v, blk_cnt, R):
     kr = torch.zeros_like(qr)
     qc = torch.zeros(B, H, _ceil64(NB), HD, device=q.device, dtype=q.dtype)
     kc, vc = torch.zeros_like(qc), torch.zeros_like(qc)
-    _lib.call("vsa_pool", _wide(q), _wide(k), _wide(v), blk_cnt, qr, kr, None, qc, kc, vc, B * H, L, D, int(R))
+    _call("vsa_pool", _wide(q), _wide(k), _wide(v), blk_cnt, qr, kr, None, qc, kc, vc, B * H, L, D, int(R))
     return [_narrow(t, D) for t in (qr, kr, qc, kc, vc)]
 
 
@@ -126,7 +136,7 @@ def fuse_fwd(of, oc, gate, blk_cnt, gate_act):
         else:
             raise RuntimeError("gate must be [B, H, L] or [B, H, L, D]")
     o = torch.empty(B, H, L, HD, device=of.device, dtype=of.dtype)
-    _lib.call("vsa_fuse_fwd", _wide(of), _wide(oc), _wide(gate) if mode == 2 else gate, o, blk_cnt, B * H, L, D,
+    _call("vsa_fuse_fwd", _wide(of), _wide(oc), _wide(gate) if mode == 2 else gate, o, blk_cnt, B * H, L, D,
               oc.shape[2], mode, int(gate_act))
     return _narrow(o, D)
 
@@ -142,7 +152,7 @@ def fuse_bwd(dout, of, oc, gate, blk_cnt, gate_act, write_dout_f=True):
     delta_c = torch.zeros(B, H, oc.shape[2], device=dout.device, dtype=torch.float32)
     gate_w = _wide(gate) if mode == 2 else gate
     dgate = torch.empty_like(gate_w) if gate is not None else None
-    _lib.call("vsa_fuse_bwd", _wide(dout), _wide(of), _wide(oc), gate_w, dout_f, delta_f, dout_c,
+    _call("vsa_fuse_bwd", _wide(dout), _wide(of), _wide(oc), gate_w, dout_f, delta_f, dout_c,
               delta_c, dgate, blk_cnt, B * H, L, D, oc.shape[2], mode, int(gate_act))
     return _narrow(dout_f, D), delta_f, _narrow(dout_c, D), delta_c, _narrow(dgate, D) if mode == 2 else dgate
 
@@ -152,7 +162,7 @@ def finalize(acc, add, blk_cnt, like):
     B, H, L, D = like.shape
     out = torch.empty(B, H, L, HD, dtype=like.dtype, device=blk_cnt.device)
     add_nb = add.shape[2] if add is not None else 0
-    _lib.call("vsa_finalize", _wide(acc), _wide(add), add_nb, out, blk_cnt, B * H, L, D)
+    _call("vsa_finalize", _wide(acc), _wide(add), add_nb, out, blk_cnt, B * H, L, D)
     return _narrow(out, D)
 
 
@@ -175,7 +185,7 @@ def block_scores(qc, kc, nb, bh0=0, bh_count=0):
         bh_count = BH - bh0
     _check(bh0 >= 0 and bh_count <= 65535 and bh0 + bh_count <= BH, "bad (b,h) range")
     scores = torch.empty(bh_count, nb, nb, device=qc.device, dtype=qc.dtype)
-    _lib.call("vsa_block_scores", _wide(qc), _wide(kc), scores, int(nb), qc.shape[2], int(bh0), int(bh_count),
+    _call("vsa_block_scores", _wide(qc), _wide(kc), scores, int(nb), qc.shape[2], int(bh0), int(bh_count),
               qc.shape[3])
     return scores
 
@@ -195,7 +205,7 @@ def row_topk_into(scores, topk, bh0, q2k_ptr, q2k_idx, k2q_ptr, k2q_idx):
     _check(bhc <= 65535, "too many (b,h) per top-k chunk")
     K = max(0, min(int(topk), NB))
     ws = _workspace(bhc, NB, scores.device)
-    _lib.call("vsa_row_topk", scores.contiguous(), NB, int(bh0), bhc, K, q2k_ptr, q2k_idx, k2q_ptr, k2q_idx, ws,
+    _call("vsa_row_topk", scores.contiguous(), NB, int(bh0), bhc, K, q2k_ptr, q2k_idx, k2q_ptr, k2q_idx, ws,
               ws.numel())
 
 
@@ -213,7 +223,7 @@ def route_rows(qc, kc, nb, topk, max_score_bytes=2 << 30):
     D, qc, kc = qc.shape[3], _wide(qc), _wide(kc)
     for bh0 in range(0, BH, chunk):
         cnt = min(chunk, BH - bh0)
-        _lib.call("vsa_route_rows", qc, kc, NB, qc.shape[2], bh0, cnt, K, D, *out, ws, ws.numel())
+        _call("vsa_route_rows", qc, kc, NB, qc.shape[2], bh0, cnt, K, D, *out, ws, ws.numel())
     return list(out)
 
 
@@ -221,7 +231,7 @@ def router_lse(qr, kr, blk_cnt, R):
     """lse2 [B, H, Lr_pad] of every pooled query row (reference vsa2_api.cpp:122-135)."""
     B, H, Lr_pad, D = qr.shape
     lse2 = torch.empty(B, H, Lr_pad, device=qr.device, dtype=torch.float32)
-    _lib.call("vsa_router_lse", _wide(qr), _wide(kr), blk_cnt, lse2, blk_cnt.numel(), int(R), B * H, D)
+    _call("vsa_router_lse", _wide(qr), _wide(kr), blk_cnt, lse2, blk_cnt.numel(), int(R), B * H, D)
     return lse2
 
 
@@ -232,7 +242,7 @@ def router_scores(qr, kr, lse2, blk_cnt, R, row_norm, bh0=0, bh_count=0):
     if bh_count <= 0:
         bh_count = B * H - bh0
     scores = torch.empty(bh_count, NB, NB, device=qr.device, dtype=torch.float32)
-    _lib.call("vsa_router_scores", _wide(qr), _wide(kr), lse2, blk_cnt, scores, NB, int(R), int(row_norm), int(bh0), int(bh_count), D)
+    _call("vsa_router_scores", _wide(qr), _wide(kr), lse2, blk_cnt, scores, NB, int(R), int(row_norm), int(bh0), int(bh_count), D)
     return scores
 
 
@@ -243,7 +253,7 @@ def global_topk_into(scores, budget, bh0, q2k_ptr, q2k_idx, k2q_ptr, k2q_idx):
     bhc, NB = scores.shape[0], scores.shape[1]
     _check(bhc <= 65535, "too many (b,h) per top-k chunk")
     ws = _workspace(bhc, NB, scores.device)
-    _lib.call("vsa_global_topk", scores.contiguous(), NB, int(bh0), bhc, int(budget), q2k_ptr, q2k_idx, k2q_ptr,
+    _call("vsa_global_topk", scores.contiguous(), NB, int(bh0), bhc, int(budget), q2k_ptr, q2k_idx, k2q_ptr,
               k2q_idx, None, ws, ws.numel())
 
 
@@ -265,8 +275,8 @@ def route(qr, kr, blk_cnt, R, budget, row_norm, max_score_bytes=2 << 30):
     for bh0 in range(0, BH, chunk):
         cnt = min(chunk, BH - bh0)
         s = scores[:cnt]
-        _lib.call("vsa_router_scores", qr, kr, lse2, blk_cnt, s, NB, int(R), int(row_norm), bh0, cnt, D)
-        _lib.call("vsa_global_topk", s, NB, bh0, cnt, int(budget), *out, None, ws, ws.numel())
+        _call("vsa_router_scores", qr, kr, lse2, blk_cnt, s, NB, int(R), int(row_norm), bh0, cnt, D)
+        _call("vsa_global_topk", s, NB, bh0, cnt, int(budget), *out, None, ws, ws.numel())
     return list(out)
 
 
@@ -280,7 +290,7 @@ def csr_transpose(ptr, idx):
     ws = _workspace(chunk, NB, ptr.device)
     for bh0 in range(0, BH, chunk):
         cnt = min(chunk, BH - bh0)
-        _lib.call("vsa_csr_transpose", ptr, idx, NB, bh0, cnt, out_ptr, out_idx, ws, ws.numel())
+        _call("vsa_csr_transpose", ptr, idx, NB, bh0, cnt, out_ptr, out_idx, ws, ws.numel())
     return out_ptr, out_idx
 
 
@@ -302,7 +312,7 @@ def attn_fwd(q, k, v, row_ptr, col_idx, blk_cnt, use_tk=False):
     _check(row_ptr.numel() == B * H * (L // BLOCK + 1), "metadata shape mismatch")
     o = torch.empty(B, H, L, HD, device=q.device, dtype=q.dtype)
     lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
-    _lib.call("vsa_attn_fwd", _wide(q), _wide(k), _wide(v), row_ptr, col_idx, blk_cnt, o, lse, B * H, L, D)
+    _call("vsa_attn_fwd", _wide(q), _wide(k), _wide(v), row_ptr, col_idx, blk_cnt, o, lse, B * H, L, D)
     return _narrow(o, D), lse
 
 
@@ -317,12 +327,12 @@ def attn_bwd(q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, dq_acc=None, 
     dk, dv = torch.empty(B, H, L, HD, **f), torch.empty(B, H, L, HD, **f)
     add_nb = add_dk.shape[2] if add_dk is not None else (add_dv.shape[2] if add_dv is not None else 0)
     q, k, v, dout = _wide(q), _wide(k), _wide(v), _wide(dout)
-    _lib.call("vsa_attn_bwd_kv", q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, _wide(add_dk), _wide(add_dv),
+    _call("vsa_attn_bwd_kv", q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, _wide(add_dk), _wide(add_dv),
               add_nb, dk, dv, 1 if out_fp32 else 0, B * H, L, D)
     if dq_acc is not None:
         q2k_ptr, q2k_idx = csr_transpose(row_ptr, col_idx)
         acc = _InPlace(dq_acc)
-        _lib.call("vsa_attn_bwd_q", q, k, v, dout, lse, delta, q2k_ptr, q2k_idx, blk_cnt, None, 0, None, acc.w,
+        _call("vsa_attn_bwd_q", q, k, v, dout, lse, delta, q2k_ptr, q2k_idx, blk_cnt, None, 0, None, acc.w,
                   B * H, L, D)
         acc.put()
     return _narrow(dk, D), _narrow(dv, D)
@@ -333,7 +343,7 @@ def attn_bwd_q(q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, add_dq=None
     _attn_args(q, k, v, blk_cnt)
     B, H, L, D = q.shape
     dq = torch.empty(B, H, L, HD, device=q.device, dtype=q.dtype)
-    _lib.call("vsa_attn_bwd_q", _wide(q), _wide(k), _wide(v), _wide(dout), lse, delta, row_ptr, col_idx, blk_cnt,
+    _call("vsa_attn_bwd_q", _wide(q), _wide(k), _wide(v), _wide(dout), lse, delta, row_ptr, col_idx, blk_cnt,
               _wide(add_dq), add_dq.shape[2] if add_dq is not None else 0, dq, None, B * H, L, D)
     return _narrow(dq, D)
 
@@ -353,7 +363,7 @@ def split_plan(ptr, chunk, max_slots, min_len=0, rel_mean=0.0, tail_frac=0.0, re
     tasks = torch.empty(NR + int(max_slots), 4, **i32)
     merges = torch.empty(max(1, min(NR, int(max_slots) // 2)), 4, **i32)
     info = torch.empty(8, **i32)
-    _lib.call("vsa_split_plan", ptr, B * H, n1 - 1, int(chunk), int(max_slots), int(min_len), float(rel_mean),
+    _call("vsa_split_plan", ptr, B * H, n1 - 1, int(chunk), int(max_slots), int(min_len), float(rel_mean),
               float(tail_frac), int(resident), int(budget), tasks, merges, info)
     return tasks, merges, info
 
@@ -366,7 +376,7 @@ def attn_fwd_tasks(q, k, v, col_idx, blk_cnt, tasks, info, part_o, part_lse):
     o = torch.empty(B, H, L, HD, device=q.device, dtype=q.dtype)
     lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
     po = _InPlace(part_o if part_o.numel() else None)
-    _lib.call("vsa_attn_fwd_tasks", _wide(q), _wide(k), _wide(v), col_idx, blk_cnt, tasks, info, tasks.shape[0], o,
+    _call("vsa_attn_fwd_tasks", _wide(q), _wide(k), _wide(v), col_idx, blk_cnt, tasks, info, tasks.shape[0], o,
               lse, po.w, part_lse if part_lse.numel() else None, B * H, L, D)
     po.put()
     return _narrow(o, D), lse
@@ -378,7 +388,7 @@ def split_merge_fwd(part_o, part_lse, merges, info, blk_cnt, o, lse, mask_rows=T
         return
     B, H, L, D = o.shape
     ow = _InPlace(o)
-    _lib.call("vsa_split_merge_fwd", _wide(part_o), part_lse, merges, info, merges.shape[0], blk_cnt, ow.w, lse,
+    _call("vsa_split_merge_fwd", _wide(part_o), part_lse, merges, info, merges.shape[0], blk_cnt, ow.w, lse,
               B * H, L, D, 1 if mask_rows else 0)
     ow.put()
 
@@ -390,7 +400,7 @@ def split_merge_sum(part, merges, info, add, blk_cnt, out):
     B, H, L, D = out.shape
     f32 = out.dtype == torch.float32
     ow = _InPlace(out)
-    _lib.call("vsa_split_merge_sum", _wide(part), merges, info, merges.shape[0], _wide(add),
+    _call("vsa_split_merge_sum", _wide(part), merges, info, merges.shape[0], _wide(add),
               add.shape[2] if add is not None else 0, blk_cnt, None if f32 else ow.w, ow.w if f32 else None,
               B * H, L, D)
     ow.put()
@@ -408,7 +418,7 @@ def attn_bwd_tasks(q, k, v, dout, lse, delta, col_idx, blk_cnt, tasks, info, dq_
     dv = torch.empty_like(dk)
     add_nb = add_dk.shape[2] if add_dk is not None else (add_dv.shape[2] if add_dv is not None else 0)
     pk, pv = _InPlace(part_dk if part_dk.numel() else None), _InPlace(part_dv if part_dv.numel() else None)
-    _lib.call("vsa_attn_bwd_kv_tasks", _wide(q), _wide(k), _wide(v), _wide(dout), lse, delta, col_idx, blk_cnt, tasks,
+    _call("vsa_attn_bwd_kv_tasks", _wide(q), _wide(k), _wide(v), _wide(dout), lse, delta, col_idx, blk_cnt, tasks,
               info, tasks.shape[0], _wide(add_dk), _wide(add_dv), add_nb, dk, dv, pk.w, pv.w, B * H, L, D)
     pk.put()
     pv.put()
@@ -421,7 +431,7 @@ def attn_bwd_q_tasks(q, k, v, dout, lse, delta, col_idx, blk_cnt, tasks, info, a
     B, H, L, D = q.shape
     dq = torch.empty(B, H, L, HD, device=q.device, dtype=q.dtype)
     pq = _InPlace(part_dq if part_dq.numel() else None)
-    _lib.call("vsa_attn_bwd_q_tasks", _wide(q), _wide(k), _wide(v), _wide(dout), lse, delta, col_idx, blk_cnt, tasks,
+    _call("vsa_attn_bwd_q_tasks", _wide(q), _wide(k), _wide(v), _wide(dout), lse, delta, col_idx, blk_cnt, tasks,
               info, tasks.shape[0], _wide(add_dq), add_dq.shape[2] if add_dq is not None else 0, dq, pq.w, B * H, L, D)
     pq.put()
     return _narrow(dq, D)
@@ -433,7 +443,7 @@ def attn_bwd_q_acc(q, k, v, dout, lse, delta, row_ptr, col_idx, blk_cnt, dq_acc)
     _f32(dq_acc, "dq_acc")
     B, H, L, D = q.shape
     acc = _InPlace(dq_acc)
-    _lib.call("vsa_attn_bwd_q", _wide(q), _wide(k), _wide(v), _wide(dout), lse, delta, row_ptr, col_idx, blk_cnt, None,
+    _call("vsa_attn_bwd_q", _wide(q), _wide(k), _wide(v), _wide(dout), lse, delta, row_ptr, col_idx, blk_cnt, None,
               0, None, acc.w, B * H, L, D)
     acc.put()
     return dq_acc
@@ -454,7 +464,7 @@ def rep_build(k, v, blk_cnt, mid_reps):
     v_tail = torch.zeros_like(k_tail)
     lc_mid = torch.empty(NB * RM, device=k.device, dtype=torch.float32)
     lc_tail = torch.empty(NB, device=k.device, dtype=torch.float32)
-    _lib.call("vsa_rep_build", _wide(k), _wide(v), blk_cnt, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, B * H, L, D,
+    _call("vsa_rep_build", _wide(k), _wide(v), blk_cnt, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, B * H, L, D,
               RM)
     k_mid, v_mid, k_tail, v_tail = (_narrow(t, D) for t in (k_mid, v_mid, k_tail, v_tail))
     return [k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail]
@@ -486,14 +496,14 @@ def route_tiers(qr, kr, blk_cnt, R, budget_a, budget_ab, row_norm, max_score_byt
     for bh0 in range(0, BH, chunk):
         cnt = min(chunk, BH - bh0)
         s = scores[:cnt]
-        _lib.call("vsa_router_scores", qr, kr, lse2, blk_cnt, s, NB, int(R), int(row_norm), bh0, cnt, D)
+        _call("vsa_router_scores", qr, kr, lse2, blk_cnt, s, NB, int(R), int(row_norm), bh0, cnt, D)
         if kab != ka:
-            _lib.call("vsa_global_topk", s, NB, bh0, cnt, kab, *ab_out, bits_ab, ws, ws.numel())
-        _lib.call("vsa_global_topk", s, NB, bh0, cnt, ka, *a_out, bits_a, ws, ws.numel())
+            _call("vsa_global_topk", s, NB, bh0, cnt, kab, *ab_out, bits_ab, ws, ws.numel())
+        _call("vsa_global_topk", s, NB, bh0, cnt, ka, *a_out, bits_a, ws, ws.numel())
     b_ptr = torch.zeros(B, H, NB + 1, **i32)
     b_idx = torch.empty(max(1, BH * (kab - ka)), **i32)
     if kab != ka:
-        _lib.call("vsa_tier_b_lists", ab_out[0], ab_out[1], a_out[0], bits_a, b_ptr, b_idx, BH, NB)
+        _call("vsa_tier_b_lists", ab_out[0], ab_out[1], a_out[0], bits_a, b_ptr, b_idx, BH, NB)
     else:
         bits_ab.copy_(bits_a)
     n = BH * ka
@@ -507,7 +517,7 @@ def rep_attn_fwd(q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, q2k_ptr
     B, H, L, D = q.shape
     o = torch.empty(B, H, L, HD, device=q.device, dtype=q.dtype)
     lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
-    _lib.call("vsa_rep_attn_fwd", _wide(q), _wide(k), _wide(v), _wide(k_mid), _wide(v_mid), lc_mid, _wide(k_tail),
+    _call("vsa_rep_attn_fwd", _wide(q), _wide(k), _wide(v), _wide(k_mid), _wide(v_mid), lc_mid, _wide(k_tail),
               _wide(v_tail), lc_tail, q2k_ptr, q2k_idx, bits_a, bits_ab, blk_cnt, o, lse, B * H, L, D, int(mid_reps),
               int(phases))
     return _narrow(o, D), lse
@@ -525,19 +535,19 @@ def rep_attn_bwd_q(q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, dout,
     q, k, v, dout = _wide(q), _wide(k), _wide(v), _wide(dout)
     k_mid, v_mid, k_tail, v_tail = _wide(k_mid), _wide(v_mid), _wide(k_tail), _wide(v_tail)
     acc = _InPlace(dq_acc)
-    _lib.call("vsa_rep_attn_bwd_q", q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, dout, lse, delta, q2k_ptr,
+    _call("vsa_rep_attn_bwd_q", q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, dout, lse, delta, q2k_ptr,
               q2k_idx, bits_a, bits_ab, blk_cnt, _wide(add_dq), add_dq.shape[2] if add_dq is not None else 0, acc.w,
               dq, B * H, L, D, int(mid_reps), int(phases))
     acc.put()
     if phases & 2:
         dkm, dvm = _InPlace(dk_mid), _InPlace(dv_mid)
-        _lib.call("vsa_rep_bwd_tables", q, dout, k_mid, v_mid, lc_mid, lse, delta, bits_a, bits_ab, dkm.w, dvm.w,
+        _call("vsa_rep_bwd_tables", q, dout, k_mid, v_mid, lc_mid, lse, delta, bits_a, bits_ab, dkm.w, dvm.w,
                   B * H, L, D, int(mid_reps), 2)
         dkm.put()
         dvm.put()
     if phases & 4:
         dkt, dvt = _InPlace(dk_tail), _InPlace(dv_tail)
-        _lib.call("vsa_rep_bwd_tables", q, dout, k_tail, v_tail, lc_tail, lse, delta, bits_a, bits_ab, dkt.w, dvt.w,
+        _call("vsa_rep_bwd_tables", q, dout, k_tail, v_tail, lc_tail, lse, delta, bits_a, bits_ab, dkt.w, dvt.w,
                   B * H, L, D, int(mid_reps), 4)
         dkt.put()
         dvt.put()
@@ -555,7 +565,7 @@ def rep_unpool(dk_a, dv_a, dk_mid, dv_mid, dk_tail, dv_tail, blk_cnt, like, mid_
     B, H, L, D = like.shape
     dk = torch.empty(B, H, L, HD, dtype=like.dtype, device=blk_cnt.device)
     dv = torch.empty_like(dk)
-    _lib.call("vsa_rep_unpool", *(_wide(t) for t in (dk_a, dv_a, dk_mid, dv_mid, dk_tail, dv_tail)), blk_cnt, dk, dv,
+    _call("vsa_rep_unpool", *(_wide(t) for t in (dk_a, dv_a, dk_mid, dv_mid, dk_tail, dv_tail)), blk_cnt, dk, dv,
               B * H, L, D, int(mid_reps))
     return _narrow(dk, D), _narrow(dv, D)
 
@@ -564,5 +574,5 @@ def row_dot(a, b, blk_cnt):
     """[B, H, L] fp32 rowsum(a * b) on valid rows, 0 on padding (reference rep_api.cpp row_dot)."""
     B, H, L, D = a.shape
     out = torch.empty(B, H, L, device=a.device, dtype=torch.float32)
-    _lib.call("vsa_row_dot", _wide(a), _wide(b), blk_cnt, out, B * H, L, D)
+    _call("vsa_row_dot", _wide(a), _wide(b), blk_cnt, out, B * H, L, D)
     return out

@@ -8,7 +8,7 @@ Backward: fusion bookkeeping (dO_f, delta, dO_c), the coarse branch backward (fp
 fine branch: a KV-owner pass for dK / dV and a Q-owner pass for dQ (no atomics; every variant number runs it), with
 the coarse gradients spread over each block's valid tokens.
 
-Tensor contract (the reference's): q, k, v [B, H, L, D] contiguous bf16, L = NB * 64 in block-major order with
+Tensor contract (the reference's): q, k, v [B, H, L, D] contiguous bf16 or fp16, L = NB * 64 in block-major order with
 blk_cnt[i] (int32, 1..64) valid tokens first in block i; padding slots hold finite values, are never pooled, output 0
 and get zero gradient. D is 64 or 128 (the native ops store rows with 128 columns; D = 64 is zero-padded).
 """

@@ -40,6 +40,14 @@ def test_bf16_rounding_matches_torch():
     assert np.array_equal(round_bf16(x), torch.from_numpy(x).to(torch.bfloat16).float().numpy())
 
 
+def test_f16_rounding_matches_torch():
+    from oracle.bf16 import round_f16
+    rng = np.random.default_rng(2)
+    x = np.concatenate([rng.standard_normal(10000) * 100, rng.standard_normal(1000) * 1e5,
+                        rng.standard_normal(1000) * 1e-6]).astype(np.float32)
+    assert np.array_equal(round_f16(x), torch.from_numpy(x).to(torch.float16).float().numpy())
+
+
 # --------------------------------------------------------------------------- selections
 def test_row_topk_known_answers():
     """reference tests/test_vsa.py:67-73"""
