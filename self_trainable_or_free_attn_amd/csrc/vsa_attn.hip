@@ -240,7 +240,10 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
 //   KV owner (dK, dV; k2q lists): one workgroup per (kv block, head), 4 waves = 2 key halves x 2 query halves of
 //     each staged query block. S = Q K^T and dP = dO V^T come out with keys on lanes, so P and dS are directly the
 //     B operands of dV^T += dO^T P and dK^T += Q^T dS (dO^T / Q^T through transposed LDS reads). K and V stay in
-//     registers; Q, dO, lse and delta of each listed query block stream through LDS. 4 products per pair.
+//     registers; Q, dO, lse and delta of each listed query block stream through LDS. It runs as two passes, dV
+//     (S, dV) then dK (S, dP, dK): 5 products per pair instead of 4, but each pass holds one 128-register
+//     accumulator set instead of two, so two waves share a SIMD (one pass with both: 5.68 ms at C2, the two
+//     passes 5.14 ms, bit-identical outputs).
 //   Q owner (dQ; q2k lists): the forward's layout. S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T with K^T through
 //     transposed LDS reads. 3 products per pair; dQ is deterministic (no atomics).
 // The two partial accumulators of a workgroup (query halves, or key halves) are summed once at the end in LDS.
@@ -288,13 +291,12 @@ __device__ __forceinline__ bool owner_of(const VsaBwdArgs& a, int& blk, int& bh,
 // lse (natural) -> log2 domain, +inf for rows that must get P = 0
 __device__ __forceinline__ float lse_to_log2(float lse) { return lse == -INFINITY ? INFINITY : lse * LOG2E; }
 
-template <bool TASKS>
-__global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
-  // V of the owned block stays in LDS (the B operand of dP = dO V^T); K stays in registers (the B operand of
-  // S = Q K^T); Q, dO, lse and delta of the listed query blocks are double-buffered. The dK / dV accumulators
-  // (128 registers) need the full register file: one wave per SIMD.
+// The KV-owner backward as two passes with half the accumulators each, so that two waves share a SIMD:
+// PART 1 = dV (S, P, dV += P^T dO), PART 2 = dK (S, dP = dO V^T with V in registers, dK += dS^T Q). S is computed
+// in both (5 products per pair instead of 4).
+template <bool TASKS, int PART>
+__global__ __launch_bounds__(256, 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
   __shared__ __attribute__((aligned(16))) char qd_s[2][2][BK * 256];  // [buffer][Q | dO]
-  __shared__ __attribute__((aligned(16))) char v_s[BK * 256];
   __shared__ __attribute__((aligned(16))) float st_s[2][2][BK];       // [buffer][lse2 (+inf: P = 0) | delta]
   int kb, bh, beg, end, slot;
   if (!owner_of<TASKS>(a, kb, bh, beg, end, slot)) return;
@@ -316,16 +318,14 @@ __global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
     const int P = (wv * 4 + i) * 64 + l, R = P >> 4;
     ld_off[i] = (unsigned)R * 256 + (unsigned)(((P & 15) ^ swz(R)) * 16);
   }
-  {
-    const srd_t rv = make_srd(a.v + head * HD, head_bytes);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(rv, v_s + wv * 4096 + i * 1024, ld_off[i], (unsigned)kb * (BK * 256));
-  }
-  ev8 kreg[8];
+  ev8 kreg[8], vreg[8];
   {
     const size_t off = (head + (size_t)kb * BK + key) * HD + 8 * hi;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) kreg[ks] = *reinterpret_cast<const ev8*>(a.k + off + 16 * ks);
+    for (int ks = 0; ks < 8; ++ks) {
+      kreg[ks] = *reinterpret_cast<const ev8*>(a.k + off + 16 * ks);
+      if (PART == 2) vreg[ks] = *reinterpret_cast<const ev8*>(a.v + off + 16 * ks);
+    }
   }
   // stage query block i (Q, dO); wave 0 returns lane l's lse2 / delta of row i * 64 + l
   auto issue = [&](int i, int sb, float& ls, float& dl) {
@@ -387,7 +387,8 @@ __global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) s = emfma(elds16(qt, aoff[ks]), kreg[ks], s);
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) dp = emfma(elds16(dt, aoff[ks]), elds16(v_s, boff[ks]), dp);
+    for (int ks = 0; ks < 8; ++ks)
+      if (PART == 2) dp = emfma(elds16(dt, aoff[ks]), vreg[ks], dp);
     float p[16], ds[16];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -404,10 +405,13 @@ __global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
     const ev8 sa = epack8(&ds[0]), sb8 = epack8(&ds[8]);
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      dv[db] = emfma(ecat_tr(lds_read_tr(dt, toff[0][db]), lds_read_tr(dt, toff[1][db])), pa, dv[db]);
-      dv[db] = emfma(ecat_tr(lds_read_tr(dt + 4096, toff[0][db]), lds_read_tr(dt + 4096, toff[1][db])), pb, dv[db]);
-      dk[db] = emfma(ecat_tr(lds_read_tr(qt, toff[0][db]), lds_read_tr(qt, toff[1][db])), sa, dk[db]);
-      dk[db] = emfma(ecat_tr(lds_read_tr(qt + 4096, toff[0][db]), lds_read_tr(qt + 4096, toff[1][db])), sb8, dk[db]);
+      if (PART == 1) {
+        dv[db] = emfma(ecat_tr(lds_read_tr(dt, toff[0][db]), lds_read_tr(dt, toff[1][db])), pa, dv[db]);
+        dv[db] = emfma(ecat_tr(lds_read_tr(dt + 4096, toff[0][db]), lds_read_tr(dt + 4096, toff[1][db])), pb, dv[db]);
+      } else {
+        dk[db] = emfma(ecat_tr(lds_read_tr(qt, toff[0][db]), lds_read_tr(qt, toff[1][db])), sa, dk[db]);
+        dk[db] = emfma(ecat_tr(lds_read_tr(qt + 4096, toff[0][db]), lds_read_tr(qt + 4096, toff[1][db])), sb8, dk[db]);
+      }
     }
     dma_wait();
     if (j + 1 < nc && wv == 0) {
@@ -419,70 +423,57 @@ __global__ __launch_bounds__(256, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
   }
 
   // sum the query-half partials: qh = 1 waves hand theirs to the qh = 0 waves of the same key half
-  float* xk = reinterpret_cast<float*>(&qd_s[0][0][0]) + kh * (2 * 64 * 64);
-  float* xv = xk + 64 * 64;
+  f32x16* acc = PART == 1 ? dv : dk;
+  float* xa = reinterpret_cast<float*>(&qd_s[0][0][0]) + kh * (64 * 64);
   if (qh == 1) {
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        xk[(db * 16 + r) * 64 + l] = dk[db][r];
-        xv[(db * 16 + r) * 64 + l] = dv[db][r];
-      }
+      for (int r = 0; r < 16; ++r) xa[(db * 16 + r) * 64 + l] = acc[db][r];
   }
   __syncthreads();
   if (qh == 1) return;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      dk[db][r] += xk[(db * 16 + r) * 64 + l];
-      dv[db][r] += xv[(db * 16 + r) * 64 + l];
-    }
+    for (int r = 0; r < 16; ++r) acc[db][r] += xa[(db * 16 + r) * 64 + l];
   const size_t tok = head + (size_t)kb * BK + key;
   if (TASKS && slot >= 0) {
-    float* pk = a.part_a + ((size_t)slot * BK + key) * HD;
-    float* pv = a.part_b + ((size_t)slot * BK + key) * HD;
+    float* pa_out = (PART == 1 ? a.part_b : a.part_a) + ((size_t)slot * BK + key) * HD;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = 32 * db + 8 * i + 4 * hi;
-        *reinterpret_cast<float4*>(pk + c) = make_float4(dk[db][4 * i], dk[db][4 * i + 1], dk[db][4 * i + 2], dk[db][4 * i + 3]);
-        *reinterpret_cast<float4*>(pv + c) = make_float4(dv[db][4 * i], dv[db][4 * i + 1], dv[db][4 * i + 2], dv[db][4 * i + 3]);
-      }
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<float4*>(pa_out + 32 * db + 8 * i + 4 * hi) =
+            make_float4(acc[db][4 * i], acc[db][4 * i + 1], acc[db][4 * i + 2], acc[db][4 * i + 3]);
     return;
   }
-  // valid keys: dK / dV + add / cnt; padding keys: 0
+  // valid keys: dK or dV + add / cnt; padding keys: 0
   const float inv = kvalid ? 1.0f / (float)kcnt : 0.0f;
   const float keep = kvalid ? 1.0f : 0.0f;
-  const float* adk = a.add_a + ((size_t)bh * a.add_nb + kb) * HD;
-  const float* adv = a.add_b + ((size_t)bh * a.add_nb + kb) * HD;
+  const float* add = PART == 1 ? a.add_b : a.add_a;
+  const float* adp = add + ((size_t)bh * a.add_nb + kb) * HD;
+  float* out32 = PART == 1 ? a.out_b32 : a.out_a32;
+  e16_t* out16 = PART == 1 ? a.out_b : a.out_a;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = 32 * db + 8 * i + 4 * hi;
-      f32x4 xk4, xv4;
+      f32x4 x4;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        xk4[e] = dk[db][4 * i + e] * keep;
-        xv4[e] = dv[db][4 * i + e] * keep;
-      }
-      if (a.add_a != nullptr) xk4 += *reinterpret_cast<const f32x4*>(adk + c) * inv;
-      if (a.add_b != nullptr) xv4 += *reinterpret_cast<const f32x4*>(adv + c) * inv;
-      if (a.out_a32 != nullptr) {
-        *reinterpret_cast<f32x4*>(a.out_a32 + tok * HD + c) = xk4;
-        *reinterpret_cast<f32x4*>(a.out_b32 + tok * HD + c) = xv4;
+      for (int e = 0; e < 4; ++e) x4[e] = acc[db][4 * i + e] * keep;
+      if (add != nullptr) x4 += *reinterpret_cast<const f32x4*>(adp + c) * inv;
+      if (out32 != nullptr) {
+        *reinterpret_cast<f32x4*>(out32 + tok * HD + c) = x4;
       } else {
-        ushort4 k4, v4;
-        k4.x = f2e(xk4[0]); k4.y = f2e(xk4[1]); k4.z = f2e(xk4[2]); k4.w = f2e(xk4[3]);
-        v4.x = f2e(xv4[0]); v4.y = f2e(xv4[1]); v4.z = f2e(xv4[2]); v4.w = f2e(xv4[3]);
-        *reinterpret_cast<ushort4*>(a.out_a + tok * HD + c) = k4;
-        *reinterpret_cast<ushort4*>(a.out_b + tok * HD + c) = v4;
+        ushort4 o4;
+        o4.x = f2e(x4[0]); o4.y = f2e(x4[1]); o4.z = f2e(x4[2]); o4.w = f2e(x4[3]);
+        *reinterpret_cast<ushort4*>(out16 + tok * HD + c) = o4;
       }
     }
 }
+
 
 template <bool TASKS>
 __global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
@@ -735,7 +726,8 @@ extern "C" int ES_VSA_API(vsa_attn_bwd_kv)(const void* q, const void* k, const v
   }
   const long long grid = 8LL * BH * a.per_xcd;
   ES_REQUIRE(grid < (1LL << 31), ES_ERR_UNSUPPORTED, "VSA: grid too large");
-  hipLaunchKernelGGL(vsa_bwd_kv_kernel<false>, dim3((unsigned)grid), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 1>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 2>), dim3((unsigned)grid), dim3(256), 0, stream, a);
   return check_launch("vsa_attn_bwd_kv");
 }
 
@@ -759,7 +751,8 @@ extern "C" int ES_VSA_API(vsa_attn_bwd_kv_tasks)(const void* q, const void* k, c
   a.out_b = (e16_t*)dv;
   a.part_a = part_dk;
   a.part_b = part_dv;
-  hipLaunchKernelGGL(vsa_bwd_kv_kernel<true>, dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<true, 1>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<true, 2>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
   return check_launch("vsa_attn_bwd_kv_tasks");
 }
 
