@@ -15,7 +15,8 @@
 //   rep_bwd_q_kernel    dQ over the same stream (S^T, dP^T, dQ^T += K^T dS^T), deterministic.
 //   rep_bwd_tab_kernel  dK / dV of the representative tables, KV-owner: a workgroup owns 64 table rows and walks
 //                       every query block that has one of its pairs in the tier (pairs outside get P = 0), so the
-//                       shared rows need no atomics. Tier-A token dK / dV come from the fine KV-owner kernel.
+//                       shared rows need no atomics; a dV pass and a dK pass (two waves per SIMD, 119.8 -> 118.0 ms
+//                       per C4 step at B = 1). Tier-A token dK / dV come from the fine KV-owner kernel.
 //   rep_unpool_kernel   dX = acc + dk_mid[group] / c_group + dk_tail[blk] / c_blk on valid rows (the adjoint of the
 //                       means), tier_b_lists_kernel (A|B lists minus tier A), row_dot_kernel (delta).
 #include "../../include/vsa_hip.h"
@@ -359,10 +360,12 @@ __device__ __forceinline__ unsigned long long tier_mask(const TabArgs& a, size_t
   return nblk >= 64 ? m : (m & ((1ull << nblk) - 1ull));
 }
 
-// grid (rows_pad / 64, BH), 256 threads; the fine KV-owner layout (2 key halves x 2 query halves), V in LDS
-__global__ __launch_bounds__(256, 1) void rep_bwd_tab_kernel(TabArgs a) {
+// grid (rows_pad / 64, BH), 256 threads; the fine KV-owner layout (2 key halves x 2 query halves). Two passes with
+// one accumulator set each, so that two waves share a SIMD: PART 1 = dV (S, dV), PART 2 = dK (S, dP with the
+// table's V rows in registers, dK).
+template <int PART>
+__global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
   __shared__ __attribute__((aligned(16))) char qd_s[2][2][BK * 256];
-  __shared__ __attribute__((aligned(16))) char v_s[BK * 256];
   __shared__ __attribute__((aligned(16))) float st_s[2][2][BK];
   const int grp = blockIdx.x, bh = blockIdx.y;
   const int tid = threadIdx.x, l = tid & 63, hi = l >> 5, lq = l & 31;
@@ -385,16 +388,14 @@ __global__ __launch_bounds__(256, 1) void rep_bwd_tab_kernel(TabArgs a) {
     const int P = (wv * 4 + i) * 64 + l, R = P >> 4;
     ld_off[i] = (unsigned)R * 256 + (unsigned)(((P & 15) ^ swz(R)) * 16);
   }
+  ev8 kreg[8], vreg[8];
   {
-    const srd_t rv = make_srd(a.v_tab + (size_t)bh * a.rows_pad * HD, (unsigned)((size_t)a.rows_pad * HD * 2));
+    const size_t off = ((size_t)bh * a.rows_pad + trow) * HD + 8 * hi;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(rv, v_s + wv * 4096 + i * 1024, ld_off[i], (unsigned)grp * (BK * 256));
-  }
-  ev8 kreg[8];
-  {
-    const e16_t* kp = a.k_tab + ((size_t)bh * a.rows_pad + trow) * HD + 8 * hi;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) kreg[ks] = *reinterpret_cast<const ev8*>(kp + 16 * ks);
+    for (int ks = 0; ks < 8; ++ks) {
+      kreg[ks] = *reinterpret_cast<const ev8*>(a.k_tab + off + 16 * ks);
+      if (PART == 2) vreg[ks] = *reinterpret_cast<const ev8*>(a.v_tab + off + 16 * ks);
+    }
   }
   auto issue = [&](int i, int sb, float& ls, float& dl) {
     const unsigned soff = (unsigned)i * (BK * 256);
@@ -418,12 +419,9 @@ __global__ __launch_bounds__(256, 1) void rep_bwd_tab_kernel(TabArgs a) {
     }
     return a.NB;
   };
-  int aoff[8], boff[8];
+  int aoff[8];
 #pragma unroll
-  for (int ks = 0; ks < 8; ++ks) {
-    aoff[ks] = qh * 8192 + tile_off(lq, 2 * ks + hi);
-    boff[ks] = kh * 8192 + tile_off(lq, 2 * ks + hi);
-  }
+  for (int ks = 0; ks < 8; ++ks) aoff[ks] = qh * 8192 + tile_off(lq, 2 * ks + hi);
   int toff[2][4];
   {
     const int g1 = (l >> 4) & 1, sub = (l & 1) * 8, rowA = 4 * hi + ((l & 15) >> 2);
@@ -467,7 +465,8 @@ __global__ __launch_bounds__(256, 1) void rep_bwd_tab_kernel(TabArgs a) {
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) s = emfma(elds16(qt, aoff[ks]), kreg[ks], s);
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) dp = emfma(elds16(dt, aoff[ks]), elds16(v_s, boff[ks]), dp);
+    for (int ks = 0; ks < 8; ++ks)
+      if (PART == 2) dp = emfma(elds16(dt, aoff[ks]), vreg[ks], dp);
     float p[16], ds[16];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -484,10 +483,13 @@ __global__ __launch_bounds__(256, 1) void rep_bwd_tab_kernel(TabArgs a) {
     const ev8 sa = epack8(&ds[0]), sb8 = epack8(&ds[8]);
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      dv[db] = emfma(ecat_tr(lds_read_tr(dt, toff[0][db]), lds_read_tr(dt, toff[1][db])), pa, dv[db]);
-      dv[db] = emfma(ecat_tr(lds_read_tr(dt + 4096, toff[0][db]), lds_read_tr(dt + 4096, toff[1][db])), pb, dv[db]);
-      dk[db] = emfma(ecat_tr(lds_read_tr(qt, toff[0][db]), lds_read_tr(qt, toff[1][db])), sa, dk[db]);
-      dk[db] = emfma(ecat_tr(lds_read_tr(qt + 4096, toff[0][db]), lds_read_tr(qt + 4096, toff[1][db])), sb8, dk[db]);
+      if (PART == 1) {
+        dv[db] = emfma(ecat_tr(lds_read_tr(dt, toff[0][db]), lds_read_tr(dt, toff[1][db])), pa, dv[db]);
+        dv[db] = emfma(ecat_tr(lds_read_tr(dt + 4096, toff[0][db]), lds_read_tr(dt + 4096, toff[1][db])), pb, dv[db]);
+      } else {
+        dk[db] = emfma(ecat_tr(lds_read_tr(qt, toff[0][db]), lds_read_tr(qt, toff[1][db])), sa, dk[db]);
+        dk[db] = emfma(ecat_tr(lds_read_tr(qt + 4096, toff[0][db]), lds_read_tr(qt + 4096, toff[1][db])), sb8, dk[db]);
+      }
     }
     dma_wait();
     if (inext < a.NB && wv == 0) {
@@ -501,34 +503,26 @@ __global__ __launch_bounds__(256, 1) void rep_bwd_tab_kernel(TabArgs a) {
     mnext = mnn;
   }
 
-  float* xk = reinterpret_cast<float*>(&qd_s[0][0][0]) + kh * (2 * 64 * 64);
-  float* xv = xk + 64 * 64;
+  f32x16* acc = PART == 1 ? dv : dk;
+  float* xa = reinterpret_cast<float*>(&qd_s[0][0][0]) + kh * (64 * 64);
   if (qh == 1) {
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        xk[(db * 16 + r) * 64 + l] = dk[db][r];
-        xv[(db * 16 + r) * 64 + l] = dv[db][r];
-      }
+      for (int r = 0; r < 16; ++r) xa[(db * 16 + r) * 64 + l] = acc[db][r];
   }
   __syncthreads();
   if (qh == 1) return;
-  float* gk = a.dk_tab + ((size_t)bh * a.rows_pad + trow) * HD;
-  float* gv = a.dv_tab + ((size_t)bh * a.rows_pad + trow) * HD;
+  float* g = (PART == 1 ? a.dv_tab : a.dk_tab) + ((size_t)bh * a.rows_pad + trow) * HD;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = 32 * db + 8 * i + 4 * hi;
-      f32x4 xk4, xv4;
+      f32x4 x4;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        xk4[e] = dk[db][4 * i + e] + xk[(db * 16 + 4 * i + e) * 64 + l];
-        xv4[e] = dv[db][4 * i + e] + xv[(db * 16 + 4 * i + e) * 64 + l];
-      }
-      *reinterpret_cast<f32x4*>(gk + c) = *reinterpret_cast<const f32x4*>(gk + c) + xk4;
-      *reinterpret_cast<f32x4*>(gv + c) = *reinterpret_cast<const f32x4*>(gv + c) + xv4;
+      for (int e = 0; e < 4; ++e) x4[e] = acc[db][4 * i + e] + xa[(db * 16 + 4 * i + e) * 64 + l];
+      *reinterpret_cast<f32x4*>(g + c) = *reinterpret_cast<const f32x4*>(g + c) + x4;
     }
 }
 
@@ -757,7 +751,8 @@ extern "C" int ES_VSA_API(vsa_rep_bwd_tables)(const void* q, const void* dout, c
   a.rows_pad = (a.rows + 63) / 64 * 64;
   a.scale_log2 = LOG2E / sqrtf((float)D);
   a.scale = 1.0f / sqrtf((float)D);
-  hipLaunchKernelGGL(rep_bwd_tab_kernel, dim3(a.rows_pad / 64, BH), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL(rep_bwd_tab_kernel<1>, dim3(a.rows_pad / 64, BH), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL(rep_bwd_tab_kernel<2>, dim3(a.rows_pad / 64, BH), dim3(256), 0, stream, a);
   return check_launch("vsa_rep_bwd_tables");
 }
 
