@@ -58,9 +58,13 @@ class _CompactState:
     its plan in place once the step has used it; with CFG branch 0 writes the other of two plans while later
     branches still read the current one (reference attention.py:72-96)."""
 
+    _serial = 0
+
     def __init__(self, L, H, device):
         nb = _cdiv(L, BK)
         self.L, self.H, self.device = L, H, device
+        _CompactState._serial += 1
+        self.serial = _CompactState._serial     # identifies the layer state whose lists the plan scratch holds
         self.words = max(_next_pow2(nb) // 32, 4 * _cdiv(nb, 128))
         self.plans = []
         self.offsets = {}
@@ -97,7 +101,13 @@ class _PlanScratch:
         self.refine_counts = torch.empty(nq, H, device=device, dtype=torch.int32)
         self.means = torch.empty(nq, H, nb, device=device, dtype=torch.int32)
         self.mean_counts = torch.empty(nq, H, device=device, dtype=torch.int32)
-        self.next_offset = torch.empty(nq * BM, H, device=device)
+        self.next_offset = torch.empty(nq * BM, H, device=device)      # branch 0
+        self.next_offset1 = torch.empty(nq * BM, H, device=device)     # later branches
+        # the block selection's own lists (the rebuilt lists above stay valid for the later branches of the step)
+        self.sel_counts = torch.empty(nq, H, device=device, dtype=torch.int32)
+        self.sel_blocks = torch.zeros(nq, H, nb, device=device, dtype=torch.int32)
+        self.sel_refine = torch.empty(nq, H, refine_width, device=device, dtype=torch.int32)
+        self.built = None          # (layer state, plan, step) the rebuilt lists belong to
 
 
 class _Buffers:
@@ -106,9 +116,13 @@ class _Buffers:
     def __init__(self, L, H, D, device, refine_iters, K):
         nq, nb = _cdiv(L, BM), _cdiv(L, BK)
         self.shape = (L, H, D)
+        # block means and tile flags: branch 0's (read by its selection on the plan stream) and the later branches'
         self.k_mean = torch.empty(nb, H, D, device=device, dtype=torch.bfloat16)
         self.v_mean = torch.empty(nb, H, D, device=device, dtype=torch.bfloat16)
         self.flags = torch.empty(nq, H, device=device, dtype=torch.int32)
+        self.k_mean1 = torch.empty_like(self.k_mean)
+        self.v_mean1 = torch.empty_like(self.v_mean)
+        self.flags1 = torch.empty_like(self.flags)
         self.all_counts = torch.full((nq, H), nb, device=device, dtype=torch.int32)
         self.all_blocks = torch.arange(nb, device=device, dtype=torch.int32).expand(nq, H, nb).contiguous()
         self.reps = K.Representatives(L, H, D, device, iters=refine_iters)
@@ -140,6 +154,9 @@ class EchoSparseAttention:
         self._states = {}
         self._buffers = None
         self._plan_scratch = None
+        self._plan_stream = None        # branch 0's next-step selection runs here, overlapping later work
+        self.overlap_selection = True   # False: the selection runs on the caller's stream (A/B measurements)
+        self._plan_done = None          # event after the last selection's kernels
 
     def reset(self):
         for st in self._states.values():
@@ -150,17 +167,27 @@ class EchoSparseAttention:
         B, L, H, D = q.shape
         assert B == 1, "batch size 1 only"
         if q.device != self._device:
+            self._join_plan()
             self.backend = backends.resolve(self.gpu, q.device)
             self.K = backends.kernels(self.backend)
             self._states.clear()
             self._buffers = self._plan_scratch = None
+            self._plan_stream = None
             self._device = q.device
         if layer in self.dense_layers or _cdiv(L, BK) < MIN_BLOCKS:
             return dense_attention(q, k, v)
         return self._call_compact(q, k, v, step, branch, layer, sink, rows)
 
+    def _join_plan(self):
+        """Order the current stream after the last selection issued on the plan stream (before anything that
+        writes what it reads: the plan scratch, branch 0's block means, flags and offset)."""
+        if self._plan_done is not None:
+            torch.cuda.current_stream().wait_event(self._plan_done)
+            self._plan_done = None
+
     def _scratch(self, L, H, D, device):
         if self._buffers is None or self._buffers.shape != (L, H, D):
+            self._join_plan()
             self._buffers = None                           # one sequence shape at a time
             self._buffers = _Buffers(L, H, D, device, self.refine_iters, self.K)
         return self._buffers
@@ -183,6 +210,13 @@ class EchoSparseAttention:
         full = step == self.dense_steps - 1
         sparse = step >= self.dense_steps and branch in st.ready and st.current is not None and st.current[1] == step
         K = self.K
+        # Branch 0 selects the next step's blocks on a side stream after its attention (estimate, selection, plan
+        # packing, the offset update): that overlaps the later branches of the step. Every call that writes what
+        # the selection reads (the plan scratch, branch 0's block means, flags and offset) waits for it first; a
+        # later branch's sparse step writes none of these (its own means, flags and next offset, the rebuilt lists
+        # are reused read-only).
+        if branch == 0 or not sparse:
+            self._join_plan()
         if not (full or sparse):
             out, lse2 = K.dense_attention(q[0], k[0], v[0])
             offset.copy_(lse2)
@@ -193,40 +227,60 @@ class EchoSparseAttention:
         buf = self._scratch(L, H, D, q.device)
         ps = self._plan_scratch
         if ps is None or ps.shape != (L, H, rw):
+            self._join_plan()
             self._plan_scratch = None
             ps = self._plan_scratch = _PlanScratch(L, H, q.device, rw)
+        k_mean, v_mean = (buf.k_mean, buf.v_mean) if branch == 0 else (buf.k_mean1, buf.v_mean1)
+        flags = buf.flags if branch == 0 else buf.flags1
+        nxt = ps.next_offset if branch == 0 else ps.next_offset1
         out = torch.empty_like(q)
         if full:
             ps.keep.fill_(1)
             ps.mass.zero_()
-            K.block_attention(q, k, v, out, buf.all_counts, buf.all_blocks, offset, ps.next_offset, buf.flags,
+            ps.built = None
+            K.block_attention(q, k, v, out, buf.all_counts, buf.all_blocks, offset, nxt, flags,
                               mass=ps.mass, threshold=self.threshold)
-            K.exact_fallback(q, k, v, out, buf.all_counts, buf.all_blocks, ps.next_offset, buf.flags)
-            K.full_step_scales(offset, ps.next_offset, ps.scale_exact, ps.scale_skip, L)
+            K.exact_fallback(q, k, v, out, buf.all_counts, buf.all_blocks, nxt, flags)
+            K.full_step_scales(offset, nxt, ps.scale_exact, ps.scale_skip, L)
             st.ready.add(branch)
         else:
             exact, skip = st.plan(st.current[0])
-            K.rebuild_plan(exact, skip, ps.keep, ps.counts, ps.blocks, ps.refine, ps.refine_counts, ps.means,
-                           ps.mean_counts)
-            buf.reps.build(q, k, v, buf.k_mean, buf.v_mean)
+            key = (st.serial, st.current[0], step)
+            if ps.built != key:      # the lists of this layer's plan (a later branch reuses branch 0's)
+                self._join_plan()
+                K.rebuild_plan(exact, skip, ps.keep, ps.counts, ps.blocks, ps.refine, ps.refine_counts, ps.means,
+                               ps.mean_counts)
+                ps.built = key
+            buf.reps.build(q, k, v, k_mean, v_mean)
             if branch == 0:
                 ps.mass.zero_()
-            K.sparse_attention(q, k, v, buf.k_mean, buf.v_mean, ps.means, ps.mean_counts, out, ps.counts, ps.blocks,
-                               offset, ps.next_offset, buf.flags, ps.refine, ps.refine_counts, buf.reps.k, buf.reps.v,
+            K.sparse_attention(q, k, v, k_mean, v_mean, ps.means, ps.mean_counts, out, ps.counts, ps.blocks,
+                               offset, nxt, flags, ps.refine, ps.refine_counts, buf.reps.k, buf.reps.v,
                                buf.reps.log_counts, mass=ps.mass if branch == 0 else None, threshold=self.threshold,
                                rows=rows)
-            K.exact_fallback(q, k, v, out, ps.counts, ps.blocks, ps.next_offset, buf.flags)
-            K.compensate_fallback(q, buf.k_mean, buf.v_mean, ps.keep, ps.next_offset, out, buf.flags)
-            if branch == 0:
-                K.estimate_skipped(q, buf.k_mean, ps.keep, offset, ps.next_offset, ps.mass, ps.scale_exact,
-                                   ps.scale_skip)
-        if branch == 0:
-            # the next step's plan, after this step's last use of the current one in a single branch
-            plan = 0 if st.current is None else st.current[0] ^ (len(st.offsets) > 1)
-            exact, skip = st.plan(plan)
-            K.select_blocks(ps.mass, ps.keep, ps.scale_exact, ps.scale_skip, ps.next_keep, ps.counts, ps.blocks,
-                            buf.flags, skip, ps.refine, top, refined, L, sink=1 << 30 if sink is None else sink)
+            K.exact_fallback(q, k, v, out, ps.counts, ps.blocks, nxt, flags)
+            K.compensate_fallback(q, k_mean, v_mean, ps.keep, nxt, out, flags)
+        if branch != 0:
+            offset.copy_(nxt)
+            return out[None]
+        # the next step's plan, after this step's last use of the current one in a single branch
+        plan = 0 if st.current is None else st.current[0] ^ (len(st.offsets) > 1)
+        exact, skip = st.plan(plan)
+        main = torch.cuda.current_stream()
+        if self._plan_stream is None and self.overlap_selection:
+            self._plan_stream = torch.cuda.Stream(device=q.device)
+        side = self._plan_stream if self.overlap_selection else main
+        side.wait_stream(main)
+        q.record_stream(side)
+        with torch.cuda.stream(side):
+            if sparse:
+                K.estimate_skipped(q, k_mean, ps.keep, offset, nxt, ps.mass, ps.scale_exact, ps.scale_skip)
+            K.select_blocks(ps.mass, ps.keep, ps.scale_exact, ps.scale_skip, ps.next_keep, ps.sel_counts,
+                            ps.sel_blocks, flags, skip, ps.sel_refine, top, refined, L,
+                            sink=1 << 30 if sink is None else sink)
             K.pack_plan(ps.next_keep, exact)
-            st.pending = (plan, step + 1)
-        offset.copy_(ps.next_offset)
+            offset.copy_(nxt)
+            self._plan_done = torch.cuda.Event()
+            self._plan_done.record(side)
+        st.pending = (plan, step + 1)
         return out[None]

@@ -35,14 +35,17 @@ def run(attn, inputs, branches=1, layer=1):
     for step, (q, k, v) in enumerate(inputs):
         for branch in range(branches):
             outs.append(attn(q, k, v, step, branch, layer=layer))
+    torch.cuda.synchronize()      # branch 0's selection runs on a side stream: settle it before reading state
     return outs
 
 
 def call_with_selection(attn, q, k, v, step, branch=0, layer=1):
     """One sparse call; returns its output and the block selection it used (counts, blocks, refine list)."""
+    torch.cuda.synchronize()
     st = attn._states[layer]
     exact, skip = (x.clone() for x in st.plan(st.pending[0] if branch == 0 else st.current[0]))
     out = attn(q, k, v, step, branch, layer=layer)
+    torch.cuda.synchronize()
     Hh, nq, _ = exact.shape
     nb = -(-q.shape[1] // 64)
     keep = torch.empty(Hh, nq, nb, device="cuda", dtype=torch.uint8)
@@ -54,13 +57,15 @@ def call_with_selection(attn, q, k, v, step, branch=0, layer=1):
     return out, (counts, blocks, refine)
 
 
-def check_formula(out, qkv, selection, buf):
+def check_formula(out, qkv, selection, buf, branch=0):
     """Exact tokens of the listed blocks, block means of the other skipped blocks and four representatives of each
-    refined block, all in one softmax (reference tests/test_attention.py:72-100)."""
+    refined block, all in one softmax (reference tests/test_attention.py:72-100). The block means are the branch's
+    own (branch 0 keeps its set for its selection on the plan stream)."""
     out = out[0].float()
     q, k, v = (x[0].float() for x in qkv)
     counts, blocks, refine = selection
-    nb = buf.k_mean.shape[0]
+    k_mean, v_mean = (buf.k_mean, buf.v_mean) if branch == 0 else (buf.k_mean1, buf.v_mean1)
+    nb = k_mean.shape[0]
     block_len = torch.full((nb,), 64.0, device="cuda")
     block_len[-1] = L - 64 * (nb - 1)
     for h in range(H):
@@ -73,7 +78,7 @@ def check_formula(out, qkv, selection, buf):
             for b in exact:
                 tok = torch.arange(64 * b, min(64 * b + 64, L), device="cuda")
                 keys.append(k[tok, h]); vals.append(v[tok, h]); bias.append(torch.zeros(len(tok), device="cuda"))
-            keys.append(buf.k_mean[means, h].float()); vals.append(buf.v_mean[means, h].float())
+            keys.append(k_mean[means, h].float()); vals.append(v_mean[means, h].float())
             bias.append(block_len[means].log())
             for b in refined:
                 sl = slice(4 * b, 4 * b + 4)
@@ -122,7 +127,7 @@ def test_second_cfg_branch_matches_formula():
     _, first = call_with_selection(attn, *cond[2], 2, branch=0)
     out, second = call_with_selection(attn, *uncond[2], 2, branch=1)
     assert all(torch.equal(a, b) for a, b in zip(first, second))
-    check_formula(out, uncond[2], second, attn._buffers)
+    check_formula(out, uncond[2], second, attn._buffers, branch=1)
 
 
 def test_fallback_tiles():
@@ -178,6 +183,7 @@ def test_rows_skip_only_unused_tiles():
     st, ps, buf = attn._states[1], None, attn._buffers
     exact, skip = st.plan(st.pending[0])
     attn(*inputs[2], 2, 0, layer=1)          # builds scratch and representatives for this shape
+    torch.cuda.synchronize()
     ps = attn._plan_scratch
     K.rebuild_plan(exact, skip, ps.keep, ps.counts, ps.blocks, ps.refine, ps.refine_counts, ps.means,
                    ps.mean_counts)
@@ -224,6 +230,7 @@ def run_steps(attn, n, branches, sink=None):
         for step in range(n):
             for branch in range(branches):
                 attn(*data[branch][step], step, branch, 1, sink=sink)
+    torch.cuda.synchronize()
     return attn._states[1]
 
 
