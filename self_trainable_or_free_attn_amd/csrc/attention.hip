@@ -62,9 +62,9 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char kv_s[2][2][BK * 256];
   __shared__ __attribute__((aligned(16))) float bias_s[2][BK];
   __shared__ float mass_s[16][129];  // [wave * 4 + row of 16 lanes][chunk % 128], rows padded against bank conflicts
-  // list entries of chunks j, j+1, j+2 (ring slot j % 3), staged from global memory straight into LDS two chunks
+  // list entries of chunks j .. j+3 (ring slot j % 4), staged from global memory straight into LDS three chunks
   // ahead, so the loop holds no global->register or scalar loads whose waits would also drain the K / V loads
-  __shared__ int ids_s[3][64];
+  __shared__ int ids_s[4][64];
   __shared__ float lc_s[BK];  // log2 counts of the next representative chunk's columns (wave 0, global -> LDS)
 
   // XCD-aware tile order: dispatch slot w runs on XCD w % 8; each XCD walks a contiguous run of tiles of one head
@@ -134,7 +134,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   // word); mean -> the ids of its 64 columns; rep -> the refined block of each of its 64 columns
   auto stage_ids = [&](int cj) {
     if (MODE == COMPENSATE || wv != 0 || cj >= nc || (cj < n && g_ex == nullptr)) return;
-    int* dst = ids_s[cj % 3];
+    int* dst = ids_s[cj & 3];
     if (cj < n) {
       dma4(make_srd(g_ex, (unsigned)n * 4u), dst, 0, (unsigned)cj * 4u);
     } else if (cj < n + cm) {
@@ -147,7 +147,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   auto read_ids = [&](int cj) -> ChunkIds {
     ChunkIds c = {};
     if (MODE == COMPENSATE || cj >= nc) return c;
-    const int* src = ids_s[cj % 3];
+    const int* src = ids_s[cj & 3];
     if (cj < n) {
       c.row[0] = g_ex == nullptr ? cj : __builtin_amdgcn_readfirstlane(src[0]);
     } else if (cj < n + cm) {
@@ -356,6 +356,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
 
   stage_ids(0);
   stage_ids(1);
+  stage_ids(2);
   dma_wait();
   __syncthreads();
   int cur_row = 0;  // exact block id of the chunk being computed
@@ -372,13 +373,18 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   dma_wait();
   __syncthreads();
 
+  // exact block id of chunk j + 1, read from the ring one chunk early so that the LDS latency of the read is
+  // spent under the previous chunk's compute rather than in front of the next transfers
+  int pre_v = (nc > 1 && 1 < n && g_ex != nullptr) ? ids_s[1][0] : 1;
   for (int j = 0; j < nc; ++j) {
     const int sb = j & 1;
     float bnext = 0.0f;
     int next_row = 0;
     bool next_lc = false;  // the next chunk's bias comes from lc_s
     if (j + 1 < nc) {
-      const ChunkIds c = read_ids(j + 1);
+      ChunkIds c;
+      if (j + 1 < n) { c = ChunkIds{}; c.row[0] = __builtin_amdgcn_readfirstlane(pre_v); }
+      else c = read_ids(j + 1);
       next_row = c.row[0];
       next_lc = COMP && j + 1 >= n + cm && c.brow >= 0;
       Dma dn;
@@ -386,7 +392,8 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
       dma_k(dn, sb ^ 1);
       dma_v(dn, sb ^ 1);
     }
-    stage_ids(j + 2);
+    stage_ids(j + 3);
+    pre_v = (j + 2 < n && g_ex != nullptr) ? ids_s[(j + 2) & 3][0] : j + 2;
     const bool biased = MODE == COMPENSATE || j >= n || (tail_block && cur_row == nb - 1);
     if (!COMP || biased)   // (non-COMP variants: one instantiation keeps them within 256 VGPRs)
       compute(j, sb, std::true_type{});
