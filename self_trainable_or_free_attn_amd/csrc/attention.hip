@@ -17,6 +17,7 @@
 #include "../../include/echosparse_hip.h"
 #include "common.h"
 
+#include <atomic>
 #include <type_traits>
 
 namespace es {
@@ -46,6 +47,8 @@ struct AttnArgs {
   float* lse;
   int* flags;  // FIXED: written; ONLINE / COMPENSATE: read (nullptr = every tile)
   float* mass;
+  int* queues;  // FIXED: 8 tile-queue counters, zero at launch
+  int fixed;    // FIXED: items per queue assigned by dispatch slot; the rest are claimed
   int L, Lk, H, nq, nb, NK, RW, tiles, per_xcd;  // L query rows, Lk key rows (Lk == L but in dense_kv)
   float threshold, tail_log2, scale;
 };
@@ -57,8 +60,9 @@ struct ChunkIds {
 };
 
 
+// one (query tile t, head h)
 template <int MODE, bool COMP, bool MASS>
-__global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
+__device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const int t) {
   __shared__ __attribute__((aligned(16))) char kv_s[2][2][BK * 256];
   __shared__ __attribute__((aligned(16))) float bias_s[2][BK];
   __shared__ float mass_s[16][129];  // [wave * 4 + row of 16 lanes][chunk % 128], rows padded against bank conflicts
@@ -67,12 +71,6 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   __shared__ int ids_s[4][64];
   __shared__ float lc_s[BK];  // log2 counts of the next representative chunk's columns (wave 0, global -> LDS)
 
-  // XCD-aware tile order: dispatch slot w runs on XCD w % 8; each XCD walks a contiguous run of tiles of one head
-  const int w = blockIdx.x;
-  const int xcd = w & 7, slot = w >> 3;
-  const int h = slot / a.per_xcd;
-  const int t = xcd * a.per_xcd + slot % a.per_xcd;
-  if (h >= a.H || t >= a.tiles) return;
   const int th = t * a.H + h;
   if (MODE != FIXED && a.flags != nullptr && sload(a.flags + th) == 0) return;
 
@@ -465,12 +463,100 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   }
 }
 
+// Work items: queue x (x = 0..7) holds, head by head, a contiguous run of per_xcd tiles, the run of head h being
+// run (x + h) % 8, so that every queue sees every region of the video. Dispatch slot w runs on XCD w % 8, and
+// neighbouring tiles (which share most K / V blocks in Morton order) then share that XCD's L2.
+__device__ __forceinline__ int item_tile(const AttnArgs& a, int x, int k, int& h) {
+  h = k / a.per_xcd;
+  return ((x + h) & 7) * a.per_xcd + k % a.per_xcd;
+}
+
+// FIXED launches balance the XCDs at run time (they do not run equally fast, and the tiles differ in work): the
+// first `fixed` items of every queue go to dispatch slots 0 .. fixed-1 as above, and the workgroups after them
+// claim the remaining items through the queue counters, their own queue first, then the others in turn, so that an
+// XCD that runs ahead takes over the tail of a slower one. There are twice as many claiming workgroups as
+// claimable items; the ones that find every queue drained leave at once, and none waits for another.
+__device__ __forceinline__ int claim_item(int* queues, int home, int fixed, int per_queue) {
+  const int l = threadIdx.x & 63;
+  const int x = (home + l) & 7;
+  // one round trip finds the queues that may still hold items; claims are tried on those only
+  const int seen = l < 8 ? __atomic_load_n(queues + x, __ATOMIC_RELAXED) : per_queue;
+  unsigned long long open = __ballot(seen < per_queue - fixed);
+  int item = -1;
+  if (l == 0) {
+    while (open) {
+      const int k = __builtin_ctzll(open);
+      open &= open - 1;
+      const int xq = (home + k) & 7;
+      const int i = atomicAdd(queues + xq, 1);
+      if (i < per_queue - fixed) {
+        item = xq * per_queue + fixed + i;
+        break;
+      }
+    }
+  }
+  return item;
+}
+
+template <int MODE, bool COMP, bool MASS>
+__global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
+  const int w = blockIdx.x;
+  int h, t;
+  if (MODE == FIXED && (w >> 3) >= a.fixed) {
+    __shared__ int item_s;
+    if (threadIdx.x < 64) {
+      const int it = claim_item(a.queues, w & 7, a.fixed, a.H * a.per_xcd);
+      if (threadIdx.x == 0) item_s = it;
+    }
+    __syncthreads();
+    const int it = __builtin_amdgcn_readfirstlane(item_s);
+    if (it < 0) return;
+    const int per_queue = a.H * a.per_xcd;
+    const int x = it / per_queue;
+    t = item_tile(a, x, it - x * per_queue, h);
+  } else {
+    t = item_tile(a, w & 7, w >> 3, h);
+  }
+  if (h >= a.H || t >= a.tiles) return;
+  attn_tile<MODE, COMP, MASS>(a, h, t);
+}
+
+__global__ __launch_bounds__(64) void zero_queues_kernel(int* q) {
+  if (threadIdx.x < 8) q[threadIdx.x] = 0;
+}
+
+// Tile-queue counters of the FIXED launches: a ring of 64 slots of 8 counters in this module's device memory (one
+// copy per GPU), one slot per launch, cleared on the launch's stream just before it. Launches on one GPU that run
+// at the same time therefore get different slots unless 64 or more of them overlap.
+__device__ int es_attn_queues[64 * 8];
+
+static int* queue_slot() {
+  static std::atomic<int*> base[64];
+  static std::atomic<unsigned> seq{0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  int* p = base[dev].load();
+  if (p == nullptr) {
+    if (hipGetSymbolAddress((void**)&p, HIP_SYMBOL(es_attn_queues)) != hipSuccess) return nullptr;
+    base[dev].store(p);
+  }
+  return p + (seq.fetch_add(1) % 64) * 8;
+}
+
 template <int MODE, bool COMP, bool MASS>
 static int launch(const AttnArgs& a0, hipStream_t stream, const char* what) {
   AttnArgs a = a0;
   a.per_xcd = (a.tiles + 7) / 8;
-  const long long grid = 8LL * a.H * a.per_xcd;
+  long long grid = 8LL * a.H * a.per_xcd;
   if (grid <= 0) return ES_OK;
+  if (MODE == FIXED) {
+    a.queues = queue_slot();
+    ES_REQUIRE(a.queues != nullptr, ES_ERR_LAUNCH, "tile queues unavailable on the current device");
+    const int per_queue = a.H * a.per_xcd, claimable = (per_queue + 7) / 8;
+    a.fixed = per_queue - claimable;
+    grid = 8LL * (a.fixed + 2 * claimable);
+    hipLaunchKernelGGL(zero_queues_kernel, dim3(1), dim3(64), 0, stream, a.queues);
+  }
   hipLaunchKernelGGL((attn_kernel<MODE, COMP, MASS>), dim3((unsigned)grid), dim3(256), 0, stream, a);
   return check_launch(what);
 }
