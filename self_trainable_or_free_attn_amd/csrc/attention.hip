@@ -16,8 +16,8 @@
 // k_rep / v_rep.
 #include "../../include/echosparse_hip.h"
 #include "common.h"
+#include "queues.h"
 
-#include <atomic>
 #include <type_traits>
 
 namespace es {
@@ -47,8 +47,8 @@ struct AttnArgs {
   float* lse;
   int* flags;  // FIXED: written; ONLINE / COMPENSATE: read (nullptr = every tile)
   float* mass;
-  int* queues;  // FIXED: 8 tile-queue counters, zero at launch
-  int fixed;    // FIXED: items per queue assigned by dispatch slot; the rest are claimed
+  int* queues;  // FIXED: the eight tile-queue counters of this launch (queues.h)
+  int fixed;    // items per queue bound to dispatch slots; FIXED launches claim the rest
   int L, Lk, H, nq, nb, NK, RW, tiles, per_xcd;  // L query rows, Lk key rows (Lk == L but in dense_kv)
   float threshold, tail_log2, scale;
 };
@@ -463,84 +463,28 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
   }
 }
 
-// Work items: queue x (x = 0..7) holds, head by head, a contiguous run of per_xcd tiles, the run of head h being
-// run (x + h) % 8, so that every queue sees every region of the video. Dispatch slot w runs on XCD w % 8, and
-// neighbouring tiles (which share most K / V blocks in Morton order) then share that XCD's L2.
-__device__ __forceinline__ int item_tile(const AttnArgs& a, int x, int k, int& h) {
-  h = k / a.per_xcd;
-  return ((x + h) & 7) * a.per_xcd + k % a.per_xcd;
-}
-
-// FIXED launches balance the XCDs at run time (they do not run equally fast, and the tiles differ in work): the
-// first `fixed` items of every queue go to dispatch slots 0 .. fixed-1 as above, and the workgroups after them
-// claim the remaining items through the queue counters, their own queue first, then the others in turn, so that an
-// XCD that runs ahead takes over the tail of a slower one. There are twice as many claiming workgroups as
-// claimable items; the ones that find every queue drained leave at once, and none waits for another.
-__device__ __forceinline__ int claim_item(int* queues, int home, int fixed, int per_queue) {
-  const int l = threadIdx.x & 63;
-  const int x = (home + l) & 7;
-  // one round trip finds the queues that may still hold items; claims are tried on those only
-  const int seen = l < 8 ? __atomic_load_n(queues + x, __ATOMIC_RELAXED) : per_queue;
-  unsigned long long open = __ballot(seen < per_queue - fixed);
-  int item = -1;
-  if (l == 0) {
-    while (open) {
-      const int k = __builtin_ctzll(open);
-      open &= open - 1;
-      const int xq = (home + k) & 7;
-      const int i = atomicAdd(queues + xq, 1);
-      if (i < per_queue - fixed) {
-        item = xq * per_queue + fixed + i;
-        break;
-      }
-    }
-  }
-  return item;
-}
-
+// XCD-aware, run-time balanced tile order (queues.h); the ONLINE / COMPENSATE launches, which skip unflagged
+// tiles, bind every item to its dispatch slot
 template <int MODE, bool COMP, bool MASS>
 __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
-  const int w = blockIdx.x;
-  int h, t;
-  if (MODE == FIXED && (w >> 3) >= a.fixed) {
+  const int w = blockIdx.x, per_queue = a.H * a.per_xcd;
+  int x = w & 7, k = w >> 3;
+  if (MODE == FIXED && k >= a.fixed) {
     __shared__ int item_s;
     if (threadIdx.x < 64) {
-      const int it = claim_item(a.queues, w & 7, a.fixed, a.H * a.per_xcd);
+      const int it = claim_item(a.queues, x, a.fixed, per_queue);
       if (threadIdx.x == 0) item_s = it;
     }
     __syncthreads();
     const int it = __builtin_amdgcn_readfirstlane(item_s);
     if (it < 0) return;
-    const int per_queue = a.H * a.per_xcd;
-    const int x = it / per_queue;
-    t = item_tile(a, x, it - x * per_queue, h);
-  } else {
-    t = item_tile(a, w & 7, w >> 3, h);
+    x = it / per_queue;
+    k = it - x * per_queue;
   }
+  const int h = k / a.per_xcd;
+  const int t = ((x + h) & 7) * a.per_xcd + k % a.per_xcd;
   if (h >= a.H || t >= a.tiles) return;
   attn_tile<MODE, COMP, MASS>(a, h, t);
-}
-
-__global__ __launch_bounds__(64) void zero_queues_kernel(int* q) {
-  if (threadIdx.x < 8) q[threadIdx.x] = 0;
-}
-
-// Tile-queue counters of the FIXED launches: a ring of 64 slots of 8 counters in this module's device memory (one
-// copy per GPU), one slot per launch, cleared on the launch's stream just before it. Launches on one GPU that run
-// at the same time therefore get different slots unless 64 or more of them overlap.
-__device__ int es_attn_queues[64 * 8];
-
-static int* queue_slot() {
-  static std::atomic<int*> base[64];
-  static std::atomic<unsigned> seq{0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  int* p = base[dev].load();
-  if (p == nullptr) {
-    if (hipGetSymbolAddress((void**)&p, HIP_SYMBOL(es_attn_queues)) != hipSuccess) return nullptr;
-    base[dev].store(p);
-  }
-  return p + (seq.fetch_add(1) % 64) * 8;
 }
 
 template <int MODE, bool COMP, bool MASS>
@@ -549,13 +493,13 @@ static int launch(const AttnArgs& a0, hipStream_t stream, const char* what) {
   a.per_xcd = (a.tiles + 7) / 8;
   long long grid = 8LL * a.H * a.per_xcd;
   if (grid <= 0) return ES_OK;
+  a.fixed = a.H * a.per_xcd;
   if (MODE == FIXED) {
-    a.queues = queue_slot();
-    ES_REQUIRE(a.queues != nullptr, ES_ERR_LAUNCH, "tile queues unavailable on the current device");
-    const int per_queue = a.H * a.per_xcd, claimable = (per_queue + 7) / 8;
-    a.fixed = per_queue - claimable;
-    grid = 8LL * (a.fixed + 2 * claimable);
-    hipLaunchKernelGGL(zero_queues_kernel, dim3(1), dim3(64), 0, stream, a.queues);
+    Queues qs;
+    ES_REQUIRE(balanced_launch(a.H, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "tile queues unavailable on this device");
+    a.queues = qs.counters;
+    a.fixed = qs.fixed;
+    grid = qs.grid;
   }
   hipLaunchKernelGGL((attn_kernel<MODE, COMP, MASS>), dim3((unsigned)grid), dim3(256), 0, stream, a);
   return check_launch(what);

@@ -1,0 +1,103 @@
+// Run-time balancing of the per-(row block, head) attention launches over the eight XCDs.
+//
+// Work items sit in eight queues, one per XCD: queue x holds, head by head, a contiguous run of `per_xcd` row
+// blocks, the run of head h being run (x + h) % 8, so that every queue sees every region of the sequence.
+// Dispatch slot w runs on XCD w % 8 and neighbouring row blocks (which share most K / V blocks) then share that
+// XCD's L2. The XCDs do not run equally fast and the items differ in work, so only the first `fixed` items of each
+// queue are bound to dispatch slots (slot w takes item w / 8 of queue w % 8); the workgroups after them claim the
+// remaining items through the queue counters, their own XCD's queue first and then the others in turn, so that an
+// XCD that runs ahead takes over the tail of a slower one. There are twice as many claiming workgroups as
+// claimable items; those that find every queue drained leave at once, and none waits for another, so every grid
+// drains.
+//
+// The counters live in a ring of 64 slots of 8 counters in this translation unit's device memory (one copy per
+// GPU, no allocation), one slot per launch, cleared by a one-wave kernel on the launch's stream just before it:
+// launches that overlap on one GPU get distinct slots unless 64 or more of them are in flight.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+
+namespace es {
+
+// a claimable item for a workgroup whose home queue is `home`, or -1 once all eight queues are drained
+// (wave 0 only; the result is valid in lane 0)
+__device__ __forceinline__ int claim_item(int* queues, int home, int fixed, int per_queue) {
+  const int l = threadIdx.x & 63;
+  const int x = (home + l) & 7;
+  // one round trip finds the queues that may still hold items; claims are tried on those only
+  const int seen = l < 8 ? __atomic_load_n(queues + x, __ATOMIC_RELAXED) : per_queue;
+  unsigned long long open = __ballot(seen < per_queue - fixed);
+  int item = -1;
+  if (l == 0) {
+    while (open) {
+      const int k = __builtin_ctzll(open);
+      open &= open - 1;
+      const int xq = (home + k) & 7;
+      const int i = atomicAdd(queues + xq, 1);
+      if (i < per_queue - fixed) {
+        item = xq * per_queue + fixed + i;
+        break;
+      }
+    }
+  }
+  return item;
+}
+
+// This workgroup's item as (head-major index `hd`, row block `rb`) of a grid with `per_xcd` row blocks per queue
+// run and `heads` heads; false when it has none (also for padding row blocks >= n_rows). Every thread of the
+// workgroup calls it (it holds a workgroup barrier when the workgroup claims).
+__device__ __forceinline__ bool balanced_item(int* queues, int fixed, int per_xcd, int heads, int n_rows, int& hd,
+                                              int& rb) {
+  const int w = blockIdx.x, per_queue = heads * per_xcd;
+  int x = w & 7, k = w >> 3;
+  if (k >= fixed) {
+    __shared__ int item_s;
+    if (threadIdx.x < 64) {
+      const int it = claim_item(queues, x, fixed, per_queue);
+      if (threadIdx.x == 0) item_s = it;
+    }
+    __syncthreads();
+    const int it = __builtin_amdgcn_readfirstlane(item_s);
+    if (it < 0) return false;
+    x = it / per_queue;
+    k = it - x * per_queue;
+  }
+  hd = k / per_xcd;
+  rb = ((x + hd) & 7) * per_xcd + k % per_xcd;
+  return hd < heads && rb < n_rows;
+}
+
+static __device__ int es_tile_queues[64 * 8];
+
+static __global__ __launch_bounds__(64) void zero_queues_kernel(int* q) {
+  if (threadIdx.x < 8) q[threadIdx.x] = 0;
+}
+
+struct Queues {
+  int* counters = nullptr;
+  int fixed = 0;
+  long long grid = 0;
+};
+
+// Sets up one balanced launch of heads x n_rows items (n_rows split into eight runs of per_xcd): takes a counter
+// slot, clears it on `stream` and gives the grid size. false if the device's counter ring is unavailable.
+static bool balanced_launch(int heads, int per_xcd, hipStream_t stream, Queues& out) {
+  static std::atomic<int*> base[64];
+  static std::atomic<unsigned> seq{0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  int* p = base[dev].load();
+  if (p == nullptr) {
+    if (hipGetSymbolAddress((void**)&p, HIP_SYMBOL(es_tile_queues)) != hipSuccess) return false;
+    base[dev].store(p);
+  }
+  out.counters = p + (seq.fetch_add(1) % 64) * 8;
+  const int per_queue = heads * per_xcd, claimable = (per_queue + 7) / 8;
+  out.fixed = per_queue - claimable;
+  out.grid = 8LL * (out.fixed + 2LL * claimable);
+  hipLaunchKernelGGL(zero_queues_kernel, dim3(1), dim3(64), 0, stream, out.counters);
+  return true;
+}
+
+}  // namespace es

@@ -17,6 +17,7 @@
 #include "../../include/vsa_hip.h"
 #include "common.h"
 #include "elem.h"
+#include "queues.h"
 
 namespace es {
 
@@ -33,7 +34,8 @@ struct VsaFwdArgs {
   const int4* tasks;
   const int* info;  // device task count (task mode)
   float *part_o, *part_lse;
-  int L, NB, BH, per_xcd;
+  int* queues;  // the eight row-block queue counters of this launch (queues.h)
+  int L, NB, BH, per_xcd, fixed;
   float scale;  // log2(e) / sqrt(D)
 };
 
@@ -53,11 +55,8 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
     end = tk.z;
     slot = tk.w;
   } else {
-    // XCD-aware order: dispatch slot w runs on XCD w % 8; each XCD walks a contiguous run of query blocks of a head
-    const int w = blockIdx.x, xcd = w & 7, s = w >> 3;
-    bh = s / a.per_xcd;
-    qb = xcd * a.per_xcd + s % a.per_xcd;
-    if (bh >= a.BH || qb >= a.NB) return;
+    // XCD-aware, run-time balanced order of (query block, head) (queues.h)
+    if (!balanced_item(a.queues, a.fixed, a.per_xcd, a.BH, a.NB, bh, qb)) return;
     const int* rp = a.row_ptr + (size_t)bh * (a.NB + 1) + qb;
     beg = sload(rp);
     end = sload(rp + 1);
@@ -258,7 +257,8 @@ struct VsaBwdArgs {
   e16_t *out_a, *out_b;       // bf16 outputs
   float *out_a32, *out_b32;    // fp32 outputs (KV owner) / accumulator dq_acc += dQ (Q owner)
   float *part_a, *part_b;      // split partials [slot, 64, D]
-  int L, NB, BH, per_xcd;
+  int* queues;                 // the eight row-block queue counters of this launch (queues.h)
+  int L, NB, BH, per_xcd, fixed;
   float scale_log2, scale;
 };
 
@@ -275,10 +275,7 @@ __device__ __forceinline__ bool owner_of(const VsaBwdArgs& a, int& blk, int& bh,
     end = tk.z;
     slot = tk.w;
   } else {
-    const int w = blockIdx.x, xcd = w & 7, s = w >> 3;
-    bh = s / a.per_xcd;
-    blk = xcd * a.per_xcd + s % a.per_xcd;
-    if (bh >= a.BH || blk >= a.NB) return false;
+    if (!balanced_item(a.queues, a.fixed, a.per_xcd, a.BH, a.NB, bh, blk)) return false;
     const int* rp = a.row_ptr + (size_t)bh * (a.NB + 1) + blk;
     beg = sload(rp);
     end = sload(rp + 1);
@@ -656,9 +653,12 @@ extern "C" int ES_VSA_API(vsa_attn_fwd)(const void* q, const void* k, const void
   a.out = (e16_t*)out;
   a.lse = lse;
   a.per_xcd = (a.NB + 7) / 8;
-  const long long grid = 8LL * BH * a.per_xcd;
-  ES_REQUIRE(grid < (1LL << 31), ES_ERR_UNSUPPORTED, "VSA: grid too large");
-  hipLaunchKernelGGL(vsa_fwd_kernel<false>, dim3((unsigned)grid), dim3(256), 0, stream, a);
+  ES_REQUIRE(8LL * BH * a.per_xcd < (1LL << 30), ES_ERR_UNSUPPORTED, "VSA: grid too large");
+  Queues qs;
+  ES_REQUIRE(balanced_launch(BH, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "VSA: row-block queues unavailable");
+  a.queues = qs.counters;
+  a.fixed = qs.fixed;
+  hipLaunchKernelGGL(vsa_fwd_kernel<false>, dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
   return check_launch("vsa_attn_fwd");
 }
 
@@ -724,10 +724,15 @@ extern "C" int ES_VSA_API(vsa_attn_bwd_kv)(const void* q, const void* k, const v
     a.out_a = (e16_t*)dk;
     a.out_b = (e16_t*)dv;
   }
-  const long long grid = 8LL * BH * a.per_xcd;
-  ES_REQUIRE(grid < (1LL << 31), ES_ERR_UNSUPPORTED, "VSA: grid too large");
-  hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 1>), dim3((unsigned)grid), dim3(256), 0, stream, a);
-  hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 2>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+  ES_REQUIRE(8LL * BH * a.per_xcd < (1LL << 30), ES_ERR_UNSUPPORTED, "VSA: grid too large");
+  Queues qs;
+  ES_REQUIRE(balanced_launch(BH, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "VSA: row-block queues unavailable");
+  a.queues = qs.counters;
+  a.fixed = qs.fixed;
+  hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 1>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
+  ES_REQUIRE(balanced_launch(BH, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "VSA: row-block queues unavailable");
+  a.queues = qs.counters;
+  hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 2>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
   return check_launch("vsa_attn_bwd_kv");
 }
 
@@ -770,9 +775,12 @@ extern "C" int ES_VSA_API(vsa_attn_bwd_q)(const void* q, const void* k, const vo
   a.add_nb = add_nb;
   a.out_a = (e16_t*)dq;
   a.out_a32 = dq_acc;
-  const long long grid = 8LL * BH * a.per_xcd;
-  ES_REQUIRE(grid < (1LL << 31), ES_ERR_UNSUPPORTED, "VSA: grid too large");
-  hipLaunchKernelGGL(vsa_bwd_q_kernel<false>, dim3((unsigned)grid), dim3(256), 0, stream, a);
+  ES_REQUIRE(8LL * BH * a.per_xcd < (1LL << 30), ES_ERR_UNSUPPORTED, "VSA: grid too large");
+  Queues qs;
+  ES_REQUIRE(balanced_launch(BH, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "VSA: row-block queues unavailable");
+  a.queues = qs.counters;
+  a.fixed = qs.fixed;
+  hipLaunchKernelGGL(vsa_bwd_q_kernel<false>, dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
   return check_launch("vsa_attn_bwd_q");
 }
 

@@ -22,6 +22,7 @@
 #include "../../include/vsa_hip.h"
 #include "common.h"
 #include "elem.h"
+#include "queues.h"
 
 namespace es {
 
@@ -44,7 +45,8 @@ struct RepArgs {
   const float* add_dq;
   int add_nb;
   float* dq_acc;
-  int L, NB, RM, W, BH, per_xcd, phases, mid_rows, tail_rows;
+  int* queues;  // the eight row-block queue counters of this launch (queues.h)
+  int L, NB, RM, W, BH, per_xcd, fixed, phases, mid_rows, tail_rows;
   float scale_log2, scale;
 };
 
@@ -111,10 +113,8 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
   __shared__ unsigned short blist[REP_MAX_NB], clist[REP_MAX_NB];
   __shared__ int counts[2];
 
-  const int w = blockIdx.x, xcd = w & 7, sidx = w >> 3;
-  const int bh = sidx / a.per_xcd;
-  const int qb = xcd * a.per_xcd + sidx % a.per_xcd;
-  if (bh >= a.BH || qb >= a.NB) return;
+  int bh, qb;  // XCD-aware, run-time balanced order of (query block, head) (queues.h)
+  if (!balanced_item(a.queues, a.fixed, a.per_xcd, a.BH, a.NB, bh, qb)) return;
   const int tid = threadIdx.x, l = tid & 63, hi = l >> 5, lq = l & 31;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int rg = wv & 1, kh = wv >> 1;
@@ -694,7 +694,11 @@ extern "C" int ES_VSA_API(vsa_rep_attn_fwd)(const void* q, const void* k, const 
                        blk_cnt, BH, L, D, RM, phases);
   a.out = (e16_t*)out;
   a.lse_out = lse;
-  hipLaunchKernelGGL(rep_q_kernel<false>, dim3(8 * BH * a.per_xcd), dim3(256), 0, stream, a);
+  Queues qs;
+  ES_REQUIRE(balanced_launch(BH, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "VSA2-rep: row-block queues unavailable");
+  a.queues = qs.counters;
+  a.fixed = qs.fixed;
+  hipLaunchKernelGGL(rep_q_kernel<false>, dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
   return check_launch("vsa_rep_attn_fwd");
 }
 
@@ -718,7 +722,11 @@ extern "C" int ES_VSA_API(vsa_rep_attn_bwd_q)(const void* q, const void* k, cons
   a.add_nb = add_nb;
   a.dq_acc = (float*)dq_acc;
   a.out = (e16_t*)dq;
-  hipLaunchKernelGGL(rep_q_kernel<true>, dim3(8 * BH * a.per_xcd), dim3(256), 0, stream, a);
+  Queues qs;
+  ES_REQUIRE(balanced_launch(BH, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "VSA2-rep: row-block queues unavailable");
+  a.queues = qs.counters;
+  a.fixed = qs.fixed;
+  hipLaunchKernelGGL(rep_q_kernel<true>, dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
   return check_launch("vsa_rep_attn_bwd_q");
 }
 
