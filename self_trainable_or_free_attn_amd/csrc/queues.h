@@ -68,6 +68,29 @@ __device__ __forceinline__ bool balanced_item(int* queues, int fixed, int per_xc
   return hd < heads && rb < n_rows;
 }
 
+// Head-major variant for kernels whose workgroups each stream a whole head's rows (the three-tier table
+// gradients): queue x holds every row group of heads x, x + 8, ..., so that one XCD's L2 serves all workgroups of
+// a head. Same claiming as above; `groups` row groups per head.
+__device__ __forceinline__ bool balanced_head_item(int* queues, int fixed, int groups, int heads, int& hd, int& grp) {
+  const int w = blockIdx.x, per_queue = (heads + 7) / 8 * groups;
+  int x = w & 7, k = w >> 3;
+  if (k >= fixed) {
+    __shared__ int item_s;
+    if (threadIdx.x < 64) {
+      const int it = claim_item(queues, x, fixed, per_queue);
+      if (threadIdx.x == 0) item_s = it;
+    }
+    __syncthreads();
+    const int it = __builtin_amdgcn_readfirstlane(item_s);
+    if (it < 0) return false;
+    x = it / per_queue;
+    k = it - x * per_queue;
+  }
+  hd = x + 8 * (k / groups);
+  grp = k % groups;
+  return hd < heads;
+}
+
 static __device__ int es_tile_queues[64 * 8];
 
 static __global__ __launch_bounds__(64) void zero_queues_kernel(int* q) {
@@ -80,9 +103,9 @@ struct Queues {
   long long grid = 0;
 };
 
-// Sets up one balanced launch of heads x n_rows items (n_rows split into eight runs of per_xcd): takes a counter
-// slot, clears it on `stream` and gives the grid size. false if the device's counter ring is unavailable.
-static bool balanced_launch(int heads, int per_xcd, hipStream_t stream, Queues& out) {
+// Sets up one balanced launch of eight queues of per_queue items each: takes a counter slot, clears it on `stream`
+// and gives the grid size. false if the device's counter ring is unavailable.
+static bool balanced_launch_queues(int per_queue, hipStream_t stream, Queues& out) {
   static std::atomic<int*> base[64];
   static std::atomic<unsigned> seq{0};
   int dev = 0;
@@ -93,11 +116,16 @@ static bool balanced_launch(int heads, int per_xcd, hipStream_t stream, Queues& 
     base[dev].store(p);
   }
   out.counters = p + (seq.fetch_add(1) % 64) * 8;
-  const int per_queue = heads * per_xcd, claimable = (per_queue + 7) / 8;
+  const int claimable = (per_queue + 7) / 8;
   out.fixed = per_queue - claimable;
   out.grid = 8LL * (out.fixed + 2LL * claimable);
   hipLaunchKernelGGL(zero_queues_kernel, dim3(1), dim3(64), 0, stream, out.counters);
   return true;
+}
+
+// heads x n_rows items, n_rows split into eight runs of per_xcd (balanced_item)
+static bool balanced_launch(int heads, int per_xcd, hipStream_t stream, Queues& out) {
+  return balanced_launch_queues(heads * per_xcd, stream, out);
 }
 
 }  // namespace es

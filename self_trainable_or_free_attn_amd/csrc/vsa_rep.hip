@@ -340,7 +340,8 @@ struct TabArgs {
   const float *lse, *delta;
   const unsigned *bits_a, *bits_ab;
   float *dk_tab, *dv_tab;       // [BH, rows_pad, D] fp32, accumulated
-  int L, NB, RM, W, rows, rows_pad, tier;  // tier: PH_B or PH_C
+  int* queues;                  // the eight row-group queue counters of this launch (queues.h)
+  int L, NB, RM, W, rows, rows_pad, tier, BH, fixed;  // tier: PH_B or PH_C
   float scale_log2, scale;
 };
 
@@ -360,14 +361,15 @@ __device__ __forceinline__ unsigned long long tier_mask(const TabArgs& a, size_t
   return nblk >= 64 ? m : (m & ((1ull << nblk) - 1ull));
 }
 
-// grid (rows_pad / 64, BH), 256 threads; the fine KV-owner layout (2 key halves x 2 query halves). Two passes with
+// one workgroup per (64 table rows, head) in head-major balanced order (queues.h), 256 threads; the fine KV-owner layout (2 key halves x 2 query halves). Two passes with
 // one accumulator set each, so that two waves share a SIMD: PART 1 = dV (S, dV), PART 2 = dK (S, dP with the
 // table's V rows in registers, dK).
 template <int PART>
 __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
   __shared__ __attribute__((aligned(16))) char qd_s[2][2][BK * 256];
   __shared__ __attribute__((aligned(16))) float st_s[2][2][BK];
-  const int grp = blockIdx.x, bh = blockIdx.y;
+  int grp, bh;
+  if (!balanced_head_item(a.queues, a.fixed, a.rows_pad / BK, a.BH, bh, grp)) return;
   const int tid = threadIdx.x, l = tid & 63, hi = l >> 5, lq = l & 31;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kh = wv & 1, qh = wv >> 1;
@@ -759,8 +761,16 @@ extern "C" int ES_VSA_API(vsa_rep_bwd_tables)(const void* q, const void* dout, c
   a.rows_pad = (a.rows + 63) / 64 * 64;
   a.scale_log2 = LOG2E / sqrtf((float)D);
   a.scale = 1.0f / sqrtf((float)D);
-  hipLaunchKernelGGL(rep_bwd_tab_kernel<1>, dim3(a.rows_pad / 64, BH), dim3(256), 0, stream, a);
-  hipLaunchKernelGGL(rep_bwd_tab_kernel<2>, dim3(a.rows_pad / 64, BH), dim3(256), 0, stream, a);
+  a.BH = BH;
+  const int per_queue = (BH + 7) / 8 * (a.rows_pad / BK);
+  Queues qs;
+  ES_REQUIRE(balanced_launch_queues(per_queue, stream, qs), ES_ERR_LAUNCH, "VSA2-rep: row-group queues unavailable");
+  a.queues = qs.counters;
+  a.fixed = qs.fixed;
+  hipLaunchKernelGGL(rep_bwd_tab_kernel<1>, dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
+  ES_REQUIRE(balanced_launch_queues(per_queue, stream, qs), ES_ERR_LAUNCH, "VSA2-rep: row-group queues unavailable");
+  a.queues = qs.counters;
+  hipLaunchKernelGGL(rep_bwd_tab_kernel<2>, dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
   return check_launch("vsa_rep_bwd_tables");
 }
 
