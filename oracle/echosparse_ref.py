@@ -25,9 +25,10 @@ Pinning (what checks each function independently of this file; the tests live in
   pack_plan / rebuild_plan
                         round trip + known answers
   representatives       invariants of reference tests/test_sm120.py:65-83 (weighted sum of reps = block sum,
-                        counts sum to block length), Lloyd fixed point, -inf for empty clusters; the exact float
-                        values beyond these invariants are parity unpinned (the reference's own clustering uses
-                        TF32 dot products)
+                        counts sum to block length), Lloyd fixed point, -inf for empty clusters; the weighted
+                        Lloyd loop equals scikit-learn's Lloyd k-means on the same points, weights and starting
+                        partition, and the probe weights equal torch.softmax (the reference's own clustering
+                        uses TF32 dot products, so its float values are matched at tolerance, not bit for bit)
 """
 import math
 

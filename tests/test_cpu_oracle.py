@@ -378,3 +378,46 @@ def test_representatives_invariants_and_lloyd_fixed_point():
         dist = np.where(cw[None] > 0, dist, np.inf)
         assert np.array_equal(np.argmin(dist, 1)[valid], lab[valid])
         assert np.isneginf(lc[cnt == 0]).all() if (cnt == 0).any() else True
+
+
+def test_kmeans_block_equals_sklearn_weighted_lloyd():
+    """The weighted Lloyd loop of kmeans_block against scikit-learn's Lloyd k-means (KMeans(algorithm="lloyd"))
+    on the same metric-space points, token weights and starting partition (contiguous quarters of the block):
+    converged labels equal, and the representatives are the count-means of those clusters. Probe weights against
+    torch.softmax."""
+    import torch
+    from sklearn.cluster import KMeans
+    L, H, D = 4152, 1, 128
+    q, k, v = qkv(L, H, seed=8)
+    metric, probes = ref.metric_and_probes(q)
+    nb = ref.cdiv(L, 64)
+    rng = np.random.default_rng(3)
+    blocks = [(k[64 * j:64 * j + 64, 0], v[64 * j:64 * j + 64, 0]) for j in list(range(0, nb, 7)) + [nb - 1]]
+    # unstructured keys as well: there the clusters move far from the starting quarters
+    blocks += [(round_bf16(rng.standard_normal((64 - 5 * (i % 3), D)).astype(np.float32)),
+                round_bf16(rng.standard_normal((64 - 5 * (i % 3), D)).astype(np.float32))) for i in range(12)]
+    checked = moved = 0
+    for kb, vb in blocks:
+        n = kb.shape[0]
+        kk = np.zeros((64, D), np.float32)
+        vv = np.zeros((64, D), np.float32)
+        kk[:n], vv[:n] = kb, vb
+        ck, cv, lc, lab, X, w = ref.kmeans_block(kk, vv, n, metric[0], probes[0], iters=100)
+        sp = torch.as_tensor(probes[0], dtype=torch.float64) @ torch.as_tensor(kk[:n], dtype=torch.float64).T
+        w_t = torch.softmax(sp, dim=1).sum(0) * (n / 64)
+        assert np.allclose(w[:n], w_t.numpy(), rtol=1e-12, atol=0)
+        init_lab = np.arange(n) // 16
+        init = np.stack([(w[:n, None] * X[:n])[init_lab == c].sum(0) / w[:n][init_lab == c].sum() for c in range(4)])
+        km = KMeans(n_clusters=4, init=init, n_init=1, max_iter=100, tol=0.0, algorithm="lloyd")
+        km.fit(X[:n], sample_weight=w[:n])
+        if len(np.unique(km.labels_)) < 4:
+            continue  # scikit-learn relocates emptied clusters; kmeans_block retires them
+        assert np.array_equal(km.labels_, lab[:n])
+        moved += int((lab[:n] != init_lab).sum())
+        cnt = np.bincount(lab[:n], minlength=4)
+        for c in range(4):
+            assert lc[c] == np.log2(cnt[c])
+            want = ref.round_bf16((kk[:n][lab[:n] == c].astype(np.float64).mean(0)).astype(np.float32))
+            assert np.array_equal(ck[c], want)
+        checked += 1
+    assert checked >= 16 and moved >= 100
