@@ -463,13 +463,13 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
   }
 }
 
-// XCD-aware, run-time balanced tile order (queues.h); the ONLINE / COMPENSATE launches, which skip unflagged
-// tiles, bind every item to its dispatch slot
+// XCD-aware, run-time balanced tile order (queues.h); the fallback launches (ONLINE with flags, COMPENSATE), which
+// skip unflagged tiles, bind every item to its dispatch slot
 template <int MODE, bool COMP, bool MASS>
 __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   const int w = blockIdx.x, per_queue = a.H * a.per_xcd;
   int x = w & 7, k = w >> 3;
-  if (MODE == FIXED && k >= a.fixed) {
+  if (MODE != COMPENSATE && k >= a.fixed) {
     __shared__ int item_s;
     if (threadIdx.x < 64) {
       const int it = claim_item(a.queues, x, a.fixed, per_queue);
@@ -494,7 +494,7 @@ static int launch(const AttnArgs& a0, hipStream_t stream, const char* what) {
   long long grid = 8LL * a.H * a.per_xcd;
   if (grid <= 0) return ES_OK;
   a.fixed = a.H * a.per_xcd;
-  if (MODE == FIXED) {
+  if (MODE == FIXED || (MODE == ONLINE && a.flags == nullptr)) {
     Queues qs;
     ES_REQUIRE(balanced_launch(a.H, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "tile queues unavailable on this device");
     a.queues = qs.counters;
