@@ -375,3 +375,41 @@ def test_sparse_attention_stream_edges(data, plan, reps, dev):
             ex[hh, qt, blocks[qt, hh, :counts[qt, hh]]] = True
     check_close("edge mass", f32(mass)[ex], rm[ex], max_abs=2e-2 * max(1.0, float(np.abs(rm).max())))
     assert (f32(mass)[~ex] == 0).all()
+
+
+def test_sparse_attention_balanced_launches_concurrent_and_repeated(data, plan, reps, dev):
+    """The sparse step hands the last tiles of each XCD queue out at run time through a 64-slot ring of counters:
+    launches on three streams at once and 70 launches in a row (the ring wraps) give bytes-identical outputs,
+    which also pins that every tile runs exactly once whichever workgroup takes it."""
+    p = plan
+    R, km, vm = reps
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    keep, counts, blocks, refine, rc, means, mc = (t(x) for x in p["lists"])
+    offset = t(p["lse"])
+
+    def outputs():
+        return (torch.full_like(data["qd"], 7.0), torch.full((NQ * 128, H), 7.0, device=dev),
+                torch.full((NQ, H), 7, device=dev, dtype=torch.int32), torch.zeros(H, NQ, NB, device=dev))
+
+    def call(o):
+        K().sparse_attention(data["qd"], data["kd"], data["vd"], km, vm, means, mc, o[0], counts, blocks, offset,
+                             o[1], o[2], refine, rc, R.k, R.v, R.log_counts, mass=o[3])
+
+    want = outputs()
+    call(want)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(3)]
+    got = [outputs() for _ in streams]
+    torch.cuda.synchronize()
+    for s, o in zip(streams, got):
+        with torch.cuda.stream(s):
+            for _ in range(4):
+                call(o)
+    torch.cuda.synchronize()
+    seq = outputs()
+    for _ in range(70):
+        call(seq)
+    torch.cuda.synchronize()
+    for o in got + [seq]:
+        for a, b in zip(o, want):
+            assert torch.equal(a, b)
