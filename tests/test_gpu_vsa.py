@@ -434,3 +434,40 @@ def test_vsa2_attention_forward_backward(qkv):
 def test_vsa_attention_forward_backward(qkv):
     log("vsa_attention end to end")
     _operator_case(qkv, "vsa")
+
+
+def test_balanced_launches_concurrent_and_repeated(qkv):
+    """The fine forward, KV-owner backward and dQ kernels hand the last query / key blocks of each XCD queue out at
+    run time through a 64-slot counter ring: calls on two streams at once and 40 calls in a row (wrapping the ring)
+    give bytes-identical outputs."""
+    log("balanced launches")
+    q, k, v = qkv["gpu"]
+    m = random_mask(5)
+    sel = selection_of(m, q.device)
+    dout = tokens(31, q.device)[1]
+
+    def run():
+        o, lse = C().attn_fwd(q, k, v, sel.q2k_ptr, sel.q2k_idx, qkv["blk"])
+        _, delta, _, _, _ = C().fuse_bwd(dout, o, torch.zeros(B, H, 64, D, dtype=q.dtype, device=q.device), None,
+                                         qkv["blk"], 0, False)
+        dk, dv = C().attn_bwd(q, k, v, dout, lse, delta, sel.k2q_ptr, sel.k2q_idx, qkv["blk"])
+        dq = C().attn_bwd_q(q, k, v, dout, lse, delta, sel.q2k_ptr, sel.q2k_idx, qkv["blk"])
+        return o, lse, dk, dv, dq
+
+    want = run()
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(2)]
+    got = []
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    for s in streams:
+        with torch.cuda.stream(s):
+            got.append(run())
+    for s in streams:
+        torch.cuda.current_stream().wait_stream(s)
+    for _ in range(40):
+        last = run()
+    torch.cuda.synchronize()
+    for res in got + [last]:
+        for a, b in zip(res, want):
+            assert torch.equal(a, b)
