@@ -494,8 +494,8 @@ static int launch(const AttnArgs& a0, hipStream_t stream, const char* what) {
   long long grid = 8LL * a.H * a.per_xcd;
   if (grid <= 0) return ES_OK;
   a.fixed = a.H * a.per_xcd;
+  Queues qs;  // (released after the launch below is enqueued)
   if (MODE == FIXED || (MODE == ONLINE && a.flags == nullptr)) {
-    Queues qs;
     ES_REQUIRE(balanced_launch(a.H, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "tile queues unavailable on this device");
     a.queues = qs.counters;
     a.fixed = qs.fixed;

@@ -11,12 +11,17 @@
 // drains.
 //
 // The counters live in a ring of 64 slots of 8 counters in this translation unit's device memory (one copy per
-// GPU, no allocation), one slot per launch, cleared by a one-wave kernel on the launch's stream just before it:
-// launches that overlap on one GPU get distinct slots unless 64 or more of them are in flight.
+// GPU, no allocation), one slot per launch, cleared by a one-wave kernel on the launch's stream just before it.
+// A slot is reused only after its previous launch: every balanced launch records the slot's event on its stream
+// once it is enqueued (when its Queues object is released), and the next launch that takes the slot makes its own
+// stream wait for that event before clearing the counters, so launches in flight on any number of streams never
+// share counters. (Inside a stream capture there is no wait and no record: a captured graph replays its launches
+// in its own order, and replays of one graph must not overlap.)
 #pragma once
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <mutex>
 
 namespace es {
 
@@ -97,25 +102,76 @@ static __global__ __launch_bounds__(64) void zero_queues_kernel(int* q) {
   if (threadIdx.x < 8) q[threadIdx.x] = 0;
 }
 
+// The counter ring of one GPU: the slots' device memory, one event per slot marking the end of its last launch,
+// and one host lock per slot held from the slot's hand-out until that event is recorded.
+struct QueueRing {
+  int* base = nullptr;
+  hipEvent_t done[64] = {};
+  std::mutex held[64];
+  std::atomic<unsigned> seq{0};
+};
+
+static QueueRing* queue_ring() {
+  static std::atomic<QueueRing*> rings[64];
+  static std::mutex init;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  QueueRing* r = rings[dev].load();
+  if (r) return r;
+  std::lock_guard<std::mutex> g(init);
+  if ((r = rings[dev].load())) return r;
+  r = new QueueRing;
+  bool ok = hipGetSymbolAddress((void**)&r->base, HIP_SYMBOL(es_tile_queues)) == hipSuccess;
+  for (int i = 0; ok && i < 64; ++i) ok = hipEventCreateWithFlags(&r->done[i], hipEventDisableTiming) == hipSuccess;
+  if (!ok) return nullptr;  // (leaks the partial ring; the device is unusable for balanced launches anyway)
+  rings[dev].store(r);
+  return r;
+}
+
+// One balanced launch's counter slot. Declare it before the launch and keep it alive until the kernel is enqueued:
+// releasing it (destructor, or the next balanced_launch_queues on the same object) records the slot's event on the
+// launch's stream.
 struct Queues {
   int* counters = nullptr;
   int fixed = 0;
   long long grid = 0;
+  QueueRing* ring = nullptr;
+  int slot = -1;
+  bool captured = false;
+  hipStream_t stream = nullptr;
+
+  Queues() = default;
+  Queues(const Queues&) = delete;
+  Queues& operator=(const Queues&) = delete;
+  ~Queues() { release(); }
+  void release() {
+    if (slot < 0) return;
+    if (!captured) (void)hipEventRecord(ring->done[slot], stream);
+    ring->held[slot].unlock();
+    slot = -1;
+  }
 };
 
-// Sets up one balanced launch of eight queues of per_queue items each: takes a counter slot, clears it on `stream`
-// and gives the grid size. false if the device's counter ring is unavailable.
+// Sets up one balanced launch of eight queues of per_queue items each: takes a counter slot, orders the stream
+// after the slot's previous launch, clears the slot on `stream` and gives the grid size. false if the device's
+// counter ring is unavailable.
 static bool balanced_launch_queues(int per_queue, hipStream_t stream, Queues& out) {
-  static std::atomic<int*> base[64];
-  static std::atomic<unsigned> seq{0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-  int* p = base[dev].load();
-  if (p == nullptr) {
-    if (hipGetSymbolAddress((void**)&p, HIP_SYMBOL(es_tile_queues)) != hipSuccess) return false;
-    base[dev].store(p);
+  out.release();
+  QueueRing* r = queue_ring();
+  if (r == nullptr) return false;
+  const int slot = (int)(r->seq.fetch_add(1) % 64);
+  r->held[slot].lock();
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  const bool captured = hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+  if (!captured && hipStreamWaitEvent(stream, r->done[slot], 0) != hipSuccess) {
+    r->held[slot].unlock();
+    return false;
   }
-  out.counters = p + (seq.fetch_add(1) % 64) * 8;
+  out.ring = r;
+  out.slot = slot;
+  out.captured = captured;
+  out.stream = stream;
+  out.counters = r->base + slot * 8;
   const int claimable = (per_queue + 7) / 8;
   out.fixed = per_queue - claimable;
   out.grid = 8LL * (out.fixed + 2LL * claimable);

@@ -413,3 +413,46 @@ def test_sparse_attention_balanced_launches_concurrent_and_repeated(data, plan, 
     for o in got + [seq]:
         for a, b in zip(o, want):
             assert torch.equal(a, b)
+
+
+def test_balanced_ring_waits_for_a_live_slot(data, plan, reps, dev):
+    """A long balanced launch (dense attention, L = 32768, H = 8) on one stream while 70 short sparse launches run
+    on another: the short ones wrap the 64-slot counter ring and reach the slot the long launch still uses; the
+    launch that takes it must wait for the long one instead of clearing its counters, so every output is
+    bytes-identical to the same launches run one after another."""
+    p = plan
+    R, km, vm = reps
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    keep, counts, blocks, refine, rc, means, mc = (t(x) for x in p["lists"])
+    offset = t(p["lse"])
+    g = torch.Generator(device=dev).manual_seed(11)
+    Lb, Hb = 32768, 8
+    qb, kb, vb = (torch.randn(Lb, Hb, D, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+
+    def short(o):
+        K().sparse_attention(data["qd"], data["kd"], data["vd"], km, vm, means, mc, o[0], counts, blocks, offset,
+                             o[1], o[2], refine, rc, R.k, R.v, R.log_counts, mass=o[3])
+
+    def outputs():
+        return (torch.full_like(data["qd"], 7.0), torch.full((NQ * 128, H), 7.0, device=dev),
+                torch.full((NQ, H), 7, device=dev, dtype=torch.int32), torch.zeros(H, NQ, NB, device=dev))
+
+    log("ring: serial reference launches")
+    want_long = K().dense_attention(qb, kb, vb)
+    want = outputs()
+    short(want)
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    got = [outputs() for _ in range(70)]
+    torch.cuda.synchronize()
+    log("ring: long launch on stream A, 70 short launches on stream B")
+    with torch.cuda.stream(sa):
+        got_long = K().dense_attention(qb, kb, vb)
+    with torch.cuda.stream(sb):
+        for o in got:
+            short(o)
+    torch.cuda.synchronize()
+    assert torch.equal(got_long[0], want_long[0]) and torch.equal(got_long[1], want_long[1])
+    for o in got:
+        for a, b in zip(o, want):
+            assert torch.equal(a, b)
