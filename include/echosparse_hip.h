@@ -136,6 +136,17 @@ int es_representatives(const void* q, const void* k, const void* v, void* k_rep,
                        void* k_mean, void* v_mean, void* workspace, size_t workspace_bytes, int iters, int L,
                        int H, int D, hipStream_t stream);
 
+/* es_representatives without a workspace argument, for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. Same kernels and
+ * results as es_representatives; the workspace is a 48 MiB device array inside the library (one per GPU, held
+ * until the process ends), so it calls no allocator. Rejects (ES_ERR_UNSUPPORTED) any (L, H) whose
+ * es_representatives_workspace exceeds es_representatives_noalloc_limit() bytes (Wan2.1-14B, L = 75 600 and
+ * H = 40, needs 44 MB). Calls that overlap on one GPU share the array and race: serialise them. */
+size_t es_representatives_noalloc_limit(void);
+int es_representatives_noalloc(const void* q, const void* k, const void* v, void* k_rep, void* v_rep,
+                               float* log_counts, void* k_mean, void* v_mean, int iters, int L, int H, int D,
+                               hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -32,6 +32,7 @@ SIGNATURES = {
     "es_pack_plan": [P, P, I, I, I, I],
     "es_rebuild_plan": [P, P, I, P, P, P, P, P, I, P, P, I, I, I],
     "es_representatives": [P, P, P, P, P, P, P, P, P, Z, I, I, I, I],
+    "es_representatives_noalloc": [P, P, P, P, P, P, P, P, I, I, I, I],
     # include/vsa_hip.h
     "vsa_pool": [P, P, P, P, P, P, P, P, P, P, I, I, I, I],
     "vsa_fuse_fwd": [P, P, P, P, P, I, I, I, I, I, I],
@@ -68,7 +69,7 @@ F16_TWINS = ("vsa_pool", "vsa_fuse_fwd", "vsa_fuse_bwd", "vsa_finalize", "vsa_at
              "vsa_split_merge_sum", "vsa_rep_build", "vsa_rep_attn_fwd", "vsa_rep_attn_bwd_q", "vsa_rep_bwd_tables",
              "vsa_rep_unpool", "vsa_row_dot")
 SIGNATURES.update({n + "_f16": SIGNATURES[n] for n in F16_TWINS})
-NO_STREAM = {"es_representatives_workspace": ([I, I, I], Z), "es_last_error_string": ([], ctypes.c_char_p),
+NO_STREAM = {"es_representatives_workspace": ([I, I, I], Z), "es_representatives_noalloc_limit": ([], Z), "es_last_error_string": ([], ctypes.c_char_p),
              "es_abi_version": ([], I), "vsa_topk_workspace": ([I, I], Z)}
 
 _lib = None

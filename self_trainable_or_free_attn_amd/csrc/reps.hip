@@ -12,6 +12,9 @@
 #include "../../include/echosparse_hip.h"
 #include "common.h"
 
+#include <atomic>
+#include <mutex>
+
 namespace es {
 
 constexpr int NPROBE = 64;
@@ -441,26 +444,10 @@ __global__ __launch_bounds__(256, 4) void kmeans_kernel(const bf16_t* __restrict
   }
 }
 
-}  // namespace es
-
-using namespace es;
-
-extern "C" size_t es_representatives_workspace(int L, int H, int D) {
-  if (L <= 0 || H <= 0 || D != HD) return 0;
-  return ws_bytes(L, H);
-}
-
-extern "C" int es_representatives(const void* q, const void* k, const void* v, void* k_rep, void* v_rep,
-                                  float* log_counts, void* k_mean, void* v_mean, void* workspace,
-                                  size_t workspace_bytes, int iters, int L, int H, int D, hipStream_t stream) {
-  ES_REQUIRE(q && k && v && k_rep && v_rep && log_counts && workspace, ES_ERR_INVALID, "null tensor pointer");
-  ES_REQUIRE(L > 0 && H > 0, ES_ERR_INVALID, "L and H must be positive");
-  ES_REQUIRE(D == HD, ES_ERR_UNSUPPORTED, "head dimension must be 128");
-  ES_REQUIRE((k_mean == nullptr) == (v_mean == nullptr), ES_ERR_INVALID, "pass both k_mean and v_mean or neither");
+static void run_representatives(const void* q, const void* k, const void* v, void* k_rep, void* v_rep,
+                                float* log_counts, void* k_mean, void* v_mean, const RepWorkspace& w, int iters,
+                                int L, int H, hipStream_t stream) {
   const int nb = (L + BK - 1) / BK;
-  ES_REQUIRE(nb >= NPROBE, ES_ERR_INVALID, "needs at least 64 kv blocks (4096 tokens)");
-  ES_REQUIRE(workspace_bytes >= ws_bytes(L, H), ES_ERR_INVALID, "workspace too small");
-  RepWorkspace w = carve(workspace, L, H);
   const float scale = 1.0f / sqrtf((float)HD);
   hipLaunchKernelGGL(gram_kernel, dim3(w.splits, H), dim3(256), 0, stream, (const bf16_t*)q, w.gram, L, H,
                      w.rows_per_split, w.splits);
@@ -477,5 +464,71 @@ extern "C" int es_representatives(const void* q, const void* k, const void* v, v
     hipLaunchKernelGGL(kmeans_kernel<false>, dim3(nb, H), dim3(256), 0, stream, (const bf16_t*)k,
                        (const bf16_t*)v, w.metric_t, w.probes, (bf16_t*)k_rep, (bf16_t*)v_rep, log_counts,
                        nullptr, nullptr, L, H, nb, iters);
+}
+
+static int check_representatives(const void* q, const void* k, const void* v, void* k_rep, void* v_rep,
+                                 float* log_counts, void* k_mean, void* v_mean, int L, int H, int D) {
+  ES_REQUIRE(q && k && v && k_rep && v_rep && log_counts, ES_ERR_INVALID, "null tensor pointer");
+  ES_REQUIRE(L > 0 && H > 0, ES_ERR_INVALID, "L and H must be positive");
+  ES_REQUIRE(D == HD, ES_ERR_UNSUPPORTED, "head dimension must be 128");
+  ES_REQUIRE((k_mean == nullptr) == (v_mean == nullptr), ES_ERR_INVALID, "pass both k_mean and v_mean or neither");
+  ES_REQUIRE((L + BK - 1) / BK >= NPROBE, ES_ERR_INVALID, "needs at least 64 kv blocks (4096 tokens)");
+  return ES_OK;
+}
+
+// The allocation-free variant's workspace: one file-scope array, of which each GPU holds its own copy at its own
+// address until the process ends. Host code never passes the array's name as a device address: the address is
+// looked up once per device (with that device current) by hipGetSymbolAddress and kept in noalloc_base. Nothing
+// in it has to start at zero (every kernel writes what it later reads), and calls that overlap on one GPU race on
+// it.
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(48) << 20;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+static void* noalloc_base() {
+  static std::atomic<void*> base[64];
+  static std::mutex init;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  void* p = base[dev].load();
+  if (p) return p;
+  std::lock_guard<std::mutex> g(init);
+  if ((p = base[dev].load())) return p;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+  base[dev].store(p);
+  return p;
+}
+
+}  // namespace es
+
+using namespace es;
+
+extern "C" size_t es_representatives_workspace(int L, int H, int D) {
+  if (L <= 0 || H <= 0 || D != HD) return 0;
+  return ws_bytes(L, H);
+}
+
+extern "C" int es_representatives(const void* q, const void* k, const void* v, void* k_rep, void* v_rep,
+                                  float* log_counts, void* k_mean, void* v_mean, void* workspace,
+                                  size_t workspace_bytes, int iters, int L, int H, int D, hipStream_t stream) {
+  if (int st = check_representatives(q, k, v, k_rep, v_rep, log_counts, k_mean, v_mean, L, H, D)) return st;
+  ES_REQUIRE(workspace, ES_ERR_INVALID, "null tensor pointer");
+  ES_REQUIRE(workspace_bytes >= ws_bytes(L, H), ES_ERR_INVALID, "workspace too small");
+  run_representatives(q, k, v, k_rep, v_rep, log_counts, k_mean, v_mean, carve(workspace, L, H), iters, L, H,
+                      stream);
   return check_launch("es_representatives");
+}
+
+extern "C" size_t es_representatives_noalloc_limit(void) { return NOALLOC_SCRATCH_BYTES; }
+
+extern "C" int es_representatives_noalloc(const void* q, const void* k, const void* v, void* k_rep, void* v_rep,
+                                          float* log_counts, void* k_mean, void* v_mean, int iters, int L, int H,
+                                          int D, hipStream_t stream) {
+  if (int st = check_representatives(q, k, v, k_rep, v_rep, log_counts, k_mean, v_mean, L, H, D)) return st;
+  ES_REQUIRE(ws_bytes(L, H) <= NOALLOC_SCRATCH_BYTES, ES_ERR_UNSUPPORTED,
+             "es_representatives_noalloc: these L and H need more than the 48 MiB device scratch "
+             "(es_representatives_workspace(L, H, D) bytes); use es_representatives with a caller workspace");
+  void* base = noalloc_base();
+  ES_REQUIRE(base, ES_ERR_LAUNCH, "es_representatives_noalloc: device scratch unavailable on this device");
+  run_representatives(q, k, v, k_rep, v_rep, log_counts, k_mean, v_mean, carve(base, L, H), iters, L, H, stream);
+  return check_launch("es_representatives_noalloc");
 }
