@@ -21,6 +21,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _C as _native
+from ._checks import nonnegative_reals, positive_ints
 from .dispatch import check_bwd_variant, select_bwd_variant
 
 GATE_ACTS = {"tanh": 0, "identity": 1}
@@ -159,20 +160,8 @@ class SplitPolicy:
     resident_ctas: Optional[int] = None
 
     def __post_init__(self):
-        for name in ("rel_mean", "tail_frac", "fwd_waves", "bwd_waves"):
-            v = getattr(self, name)
-            if isinstance(v, bool) or not isinstance(v, (int, float)):
-                raise TypeError(f"SplitPolicy.{name} must be a real number, got {type(v).__name__}")
-            if not math.isfinite(v) or v < 0:
-                raise ValueError(f"SplitPolicy.{name} must be finite and >= 0, got {v!r}")
-        for name in ("min_chunks", "max_task_waves", "resident_ctas"):
-            v = getattr(self, name)
-            if v is None and name == "resident_ctas":
-                continue
-            if isinstance(v, bool) or not isinstance(v, int):
-                raise TypeError(f"SplitPolicy.{name} must be an int, got {type(v).__name__}")
-            if v < 1:
-                raise ValueError(f"SplitPolicy.{name} must be >= 1, got {v!r}")
+        nonnegative_reals(self, "rel_mean", "tail_frac", "fwd_waves", "bwd_waves")
+        positive_ints(self, "min_chunks", "max_task_waves", "resident_ctas", optional=("resident_ctas",))
 
 
 @dataclass(frozen=True)
@@ -188,12 +177,14 @@ class SplitKV:
     policy: Optional[SplitPolicy] = None
 
     def __post_init__(self):
-        if not 1 <= int(self.chunk) <= 1 << 30:
-            raise ValueError(f"SplitKV.chunk must be in [1, 2**30], got {self.chunk}")
-        if int(self.max_scratch_bytes) < 0:
-            raise ValueError("SplitKV.max_scratch_bytes must be >= 0")
-        if self.policy is not None and not isinstance(self.policy, SplitPolicy):
-            raise TypeError("SplitKV.policy must be a SplitPolicy or None")
+        problems = [(not 1 <= int(self.chunk) <= 1 << 30, ValueError,
+                     f"SplitKV.chunk must be in [1, 2**30], got {self.chunk}"),
+                    (int(self.max_scratch_bytes) < 0, ValueError, "SplitKV.max_scratch_bytes must be >= 0"),
+                    (not isinstance(self.policy, (SplitPolicy, type(None))), TypeError,
+                     "SplitKV.policy must be a SplitPolicy or None")]
+        for bad, kind, msg in problems:
+            if bad:
+                raise kind(msg)
 
     @classmethod
     def auto(cls, chunk: int = 64, fwd: bool = True, bwd: bool = True, max_scratch_bytes: int = 64 << 20,
@@ -218,17 +209,20 @@ def split_resident(q, use_tk: bool, kind: str, policy: Optional[SplitPolicy] = N
 
 
 def split_plan_for(C, q, ptr, idx, split: SplitKV, use_tk: bool, kind: str, slot_bytes: Optional[int]):
-    """(tasks, merges, info, slots) of one direction: fwd (q2k), bwd_kv (k2q), bwd_q (q2k)."""
-    nnz, nb = idx.numel(), ptr.shape[-1] - 1
-    slots = split_slots(nnz, split.chunk, slot_bytes or 1, (1 << 62) if slot_bytes is None else split.max_scratch_bytes)
+    """(tasks, merges, info, slots) of one direction: fwd (q2k), bwd_kv (k2q), bwd_q (q2k). slot_bytes None: the
+    direction keeps no partials, so the slot count only bounds the task grid."""
+    chunks = -(-int(idx.numel()) // split.chunk)
+    cap = (1 << 62) if slot_bytes is None else int(split.max_scratch_bytes) // int(slot_bytes)
+    slots = max(0, min(cap, 2 * chunks))       # a plan needs at most nnz / chunk + (split rows) <= 2 * chunks
     pol = split.policy
-    if pol is None:
+    if pol is None:                            # manual: every list longer than one chunk
         return (*C.split_plan(ptr, split.chunk, slots), slots)
     resident = split_resident(q, use_tk, kind, pol)
-    budget = int((pol.fwd_waves if kind == "fwd" else pol.bwd_waves) * resident)
-    slots = min(slots, budget * (-(-nb // split.chunk)), pol.max_task_waves * resident)
-    return (*C.split_plan(ptr, split.chunk, slots, max(split.chunk + 1, pol.min_chunks * split.chunk), pol.rel_mean,
-                          pol.tail_frac, resident, budget), slots)
+    budget = int(resident * (pol.fwd_waves if kind == "fwd" else pol.bwd_waves))
+    per_row = -(-(ptr.shape[-1] - 1) // split.chunk)          # chunks of the longest possible list
+    slots = min(slots, budget * per_row, pol.max_task_waves * resident)
+    min_len = max(split.chunk + 1, pol.min_chunks * split.chunk)
+    return (*C.split_plan(ptr, split.chunk, slots, min_len, pol.rel_mean, pol.tail_frac, resident, budget), slots)
 
 
 def _as_split(split) -> Optional[SplitKV]:

@@ -20,6 +20,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _C as _native
+from ._checks import nonnegative_reals
 from .ops import GATE_ACTS, ROW_NORMS, _coarse_lists
 
 PHASE_A, PHASE_B, PHASE_C = 1, 2, 4
@@ -41,12 +42,7 @@ class RepTiers:
     mid_reps: int = 4
 
     def __post_init__(self):
-        for name in ("frac_full", "frac_mid"):
-            v = getattr(self, name)
-            if isinstance(v, bool) or not isinstance(v, (int, float)):
-                raise TypeError(f"RepTiers.{name} must be a real number, got {type(v).__name__}")
-            if not math.isfinite(v) or v < 0:
-                raise ValueError(f"RepTiers.{name} must be finite and >= 0, got {v!r}")
+        nonnegative_reals(self, "frac_full", "frac_mid")
         if self.frac_full + self.frac_mid > 1.0 + 1e-9:
             raise ValueError(f"frac_full + frac_mid must be <= 1, got {self.frac_full} + {self.frac_mid}")
         if self.mid_reps not in MID_REPS_OK:

@@ -112,13 +112,13 @@ def test_wan_hooks_reorder_and_route(monkeypatch):
     model = fd.WanTransformer3DModel(tw, depth=3)
     lat, enc = torch.randn(1, 4, 3, 12, 10), torch.randn(1, 9, 64)
     want = _dense_model_output(model, tw, lat, enc)
-    from self_trainable_or_free_attn_amd.models import wan
-    monkeypatch.setattr(wan, "dense_attention", lambda q, k, v: sdpa(q, k, v))
+    from self_trainable_or_free_attn_amd.models import common, wan
+    monkeypatch.setattr(common, "dense_attention", lambda q, k, v: sdpa(q, k, v))
     monkeypatch.setattr(tw, "dispatch_attention_fn", tw.dispatch_attention_fn)
     pipe = fd.Pipe(model)
     att = RecordingAttention()
-    wan.enable(pipe, att)
-    assert tw.dispatch_attention_fn is wan._dispatch
+    wan.install(pipe, att)
+    assert tw.dispatch_attention_fn.original is fd.default_dispatch
     pipe.scheduler.set_timesteps(2)
     with torch.no_grad():
         for step in range(2):
@@ -143,13 +143,12 @@ def test_hunyuan_hooks_crop_sink_and_text_rows(monkeypatch):
     vl = 2 * 8 * 9
     before = fd.default_dispatch.calls
     want = _dense_model_output(model, hv, lat, txt, tmask)
-    from self_trainable_or_free_attn_amd.models import hunyuan_video
-    monkeypatch.setattr(hunyuan_video, "dense_attention", lambda q, k, v: sdpa(q, k, v))
-    monkeypatch.setattr(hv, "dispatch_attention_fn", hv.dispatch_attention_fn)
-    monkeypatch.setattr(hunyuan_video, "_original_dispatch", fd.default_dispatch)
+    from self_trainable_or_free_attn_amd.models import common, hunyuan_video
+    monkeypatch.setattr(common, "dense_attention", lambda q, k, v: sdpa(q, k, v))
+    monkeypatch.setattr(hv, "dispatch_attention_fn", fd.default_dispatch)
     pipe = fd.Pipe(model)
     att = RecordingAttention()
-    hunyuan_video.enable(pipe, att)
+    hunyuan_video.install(pipe, att)
     pipe.scheduler.set_timesteps(1)
     with torch.no_grad():
         got = model(lat, txt, tmask)
@@ -157,7 +156,8 @@ def test_hunyuan_hooks_crop_sink_and_text_rows(monkeypatch):
     L = vl + 6
     torch.testing.assert_close(got[:, :L], want[:, :L], rtol=1e-5, atol=1e-5)
     assert fd.default_dispatch.calls - before == 3 + 1      # 3 dense-model calls, then the refiner call
-    assert [c["sink"] for c in att.calls] == [vl // 64] * 2 and [c["L"] for c in att.calls] == [L] * 2
+    # only the video rows enter the sparse kernels; the text rows are computed densely
+    assert [(c["sink"], c["rows"], c["L"]) for c in att.calls] == [(vl // 64, vl, L)] * 2
     assert [c["layer"] for c in att.calls] == [0, 1]
 
 
@@ -171,25 +171,24 @@ def test_minimax_hooks_packed_sequence(monkeypatch):
     L = prefix + grid[0] * grid[1] * grid[2]
     x = torch.randn(1, L, 64)
     want = _dense_model_output(model, th3, x, position_ids=pos, video_indices=vi)
-    from self_trainable_or_free_attn_amd.models import minimax_h3
-    monkeypatch.setattr(minimax_h3, "dense_attention", lambda q, k, v: sdpa(q, k, v))
-    monkeypatch.setattr(th3, "dispatch_attention_fn", th3.dispatch_attention_fn)
-    monkeypatch.setattr(minimax_h3, "_original_dispatch", fd.default_dispatch)
+    from self_trainable_or_free_attn_amd.models import common, minimax_h3
+    monkeypatch.setattr(common, "dense_attention", lambda q, k, v: sdpa(q, k, v))
+    monkeypatch.setattr(th3, "dispatch_attention_fn", fd.default_dispatch)
     pipe = fd.Pipe(model)
     att = RecordingAttention()
-    impl = minimax_h3.enable(pipe, att)
+    impl = minimax_h3.install(pipe, att)
     pipe.scheduler.set_timesteps(1)
     with torch.no_grad():
         got = model(x, position_ids=pos, video_indices=vi)
     torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
     nv = L - prefix
-    assert impl.layout.video_start == prefix and impl.layout.video == nv
+    assert impl.layout.start == prefix and impl.layout.n == nv
     assert [(c["sink"], c["rows"], c["L"]) for c in att.calls] == [(nv // 64, nv, L)] * 2
     # the video part of the packed order is the Morton order of the ranked rotary coordinates
     from self_trainable_or_free_attn_amd.models.common import grid_morton_order
     perm, _ = grid_morton_order(*grid, torch.device("cpu"))
-    assert torch.equal(impl.layout.packed_to_original[:nv], perm + prefix)
-    assert torch.equal(impl.layout.packed_to_original[nv:], torch.arange(prefix))
+    assert torch.equal(impl.layout.gather[:nv], perm + prefix)
+    assert torch.equal(impl.layout.gather[nv:], torch.arange(prefix))
 
 
 def test_morton_known_answer():
@@ -206,17 +205,17 @@ def test_h3_layout_strided_time_axis():
     order of the ranked coordinates, then the prefix in its own order."""
     fd.install()
     from self_trainable_or_free_attn_amd.models.common import morton_order
-    from self_trainable_or_free_attn_amd.models.minimax_h3 import _Layout
+    from self_trainable_or_free_attn_amd.models.minimax_h3 import packed_layout
     t, y, x = torch.meshgrid(torch.arange(0, 4, 2), torch.arange(3), torch.arange(4), indexing="ij")
     video = torch.stack([t.flatten(), y.flatten(), x.flatten()], 1)
     pos = torch.cat([torch.zeros(9, 3, dtype=torch.long), video])
     L, vs = pos.shape[0], 9
-    layout = _Layout(pos, torch.cat([torch.arange(3, 7), torch.arange(vs, L)]))
+    layout = packed_layout(pos, torch.cat([torch.arange(3, 7), torch.arange(vs, L)]))
     perm, _ = morton_order(video[:, 0] // 2, video[:, 1], video[:, 2])
-    assert layout.video == L - vs and layout.video_start == vs
-    assert torch.equal(layout.packed_to_original[:L - vs], perm + vs)
-    assert torch.equal(layout.packed_to_original[L - vs:], torch.arange(vs))
-    assert torch.equal(layout.packed_to_original[layout.original_to_packed], torch.arange(L))
+    assert layout.n == L - vs and layout.start == vs
+    assert torch.equal(layout.gather[:L - vs], perm + vs)
+    assert torch.equal(layout.gather[L - vs:], torch.arange(vs))
+    assert torch.equal(torch.sort(layout.gather).values, torch.arange(L))
 
 
 def test_enable_and_attention_agree(monkeypatch):
@@ -228,7 +227,8 @@ def test_enable_and_attention_agree(monkeypatch):
     from self_trainable_or_free_attn_amd import models
     seen = {}
     fake = types.ModuleType("self_trainable_or_free_attn_amd.models.minimax_h3")
-    fake.enable = lambda pipe, attention: seen.update(attention=attention)
+    fake.TRANSFORMER_PREFIX = "MiniMaxH3"
+    fake.install = lambda pipe, attention: seen.update(attention=attention)
     monkeypatch.setitem(sys.modules, fake.__name__, fake)
     monkeypatch.setattr(models, "minimax_h3", fake, raising=False)
     pipe = types.SimpleNamespace(transformer=type("MiniMaxH3Transformer", (), {})())
@@ -259,3 +259,65 @@ def test_device_change_releases_old_history(monkeypatch):
     attn(q, q, q, step=0, branch=0, layer=0)
     assert not attn._states
     assert attn._buffers is None and attn._plan_scratch is None
+
+
+def test_target_video_start_is_the_last_consecutive_run():
+    """The split of H3's video_indices against a brute-force walk back from the end, on random ascending index
+    lists made of several runs."""
+    fd.install()
+    from self_trainable_or_free_attn_amd.models.minimax_h3 import target_video_start
+    g = np.random.default_rng(7)
+    for _ in range(200):
+        runs, pos, idx = g.integers(1, 5), 0, []
+        for _r in range(runs):
+            pos += int(g.integers(1, 6))
+            n = int(g.integers(1, 9))
+            idx.extend(range(pos, pos + n))
+            pos += n
+        i = len(idx) - 1
+        while i > 0 and idx[i - 1] == idx[i] - 1:
+            i -= 1
+        assert target_video_start(torch.tensor(idx)) == i
+
+
+def test_sink_layout_rows_and_padding():
+    """A joint sequence with a prefix, a video span, a suffix and padding: video rows come from the sparse call in
+    the original order, other valid rows from dense attention over every valid key, padding rows are zero, and the
+    sparse call sees the video first with sink = n // 64 and rows = n."""
+    from self_trainable_or_free_attn_amd.models import common
+    torch.manual_seed(3)
+    start, n, valid, total = 5, 150, 170, 180
+    perm = torch.randperm(n)
+    lay = common.SinkLayout(start, perm, valid)
+    q, k, v = (torch.randn(1, total, 2, 16) for _ in range(3))
+    seen = {}
+
+    def attention(qp, kp, vp, step, branch, layer, sink=None, rows=None):
+        seen.update(sink=sink, rows=rows, q=qp)
+        return sdpa(qp, kp, vp)
+
+    clock = type("C", (), dict(step=0, branch=0, layer=4))()
+    dense = common.dense_attention
+    common.dense_attention = lambda a, b, c: sdpa(a, b, c)
+    try:
+        out = lay(attention, clock, q, k, v)
+    finally:
+        common.dense_attention = dense
+    assert (seen["sink"], seen["rows"], clock.layer) == (n // 64, n, 5)
+    assert torch.equal(seen["q"][:, :n], q[:, start + perm])
+    want = sdpa(q[:, :valid], k[:, :valid], v[:, :valid])
+    torch.testing.assert_close(out[:, :valid], want, rtol=1e-5, atol=1e-5)
+    assert (out[:, valid:] == 0).all()
+    with pytest.raises(ValueError, match="outside"):
+        common.SinkLayout(30, perm, valid)
+
+
+def test_model_family_accepts_subclasses():
+    from self_trainable_or_free_attn_amd import models
+    mods = fd.install()
+
+    class MyWan(fd.WanTransformer3DModel):
+        pass
+
+    assert models.model_family(fd.Pipe(MyWan(mods["transformer_wan"]))) == "wan"
+    assert models.family_presets("minimax_h3") == ["minimax_h3", "minimax_h3_rtx5090"]
