@@ -179,11 +179,29 @@ int vsa_split_merge_sum(const float* part, const int* merges, const int* info, i
 int vsa_rep_build(const void* k, const void* v, const int* blk_cnt, void* k_mid, void* v_mid, float* lc_mid,
                   void* k_tail, void* v_tail, float* lc_tail, int BH, int L, int D, int RM, hipStream_t stream);
 
+/* Seeded k-means tier-B tables (no reference counterpart, whose tables are contiguous means):
+ * every block's valid keys clustered into RM groups by `iters` Lloyd rounds from seed tokens drawn with `seed`;
+ * k_mid / v_mid rows (blk * RM + c, as vsa_rep_build) = the clusters' key / value means (zero when empty),
+ * lc_mid / counts [BH, NB * RM] per head = log2 cluster sizes (-inf when empty) / sizes, labels [BH, L] uint8 =
+ * each valid token's cluster (255 on padding). Float32 in a fixed order, no fused multiply-add (bit-exact against
+ * oracle/vsa_ref.py kmeans_tables). The tail tables come from vsa_rep_build. */
+int vsa_rep_build_kmeans(const void* k, const void* v, const int* blk_cnt, void* k_mid, void* v_mid, float* lc_mid,
+                         int* counts, uint8_t* labels, int BH, int L, int D, int RM, int iters, unsigned seed,
+                         hipStream_t stream);
+
+/* Per-query-block tiers (BASELINE config 4's split; the reference splits by global budgets, rep_api.cpp
+ * route_tiers): for every row i of the fp32 scores [bh_count, NB, NB] of (b, h) rows bh0.., the ka (tier A) and
+ * kab (tiers A and B) best blocks, score desc, ties to the smaller index, -0 == +0, as ascending CSR lists with
+ * offsets (bh * NB + i) * K and as selection bitmaps [BH, NB, ceil(NB / 32)]. 0 <= ka <= kab <= NB <= 2048. */
+int vsa_row_tiers(const float* scores, int NB, int bh0, int bh_count, int ka, int kab, int* a_ptr, int* a_idx,
+                  int* ab_ptr, int* ab_idx, unsigned* bits_a, unsigned* bits_ab, hipStream_t stream);
+
 /* Three-tier forward: one softmax over the tier-A tokens (q2k CSR), the tier-B representatives (bits_ab & ~bits_a)
  * and the tier-C means (~bits_ab), each representative column with + log2(count); O bf16, lse natural. phases:
- * 1 | 2 | 4 selects the tiers. NB <= 2048. Replaces rep_api.cpp rep_attn_fwd (rep_attn_fwd.cu:37). */
+ * 1 | 2 | 4 selects the tiers. lc_mid_stride: 0 when lc_mid is one [NB * RM] table for every head, NB * RM when
+ * it is per head (k-means tables). NB <= 2048. Replaces rep_api.cpp rep_attn_fwd (rep_attn_fwd.cu:37). */
 int vsa_rep_attn_fwd(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
-                     const float* lc_mid, const void* k_tail, const void* v_tail, const float* lc_tail,
+                     const float* lc_mid, int lc_mid_stride, const void* k_tail, const void* v_tail, const float* lc_tail,
                      const int* q2k_ptr, const int* q2k_idx, const unsigned* bits_a, const unsigned* bits_ab,
                      const int* blk_cnt, void* out, float* lse, int BH, int L, int D, int RM, int phases,
                      hipStream_t stream);
@@ -191,7 +209,7 @@ int vsa_rep_attn_fwd(const void* q, const void* k, const void* v, const void* k_
 /* dQ of the three-tier attention (deterministic, no atomics), + dq_acc (fp32, optional) + add_dq / blk_cnt
  * (optional); padding rows 0. Replaces the dQ part of rep_api.cpp rep_attn_bwd_q (rep_attn_bwd.cu:141). */
 int vsa_rep_attn_bwd_q(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
-                       const float* lc_mid, const void* k_tail, const void* v_tail, const float* lc_tail,
+                       const float* lc_mid, int lc_mid_stride, const void* k_tail, const void* v_tail, const float* lc_tail,
                        const void* dout, const float* lse, const float* delta, const int* q2k_ptr,
                        const int* q2k_idx, const unsigned* bits_a, const unsigned* bits_ab, const int* blk_cnt,
                        const float* add_dq, int add_nb, const float* dq_acc, void* dq, int BH, int L, int D, int RM,
@@ -201,13 +219,15 @@ int vsa_rep_attn_bwd_q(const void* q, const void* k, const void* v, const void* 
  * accumulated into dk_tab / dv_tab (fp32, the table's row layout) by a KV-owner pass: no atomics, deterministic.
  * Replaces the representative dK / dV atomics of rep_api.cpp rep_attn_bwd_q (rep_attn_bwd.cu:141). */
 int vsa_rep_bwd_tables(const void* q, const void* dout, const void* k_tab, const void* v_tab, const float* lc,
-                       const float* lse, const float* delta, const unsigned* bits_a, const unsigned* bits_ab,
+                       int lc_stride, const float* lse, const float* delta, const unsigned* bits_a, const unsigned* bits_ab,
                        float* dk_tab, float* dv_tab, int BH, int L, int D, int RM, int tier, hipStream_t stream);
 
 /* dK, dV (bf16) = acc (fp32 tier-A token gradients, optional) + dk_mid[group] / c_group + dk_tail[blk] / c_blk on
- * valid rows, 0 on padding. Replaces rep_api.cpp rep_unpool (rep_pool.cu:59-88). */
+ * valid rows, 0 on padding; group = the token's contiguous group, or with labels / mid_counts (k-means tables,
+ * both or neither) its cluster and that cluster's size. Replaces rep_api.cpp rep_unpool (rep_pool.cu:59-88). */
 int vsa_rep_unpool(const float* acc_k, const float* acc_v, const float* dk_mid, const float* dv_mid,
-                   const float* dk_tail, const float* dv_tail, const int* blk_cnt, void* dk, void* dv, int BH, int L,
+                   const float* dk_tail, const float* dv_tail, const int* blk_cnt, const uint8_t* labels,
+                   const int* mid_counts, void* dk, void* dv, int BH, int L,
                    int D, int RM, hipStream_t stream);
 
 /* out [BH, L] = rowsum(x * y) on valid rows, 0 on padding. Replaces rep_api.cpp row_dot (rep_pool.cu:90-112). */
@@ -224,7 +244,7 @@ int vsa_tier_b_lists(const int* ab_ptr, const int* ab_idx, const int* a_ptr, con
  * tier tables, gradients) has an fp16 twin with the suffix _f16 and the same arguments: the same kernels built for
  * fp16 storage and v_mfma_f32_32x32x16_f16 (fp32 accumulation), as the reference dispatches its kernels on the
  * tensor dtype (csrc/vsa/vsa2_api.cpp:51). Entry points without token tensors (vsa_topk_workspace,
- * vsa_global_topk, vsa_csr_transpose, vsa_split_plan, vsa_tier_b_lists) serve both. */
+ * vsa_global_topk, vsa_csr_transpose, vsa_split_plan, vsa_tier_b_lists, vsa_row_tiers) serve both. */
 int vsa_pool_f16(const void* q, const void* k, const void* v, const int* blk_cnt, void* qr, void* kr, void* vr,
                  void* qc, void* kc, void* vc, int BH, int L, int D, int R, hipStream_t stream);
 int vsa_fuse_fwd_f16(const void* of, const void* oc, const void* gate, void* o, const int* blk_cnt, int BH, int L,
@@ -276,21 +296,25 @@ int vsa_split_merge_sum_f16(const float* part, const int* merges, const int* inf
 int vsa_rep_build_f16(const void* k, const void* v, const int* blk_cnt, void* k_mid, void* v_mid, float* lc_mid,
                       void* k_tail, void* v_tail, float* lc_tail, int BH, int L, int D, int RM, hipStream_t stream);
 int vsa_rep_attn_fwd_f16(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
-                         const float* lc_mid, const void* k_tail, const void* v_tail, const float* lc_tail,
+                         const float* lc_mid, int lc_mid_stride, const void* k_tail, const void* v_tail, const float* lc_tail,
                          const int* q2k_ptr, const int* q2k_idx, const unsigned* bits_a, const unsigned* bits_ab,
                          const int* blk_cnt, void* out, float* lse, int BH, int L, int D, int RM, int phases,
                          hipStream_t stream);
 int vsa_rep_attn_bwd_q_f16(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
-                           const float* lc_mid, const void* k_tail, const void* v_tail, const float* lc_tail,
+                           const float* lc_mid, int lc_mid_stride, const void* k_tail, const void* v_tail, const float* lc_tail,
                            const void* dout, const float* lse, const float* delta, const int* q2k_ptr,
                            const int* q2k_idx, const unsigned* bits_a, const unsigned* bits_ab, const int* blk_cnt,
                            const float* add_dq, int add_nb, const float* dq_acc, void* dq, int BH, int L, int D, int RM,
                            int phases, hipStream_t stream);
 int vsa_rep_bwd_tables_f16(const void* q, const void* dout, const void* k_tab, const void* v_tab, const float* lc,
-                           const float* lse, const float* delta, const unsigned* bits_a, const unsigned* bits_ab,
+                           int lc_stride, const float* lse, const float* delta, const unsigned* bits_a, const unsigned* bits_ab,
                            float* dk_tab, float* dv_tab, int BH, int L, int D, int RM, int tier, hipStream_t stream);
+int vsa_rep_build_kmeans_f16(const void* k, const void* v, const int* blk_cnt, void* k_mid, void* v_mid,
+                             float* lc_mid, int* counts, uint8_t* labels, int BH, int L, int D, int RM, int iters,
+                             unsigned seed, hipStream_t stream);
 int vsa_rep_unpool_f16(const float* acc_k, const float* acc_v, const float* dk_mid, const float* dv_mid,
-                       const float* dk_tail, const float* dv_tail, const int* blk_cnt, void* dk, void* dv, int BH, int L,
+                       const float* dk_tail, const float* dv_tail, const int* blk_cnt, const uint8_t* labels,
+                       const int* mid_counts, void* dk, void* dv, int BH, int L,
                        int D, int RM, hipStream_t stream);
 int vsa_row_dot_f16(const void* x, const void* y, const int* blk_cnt, float* out, int BH, int L, int D,
                     hipStream_t stream);

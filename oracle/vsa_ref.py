@@ -26,6 +26,11 @@ Functions and what pins each one (tests/test_cpu_vsa_oracle.py):
   plan_reference           the split planner's contract (reference tests/test_vsa2_split.py:60-87), pinned by hand
                            cases and by every edge being covered exactly once
   merge_fwd                LSE merge of normalized partials equals the unsplit softmax (closed form)
+  kmeans_seed_tokens       distinct in-range tokens, deterministic per (seed, bh, blk), varying with the seed
+  kmeans_tables            counts partition the valid tokens, rows are the float64 means of their members, empty
+                           clusters retire; centroids equal scikit-learn's Lloyd k-means started from the same seed
+                           tokens for the same number of rounds
+  row_tiers                exact per-row counts, A inside A|B, brute-force order with ties and -0 / +0
 """
 import math
 
@@ -304,23 +309,33 @@ def rep_tables(k, v, blk_cnt, RM, rnd=round_bf16):
     return km, vm, kt, vt, lc_mid, lc_tail
 
 
-def rep_fine_torch(q, k, v, blk_cnt, mask_a, mask_ab, RM, phases=7, tables=None):
+def rep_fine_torch(q, k, v, blk_cnt, mask_a, mask_ab, RM, phases=7, tables=None, labels=None):
     """Three-tier attention as a torch float64 graph: one softmax over tier-A tokens (mask_a), tier-B representatives
     (mask_ab & ~mask_a; means of 64 / RM-token groups with + ln c) and tier-C block means (~mask_ab, + ln cnt); O = 0
     and lse = -inf on padding rows and rows with no column (reference vsa2_rep/reference.py:53-96). The means are
     functions of k / v (so autograd reaches the tokens); `tables` = (k_mid, v_mid, k_tail, v_tail) overrides their
-    values (e.g. the bf16 tables the kernels use) straight-through. Returns (O, lse natural)."""
+    values (e.g. the bf16 tables the kernels use) straight-through. `labels` [B, H, L] (-1 on padding) replaces the
+    contiguous groups by clusters: representative c of a block is the mean of its tokens labelled c (k-means
+    tables). Returns (O, lse natural)."""
     import torch
     B, H, L, D = q.shape
     NB, gs = L // BLOCK, BLOCK // RM
     cnt = np.asarray(blk_cnt, np.int64)
     valid = torch.as_tensor(token_valid(cnt, L))
     z = valid[None, None, :, None].to(q.dtype)
-    ng = torch.as_tensor(np.clip(cnt[:, None] - np.arange(RM)[None, :] * gs, 0, gs).reshape(-1), dtype=q.dtype)
+    blk = np.arange(L) // BLOCK
+    if labels is None:
+        grp = np.where(token_valid(cnt, L), blk * RM + (np.arange(L) % BLOCK) // gs, -1)
+        grp = np.broadcast_to(grp, (B, H, L))
+    else:
+        lab = np.asarray(labels, np.int64)
+        grp = np.where(lab >= 0, blk[None, None, :] * RM + lab, -1)
+    member = torch.as_tensor(grp[..., None, :] == np.arange(NB * RM)[:, None]).to(q.dtype)   # [B, H, NB*RM, L]
+    ng = member.sum(-1)                                                                        # [B, H, NB*RM]
 
     def means(x):
-        xs = (x * z).reshape(B, H, NB, RM, gs, D).sum(4).reshape(B, H, NB * RM, D)
-        mid = xs / ng.clamp(min=1)[None, None, :, None]
+        xs = member @ (x * z)
+        mid = xs / ng.clamp(min=1)[..., None]
         tail = xs.reshape(B, H, NB, RM, D).sum(3) / torch.as_tensor(cnt, dtype=q.dtype)[None, None, :, None]
         return mid, tail
 
@@ -335,11 +350,13 @@ def rep_fine_torch(q, k, v, blk_cnt, mask_a, mask_ab, RM, phases=7, tables=None)
     tc = (~ab) & bool(phases & 4)
     blk = np.arange(L) // BLOCK
     vis_a = a[:, :, blk][:, :, :, blk] & token_valid(cnt, L)[None, None, None, :]
-    vis_b = np.repeat(tb, RM, axis=3)[:, :, blk] & (ng.numpy() > 0)[None, None, None, :]
+    vis_b = np.repeat(tb, RM, axis=3)[:, :, blk] & (ng.numpy() > 0)[:, :, None, :]
     vis_c = tc[:, :, blk]
     vis = torch.as_tensor(np.concatenate([vis_a, vis_b, vis_c], axis=3))
     with np.errstate(divide="ignore"):
-        bias = torch.as_tensor(np.concatenate([np.zeros(L), np.log(np.maximum(ng.numpy(), 1)), np.log(cnt)]))
+        bias = np.concatenate([np.zeros((B, H, L)), np.log(np.maximum(ng.numpy(), 1)),
+                               np.broadcast_to(np.log(cnt), (B, H, NB))], axis=2)
+        bias = torch.as_tensor(bias)[:, :, None, :]
     Kc = torch.cat([k, km, kt], 2)
     Vc = torch.cat([v, vm, vt], 2)
     s = (q @ Kc.transpose(-1, -2)) / math.sqrt(D) + bias
@@ -381,3 +398,101 @@ def fine_attention_blocks(q, k, v, blk_cnt, ptr, idx, bh, qblocks):
         outs.append(np.where(live[:, None], o / np.where(live, l, 1)[:, None], 0))
         lses.append(np.where(live, m + np.log(np.where(live, l, 1)), -np.inf))
     return np.stack(outs), np.stack(lses)
+
+
+# --------------------------------------------------------------------- seeded k-means representative tables
+# Not in the reference (its tables are contiguous group means, vsa2_rep/reference.py:23-50); this is the
+# construction BASELINE.json's config 4 names ("tables built from seeded k-means, 5 iterations"), defined here and
+# built by vsa_rep_build_kmeans. The arithmetic is float32 in a fixed order with no fused multiply-add, so the GPU
+# tables, counts and labels equal these bit for bit.
+_M32 = 0xFFFFFFFF
+
+
+def _fmix32(h):
+    """MurmurHash3's 32-bit finaliser (on Python ints, kept to 32 bits)."""
+    h &= _M32
+    h ^= h >> 16
+    h = (h * 0x85EBCA6B) & _M32
+    h ^= h >> 13
+    h = (h * 0xC2B2AE35) & _M32
+    h ^= h >> 16
+    return h
+
+
+def kmeans_seed_tokens(seed, bh, blk, n, RM):
+    """The tokens of a block of n valid tokens that seed its min(RM, n) clusters: a partial Fisher-Yates shuffle of
+    0..n-1 whose i-th swap partner is i + h_i mod (n - i), h_i = fmix32(seed * 0x9E3779B9 ^ fmix32(bh * 0x85EBCA6B ^
+    fmix32(blk * 0xC2B2AE35 ^ i)))."""
+    perm = list(range(n))
+    for i in range(min(RM, n)):
+        h = _fmix32((seed * 0x9E3779B9) ^ _fmix32((bh * 0x85EBCA6B) ^ _fmix32((blk * 0xC2B2AE35) ^ i)))
+        j = i + h % (n - i)
+        perm[i], perm[j] = perm[j], perm[i]
+    return perm[:min(RM, n)]
+
+
+def kmeans_tables(k, v, blk_cnt, RM, iters=5, seed=0, rnd=round_bf16):
+    """Seeded Lloyd k-means of every block's valid keys into RM clusters: (k_mid, v_mid [B, H, NB * RM, D] rnd-ed
+    cluster means (zero rows for empty clusters), lc_mid [B, H, NB * RM] log2 counts (-inf when empty), counts
+    [B, H, NB * RM] int, labels [B, H, L] int (-1 on padding)).
+
+    Per block: centroids start at the seed tokens' keys (clusters past n stay empty); each of `iters` rounds
+    assigns every valid token to its nearest centroid (squared distance summed over the D columns in order,
+    float32, each difference squared then added; ties to the smaller cluster) and moves every non-empty cluster's
+    centroid to the float32 mean of its members' keys (summed in token order, then one division). The tables hold
+    the last round's centroids and the mean values of the same clusters."""
+    k, v = np.asarray(k, np.float32), np.asarray(v, np.float32)
+    B, H, L, D = k.shape
+    NB = L // BLOCK
+    cnt = np.asarray(blk_cnt, np.int64)
+    k_mid = np.zeros((B, H, NB * RM, D), np.float32)
+    v_mid = np.zeros_like(k_mid)
+    counts = np.zeros((B, H, NB * RM), np.int64)
+    labels = np.full((B, H, L), -1, np.int64)
+    for b in range(B):
+        for h in range(H):
+            bh = b * H + h
+            for blk in range(NB):
+                n = int(cnt[blk])
+                x = k[b, h, blk * BLOCK:blk * BLOCK + n]
+                seeds = kmeans_seed_tokens(seed, bh, blk, n, RM)
+                cent = np.zeros((RM, D), np.float32)
+                cent[:len(seeds)] = x[seeds]
+                live = np.arange(RM) < len(seeds)
+                lab = np.zeros(n, np.int64)
+                for _ in range(iters):
+                    dist = np.zeros((n, RM), np.float32)
+                    for d in range(D):
+                        diff = (x[:, d:d + 1] - cent[None, :, d]).astype(np.float32)
+                        dist = (dist + (diff * diff).astype(np.float32)).astype(np.float32)
+                    dist[:, ~live] = np.inf
+                    lab = np.argmin(dist, axis=1)          # first minimum: ties to the smaller cluster
+                    for c in range(RM):
+                        members = np.nonzero(lab == c)[0]
+                        if members.size:
+                            s = np.zeros(D, np.float32)
+                            for t in members:
+                                s = (s + x[t]).astype(np.float32)
+                            cent[c] = (s / np.float32(members.size)).astype(np.float32)
+                y = v[b, h, blk * BLOCK:blk * BLOCK + n]
+                for c in range(RM):
+                    members = np.nonzero(lab == c)[0]
+                    row = blk * RM + c
+                    counts[b, h, row] = members.size
+                    if members.size:
+                        s = np.zeros(D, np.float32)
+                        for t in members:
+                            s = (s + y[t]).astype(np.float32)
+                        k_mid[b, h, row] = rnd(cent[c])
+                        v_mid[b, h, row] = rnd((s / np.float32(members.size)).astype(np.float32))
+                labels[b, h, blk * BLOCK:blk * BLOCK + n] = lab
+    with np.errstate(divide="ignore"):
+        lc = np.where(counts > 0, np.log2(np.maximum(counts, 1).astype(np.float64)), -np.inf)
+    return k_mid, v_mid, lc, counts, labels
+
+
+def row_tiers(scores, ka, kab):
+    """Per-query-block tier split (BASELINE.json config 4's wording; the reference splits by two global budgets,
+    vsa2_rep/ops.py:50-85): tier A = the min(ka, NB) best kv blocks of each row, A|B = the min(kab, NB) best, under
+    row_topk_mask's order (score desc, ties to the smaller index). Returns the two bool masks."""
+    return row_topk_mask(scores, ka), row_topk_mask(scores, max(ka, kab))

@@ -55,10 +55,12 @@ SIGNATURES = {
     "vsa_split_merge_fwd": [P, P, P, P, I, P, P, P, I, I, I, I],
     "vsa_split_merge_sum": [P, P, P, I, P, I, P, P, P, I, I, I],
     "vsa_rep_build": [P, P, P, P, P, P, P, P, P, I, I, I, I],
-    "vsa_rep_attn_fwd": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I],
-    "vsa_rep_attn_bwd_q": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I, I, I, I, I],
-    "vsa_rep_bwd_tables": [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I],
-    "vsa_rep_unpool": [P, P, P, P, P, P, P, P, P, I, I, I, I],
+    "vsa_rep_build_kmeans": [P, P, P, P, P, P, P, P, I, I, I, I, I, ctypes.c_uint],
+    "vsa_row_tiers": [P, I, I, I, I, I, P, P, P, P, P, P],
+    "vsa_rep_attn_fwd": [P, P, P, P, P, P, I, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I],
+    "vsa_rep_attn_bwd_q": [P, P, P, P, P, P, I, P, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I, I, I, I, I],
+    "vsa_rep_bwd_tables": [P, P, P, P, P, I, P, P, P, P, P, P, I, I, I, I, I],
+    "vsa_rep_unpool": [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I],
     "vsa_row_dot": [P, P, P, P, I, I, I],
     "vsa_tier_b_lists": [P, P, P, P, P, P, I, I],
 }
@@ -66,7 +68,7 @@ SIGNATURES = {
 F16_TWINS = ("vsa_pool", "vsa_fuse_fwd", "vsa_fuse_bwd", "vsa_finalize", "vsa_attn_fwd", "vsa_attn_fwd_tasks",
              "vsa_attn_bwd_kv", "vsa_attn_bwd_kv_tasks", "vsa_attn_bwd_q", "vsa_attn_bwd_q_tasks", "vsa_block_scores",
              "vsa_route_rows", "vsa_row_topk", "vsa_router_lse", "vsa_router_scores", "vsa_split_merge_fwd",
-             "vsa_split_merge_sum", "vsa_rep_build", "vsa_rep_attn_fwd", "vsa_rep_attn_bwd_q", "vsa_rep_bwd_tables",
+             "vsa_split_merge_sum", "vsa_rep_build", "vsa_rep_build_kmeans", "vsa_rep_attn_fwd", "vsa_rep_attn_bwd_q", "vsa_rep_bwd_tables",
              "vsa_rep_unpool", "vsa_row_dot")
 SIGNATURES.update({n + "_f16": SIGNATURES[n] for n in F16_TWINS})
 NO_STREAM = {"es_representatives_workspace": ([I, I, I], Z), "es_representatives_noalloc_limit": ([], Z), "es_last_error_string": ([], ctypes.c_char_p),

@@ -5,7 +5,8 @@
 //
 // Tables (built by vsa_rep_build): k_mid / v_mid [BH, ceil64(NB * RM), D] (row blk * RM + g), k_tail / v_tail
 // [BH, ceil64(NB), D] (row blk), lc_mid [NB * RM] and lc_tail [NB] log2 counts (-inf: empty group), shared by
-// every head. Tier membership of pair (query block i, kv block j) comes from the bitmaps bits_a / bits_ab
+// every head; lc_mid may instead be per head ([BH, NB * RM], lc_mid_stride = NB * RM), as the seeded k-means tables
+// of vsa_rep_build_kmeans need. Tier membership of pair (query block i, kv block j) comes from the bitmaps bits_a / bits_ab
 // [BH, NB, W], W = ceil(NB / 32): A = a, B = ab & ~a, C = ~ab.
 //
 //   rep_fwd_kernel      one workgroup per (query block, head), the VSA fine forward's layout (2 row groups x 2 key
@@ -37,6 +38,7 @@ struct RepArgs {
   const e16_t *q, *k, *v, *dout;
   const e16_t *k_mid, *v_mid, *k_tail, *v_tail;
   const float *lc_mid, *lc_tail;
+  int lc_mid_stride;  // per-head stride of lc_mid (0: one table for every head)
   const float *lse, *delta;
   e16_t* out;
   float* lse_out;
@@ -184,7 +186,7 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
       dma16(r2, vd + i * 1024, off, 0);
     }
     const int row = table_row(p0 + l);
-    return row < 0 ? -INFINITY : (tb ? a.lc_mid[row] : a.lc_tail[row]);
+    return row < 0 ? -INFINITY : (tb ? a.lc_mid[(size_t)bh * a.lc_mid_stride + row] : a.lc_tail[row]);
   };
 
   ev8 qreg[8], dreg[8];
@@ -336,7 +338,8 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
 struct TabArgs {
   const e16_t *q, *dout;
   const e16_t *k_tab, *v_tab;  // [BH, rows_pad, D]
-  const float* lc;              // [rows]
+  const float* lc;              // [rows], or [BH, lc_stride] per head
+  int lc_stride;
   const float *lse, *delta;
   const unsigned *bits_a, *bits_ab;
   float *dk_tab, *dv_tab;       // [BH, rows_pad, D] fp32, accumulated
@@ -378,7 +381,7 @@ __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
   const int per_blk = a.tier == PH_B ? a.RM : 1;
   const int fb = grp * BK / per_blk, nblk = BK / per_blk;
   const int lblk = key / per_blk;   // block of this key within the workgroup's blocks
-  const float kbias = trow < a.rows ? a.lc[trow] : -INFINITY;
+  const float kbias = trow < a.rows ? a.lc[(size_t)bh * a.lc_stride + trow] : -INFINITY;
   const size_t head = (size_t)bh * a.L;
 
   const unsigned head_bytes = (unsigned)((size_t)a.L * HD * 2);
@@ -535,7 +538,9 @@ __global__ __launch_bounds__(256) void rep_unpool_kernel(const float* __restrict
                                                          const float* __restrict__ dk_tail,
                                                          const float* __restrict__ dv_tail, e16_t* __restrict__ dk,
                                                          e16_t* __restrict__ dv, const int* __restrict__ blk_cnt,
-                                                         int L, int NB, int RM, int mid_rows, int tail_rows) {
+                                                         const uint8_t* __restrict__ labels,
+                                                         const int* __restrict__ mid_counts, int L, int NB, int RM,
+                                                         int mid_rows, int tail_rows) {
   const int blk = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (blk >= NB) return;
   const int l = threadIdx.x & 63, s = l >> 4, c8 = (l & 15) * 8;
@@ -545,8 +550,10 @@ __global__ __launch_bounds__(256) void rep_unpool_kernel(const float* __restrict
   const size_t tail = (bh * tail_rows + blk) * HD + c8;
   for (int r = s; r < BK; r += 4) {
     const size_t tok = (bh * L + (size_t)blk * BK + r) * HD + c8;
-    const int g = r / gs;
-    const int n = min(max(cnt - g * gs, 0), gs);
+    // the token's representative: its contiguous group, or (k-means tables) its cluster
+    const size_t lrow = bh * L + (size_t)blk * BK + r;
+    const int g = labels ? (r < cnt ? (int)labels[lrow] : 0) : r / gs;
+    const int n = labels ? mid_counts[(bh * NB + blk) * RM + g] : min(max(cnt - g * gs, 0), gs);
     const size_t mid = (bh * mid_rows + (size_t)blk * RM + g) * HD + c8;
     float xk[8], xv[8];
 #pragma unroll
@@ -650,7 +657,7 @@ static int rep_check(int BH, int L, int D, int RM) {
 }
 
 static RepArgs rep_args(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
-                        const float* lc_mid, const void* k_tail, const void* v_tail, const float* lc_tail,
+                        const float* lc_mid, int lc_mid_stride, const void* k_tail, const void* v_tail, const float* lc_tail,
                         const int* q2k_ptr, const int* q2k_idx, const unsigned* bits_a, const unsigned* bits_ab,
                         const int* blk_cnt, int BH, int L, int D, int RM, int phases) {
   RepArgs a = {};
@@ -660,6 +667,7 @@ static RepArgs rep_args(const void* q, const void* k, const void* v, const void*
   a.k_mid = (const e16_t*)k_mid;
   a.v_mid = (const e16_t*)v_mid;
   a.lc_mid = lc_mid;
+  a.lc_mid_stride = lc_mid_stride;
   a.k_tail = (const e16_t*)k_tail;
   a.v_tail = (const e16_t*)v_tail;
   a.lc_tail = lc_tail;
@@ -683,7 +691,7 @@ static RepArgs rep_args(const void* q, const void* k, const void* v, const void*
 }
 
 extern "C" int ES_VSA_API(vsa_rep_attn_fwd)(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
-                                const float* lc_mid, const void* k_tail, const void* v_tail, const float* lc_tail,
+                                const float* lc_mid, int lc_mid_stride, const void* k_tail, const void* v_tail, const float* lc_tail,
                                 const int* q2k_ptr, const int* q2k_idx, const unsigned* bits_a,
                                 const unsigned* bits_ab, const int* blk_cnt, void* out, float* lse, int BH, int L,
                                 int D, int RM, int phases, hipStream_t stream) {
@@ -692,7 +700,9 @@ extern "C" int ES_VSA_API(vsa_rep_attn_fwd)(const void* q, const void* k, const 
                  blk_cnt && out && lse,
              ES_ERR_INVALID, "VSA2-rep: null tensor pointer");
   ES_REQUIRE(phases >= 0 && phases <= 7, ES_ERR_INVALID, "VSA2-rep: phases must be a mask of 1 | 2 | 4");
-  RepArgs a = rep_args(q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, q2k_ptr, q2k_idx, bits_a, bits_ab,
+  ES_REQUIRE(lc_mid_stride == 0 || lc_mid_stride >= (L / BK) * RM, ES_ERR_INVALID,
+             "VSA2-rep: lc_mid_stride must be 0 (shared) or >= NB * RM (per head)");
+  RepArgs a = rep_args(q, k, v, k_mid, v_mid, lc_mid, lc_mid_stride, k_tail, v_tail, lc_tail, q2k_ptr, q2k_idx, bits_a, bits_ab,
                        blk_cnt, BH, L, D, RM, phases);
   a.out = (e16_t*)out;
   a.lse_out = lse;
@@ -705,7 +715,7 @@ extern "C" int ES_VSA_API(vsa_rep_attn_fwd)(const void* q, const void* k, const 
 }
 
 extern "C" int ES_VSA_API(vsa_rep_attn_bwd_q)(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
-                                  const float* lc_mid, const void* k_tail, const void* v_tail, const float* lc_tail,
+                                  const float* lc_mid, int lc_mid_stride, const void* k_tail, const void* v_tail, const float* lc_tail,
                                   const void* dout, const float* lse, const float* delta, const int* q2k_ptr,
                                   const int* q2k_idx, const unsigned* bits_a, const unsigned* bits_ab,
                                   const int* blk_cnt, const float* add_dq, int add_nb, const float* dq_acc, void* dq,
@@ -715,7 +725,9 @@ extern "C" int ES_VSA_API(vsa_rep_attn_bwd_q)(const void* q, const void* k, cons
                  q2k_ptr && bits_a && bits_ab && blk_cnt && dq,
              ES_ERR_INVALID, "VSA2-rep: null tensor pointer");
   ES_REQUIRE(add_dq == nullptr || add_nb >= L / BK, ES_ERR_INVALID, "VSA2-rep: add_dq has fewer rows than blocks");
-  RepArgs a = rep_args(q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, q2k_ptr, q2k_idx, bits_a, bits_ab,
+  ES_REQUIRE(lc_mid_stride == 0 || lc_mid_stride >= (L / BK) * RM, ES_ERR_INVALID,
+             "VSA2-rep: lc_mid_stride must be 0 (shared) or >= NB * RM (per head)");
+  RepArgs a = rep_args(q, k, v, k_mid, v_mid, lc_mid, lc_mid_stride, k_tail, v_tail, lc_tail, q2k_ptr, q2k_idx, bits_a, bits_ab,
                        blk_cnt, BH, L, D, RM, phases);
   a.dout = (const e16_t*)dout;
   a.lse = lse;
@@ -733,9 +745,9 @@ extern "C" int ES_VSA_API(vsa_rep_attn_bwd_q)(const void* q, const void* k, cons
 }
 
 extern "C" int ES_VSA_API(vsa_rep_bwd_tables)(const void* q, const void* dout, const void* k_tab, const void* v_tab,
-                                  const float* lc, const float* lse, const float* delta, const unsigned* bits_a,
-                                  const unsigned* bits_ab, float* dk_tab, float* dv_tab, int BH, int L, int D, int RM,
-                                  int tier, hipStream_t stream) {
+                                  const float* lc, int lc_stride, const float* lse, const float* delta,
+                                  const unsigned* bits_a, const unsigned* bits_ab, float* dk_tab, float* dv_tab,
+                                  int BH, int L, int D, int RM, int tier, hipStream_t stream) {
   if (int st = rep_check(BH, L, D, RM)) return st;
   ES_REQUIRE(q && dout && k_tab && v_tab && lc && lse && delta && bits_a && bits_ab && dk_tab && dv_tab,
              ES_ERR_INVALID, "VSA2-rep: null tensor pointer");
@@ -746,6 +758,7 @@ extern "C" int ES_VSA_API(vsa_rep_bwd_tables)(const void* q, const void* dout, c
   a.k_tab = (const e16_t*)k_tab;
   a.v_tab = (const e16_t*)v_tab;
   a.lc = lc;
+  a.lc_stride = lc_stride;
   a.lse = lse;
   a.delta = delta;
   a.bits_a = bits_a;
@@ -775,14 +788,17 @@ extern "C" int ES_VSA_API(vsa_rep_bwd_tables)(const void* q, const void* dout, c
 }
 
 extern "C" int ES_VSA_API(vsa_rep_unpool)(const float* acc_k, const float* acc_v, const float* dk_mid, const float* dv_mid,
-                              const float* dk_tail, const float* dv_tail, const int* blk_cnt, void* dk, void* dv,
-                              int BH, int L, int D, int RM, hipStream_t stream) {
+                              const float* dk_tail, const float* dv_tail, const int* blk_cnt, const uint8_t* labels,
+                              const int* mid_counts, void* dk, void* dv, int BH, int L, int D, int RM,
+                              hipStream_t stream) {
   if (int st = rep_check(BH, L, D, RM)) return st;
   ES_REQUIRE(dk_mid && dv_mid && dk_tail && dv_tail && blk_cnt && dk && dv, ES_ERR_INVALID,
              "VSA2-rep: null tensor pointer");
+  ES_REQUIRE((labels == nullptr) == (mid_counts == nullptr), ES_ERR_INVALID,
+             "VSA2-rep: pass labels and mid_counts together (k-means tables) or neither (contiguous groups)");
   const int NB = L / BK;
   hipLaunchKernelGGL(rep_unpool_kernel, dim3((NB + 3) / 4, BH), dim3(256), 0, stream, acc_k, acc_v, dk_mid, dv_mid,
-                     dk_tail, dv_tail, (e16_t*)dk, (e16_t*)dv, blk_cnt, L, NB, RM, (NB * RM + 63) / 64 * 64,
+                     dk_tail, dv_tail, (e16_t*)dk, (e16_t*)dv, blk_cnt, labels, mid_counts, L, NB, RM, (NB * RM + 63) / 64 * 64,
                      (NB + 63) / 64 * 64);
   return check_launch("vsa_rep_unpool");
 }

@@ -470,6 +470,61 @@ def rep_build(k, v, blk_cnt, mid_reps):
     return [k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail]
 
 
+def _lc_stride(lc_mid):
+    """Per-head stride of a log2-count table: 0 for one [NB * RM] table, NB * RM for [B, H, NB * RM]."""
+    return 0 if lc_mid.dim() == 1 else int(lc_mid.shape[-1])
+
+
+def rep_build_kmeans(k, v, blk_cnt, mid_reps, iters=5, seed=0):
+    """Seeded k-means tier-B tables with the block-mean tail tables: [k_mid, v_mid, lc_mid [B, H, NB * RM] (per
+    head), k_tail, v_tail, lc_tail [NB]] as rep_build, plus (counts [B, H, NB * RM] int32, labels [B, H, L]
+    uint8). BASELINE config 4's construction; the reference has only the contiguous tables."""
+    tab = rep_build(k, v, blk_cnt, mid_reps)
+    B, H, L, D = k.shape
+    NB, RM = L // BLOCK, int(mid_reps)
+    k_mid = torch.zeros(B, H, _ceil64(NB * RM), HD, device=k.device, dtype=k.dtype)
+    v_mid = torch.zeros_like(k_mid)
+    lc = torch.empty(B, H, NB * RM, device=k.device, dtype=torch.float32)
+    counts = torch.empty(B, H, NB * RM, device=k.device, dtype=torch.int32)
+    labels = torch.empty(B, H, L, device=k.device, dtype=torch.uint8)
+    _call("vsa_rep_build_kmeans", _wide(k), _wide(v), blk_cnt, k_mid, v_mid, lc, counts, labels, B * H, L, D, RM,
+          int(iters), int(seed) & 0xFFFFFFFF)
+    tab[0], tab[1], tab[2] = _narrow(k_mid, D), _narrow(v_mid, D), lc
+    return tab, counts, labels
+
+
+def route_tier_rows(qr, kr, blk_cnt, R, ka, kab, row_norm, max_score_bytes=2 << 30):
+    """Per-query-block tiers over VSA2's PSP router scores: the ka best kv blocks of every query block are tier A,
+    the next kab - ka tier B; same outputs as route_tiers (BASELINE config 4's split)."""
+    _i32(blk_cnt, "blk_cnt")
+    B, H = qr.shape[:2]
+    NB, BH = blk_cnt.numel(), B * H
+    ka, kab = max(0, min(int(ka), NB)), max(0, min(int(kab), NB))
+    _check(ka <= kab, "need ka <= kab")
+    _check(BH * NB * kab < 2 ** 31, "vsa2_rep: selected blocks exceed int32 CSR range")
+    W = (NB + 31) // 32
+    dev = qr.device
+    i32 = dict(device=dev, dtype=torch.int32)
+    a_ptr, a_idx = torch.empty(B, H, NB + 1, **i32), torch.empty(max(BH * NB * ka, 1), **i32)
+    ab_ptr, ab_idx = torch.empty(B, H, NB + 1, **i32), torch.empty(max(BH * NB * kab, 1), **i32)
+    bits_a = torch.zeros(B, H, NB, W, **i32)
+    bits_ab = torch.zeros(B, H, NB, W, **i32)
+    lse2 = router_lse(qr, kr, blk_cnt, R)
+    D, qr, kr = qr.shape[3], _wide(qr), _wide(kr)
+    chunk = int(max(1, min(BH, int(max_score_bytes) // max(NB * NB * 4, 1), 65535)))
+    scores = torch.empty(chunk, NB, NB, device=dev, dtype=torch.float32)
+    for bh0 in range(0, BH, chunk):
+        cnt = min(chunk, BH - bh0)
+        s = scores[:cnt]
+        _call("vsa_router_scores", qr, kr, lse2, blk_cnt, s, NB, int(R), int(row_norm), bh0, cnt, D)
+        _call("vsa_row_tiers", s, NB, bh0, cnt, ka, kab, a_ptr, a_idx, ab_ptr, ab_idx, bits_a, bits_ab)
+    k2q_ptr, k2q_idx = csr_transpose(a_ptr, a_idx)
+    b_ptr = torch.zeros(B, H, NB + 1, **i32)
+    b_idx = torch.empty(max(1, BH * NB * (kab - ka)), **i32)
+    _call("vsa_tier_b_lists", ab_ptr, ab_idx, a_ptr, bits_a, b_ptr, b_idx, BH, NB)
+    return [a_ptr, a_idx, k2q_ptr, k2q_idx, bits_a, bits_ab, b_ptr, b_idx]
+
+
 def route_tiers(qr, kr, blk_cnt, R, budget_a, budget_ab, row_norm, max_score_bytes=2 << 30):
     """VSA2's router at two budgets over one score matrix: (q2k_ptr, q2k_idx, k2q_ptr, k2q_idx) of tier A, the
     bitmaps bits_a / bits_ab [B, H, NB, ceil(NB / 32)] and the tier-B lists (b_ptr, b_idx) (reference rep_api.cpp
@@ -517,7 +572,8 @@ def rep_attn_fwd(q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, q2k_ptr
     B, H, L, D = q.shape
     o = torch.empty(B, H, L, HD, device=q.device, dtype=q.dtype)
     lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
-    _call("vsa_rep_attn_fwd", _wide(q), _wide(k), _wide(v), _wide(k_mid), _wide(v_mid), lc_mid, _wide(k_tail),
+    _call("vsa_rep_attn_fwd", _wide(q), _wide(k), _wide(v), _wide(k_mid), _wide(v_mid), lc_mid,
+              _lc_stride(lc_mid), _wide(k_tail),
               _wide(v_tail), lc_tail, q2k_ptr, q2k_idx, bits_a, bits_ab, blk_cnt, o, lse, B * H, L, D, int(mid_reps),
               int(phases))
     return _narrow(o, D), lse
@@ -535,19 +591,21 @@ def rep_attn_bwd_q(q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, dout,
     q, k, v, dout = _wide(q), _wide(k), _wide(v), _wide(dout)
     k_mid, v_mid, k_tail, v_tail = _wide(k_mid), _wide(v_mid), _wide(k_tail), _wide(v_tail)
     acc = _InPlace(dq_acc)
-    _call("vsa_rep_attn_bwd_q", q, k, v, k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail, dout, lse, delta, q2k_ptr,
+    _call("vsa_rep_attn_bwd_q", q, k, v, k_mid, v_mid, lc_mid, _lc_stride(lc_mid), k_tail, v_tail, lc_tail, dout,
+              lse, delta, q2k_ptr,
               q2k_idx, bits_a, bits_ab, blk_cnt, _wide(add_dq), add_dq.shape[2] if add_dq is not None else 0, acc.w,
               dq, B * H, L, D, int(mid_reps), int(phases))
     acc.put()
     if phases & 2:
         dkm, dvm = _InPlace(dk_mid), _InPlace(dv_mid)
-        _call("vsa_rep_bwd_tables", q, dout, k_mid, v_mid, lc_mid, lse, delta, bits_a, bits_ab, dkm.w, dvm.w,
+        _call("vsa_rep_bwd_tables", q, dout, k_mid, v_mid, lc_mid, _lc_stride(lc_mid), lse, delta, bits_a, bits_ab,
+                  dkm.w, dvm.w,
                   B * H, L, D, int(mid_reps), 2)
         dkm.put()
         dvm.put()
     if phases & 4:
         dkt, dvt = _InPlace(dk_tail), _InPlace(dv_tail)
-        _call("vsa_rep_bwd_tables", q, dout, k_tail, v_tail, lc_tail, lse, delta, bits_a, bits_ab, dkt.w, dvt.w,
+        _call("vsa_rep_bwd_tables", q, dout, k_tail, v_tail, lc_tail, 0, lse, delta, bits_a, bits_ab, dkt.w, dvt.w,
                   B * H, L, D, int(mid_reps), 4)
         dkt.put()
         dvt.put()
@@ -560,13 +618,15 @@ def tier_a_bwd_kv(q, k, v, dout, lse, delta, k2q_ptr, k2q_idx, blk_cnt, dq_acc=N
     return attn_bwd(q, k, v, dout, lse, delta, k2q_ptr, k2q_idx, blk_cnt, dq_acc, None, None, True)
 
 
-def rep_unpool(dk_a, dv_a, dk_mid, dv_mid, dk_tail, dv_tail, blk_cnt, like, mid_reps):
-    """(dk, dv) in like's dtype: tier-A gradients + the representative gradients spread as / count."""
+def rep_unpool(dk_a, dv_a, dk_mid, dv_mid, dk_tail, dv_tail, blk_cnt, like, mid_reps, labels=None,
+               mid_counts=None):
+    """(dk, dv) in like's dtype: tier-A gradients + the representative gradients spread as / count (over the
+    contiguous groups, or over the k-means clusters given labels and mid_counts)."""
     B, H, L, D = like.shape
     dk = torch.empty(B, H, L, HD, dtype=like.dtype, device=blk_cnt.device)
     dv = torch.empty_like(dk)
-    _call("vsa_rep_unpool", *(_wide(t) for t in (dk_a, dv_a, dk_mid, dv_mid, dk_tail, dv_tail)), blk_cnt, dk, dv,
-              B * H, L, D, int(mid_reps))
+    _call("vsa_rep_unpool", *(_wide(t) for t in (dk_a, dv_a, dk_mid, dv_mid, dk_tail, dv_tail)), blk_cnt, labels,
+              mid_counts, dk, dv, B * H, L, D, int(mid_reps))
     return _narrow(dk, D), _narrow(dv, D)
 
 

@@ -20,7 +20,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _C as _native
-from ._checks import nonnegative_reals
+from ._checks import nonnegative_reals, positive_ints
 from .ops import GATE_ACTS, ROW_NORMS, _coarse_lists
 
 PHASE_A, PHASE_B, PHASE_C = 1, 2, 4
@@ -32,14 +32,28 @@ def ext():
     return _native
 
 
+TABLES = ("contiguous", "kmeans")
+SPLITS = ("global", "per_row")
+
+
 @dataclass(frozen=True)
 class RepTiers:
-    """Three-tier budget as fractions of all NB * NB pairs; defaults 10 % full blocks, 20 % with 4 representatives,
-    the rest as block means. ``frac_full`` alone is VSA2's budget (topk = frac_full * NB)."""
+    """Three-tier budget; defaults 10 % full blocks, 20 % with 4 representatives, the rest as block means.
+
+    split="global" (the reference's): fractions of all NB * NB pairs of a (b, h), taken by two exact global top-k
+    selections; ``frac_full`` alone is VSA2's budget (topk = frac_full * NB). split="per_row":
+    every query block takes round(frac_full * NB) tier-A and round(frac_mid * NB) tier-B blocks of its own row.
+    tables="contiguous" (the reference's): tier-B representatives are means of the mid_reps contiguous
+    64 / mid_reps-token groups; tables="kmeans": means of mid_reps clusters of the block's keys from
+    ``kmeans_iters`` Lloyd rounds started at seed tokens drawn with ``seed`` (5 rounds)."""
 
     frac_full: float = 0.10
     frac_mid: float = 0.20
     mid_reps: int = 4
+    split: str = "global"
+    tables: str = "contiguous"
+    kmeans_iters: int = 5
+    seed: int = 0
 
     def __post_init__(self):
         nonnegative_reals(self, "frac_full", "frac_mid")
@@ -47,6 +61,15 @@ class RepTiers:
             raise ValueError(f"frac_full + frac_mid must be <= 1, got {self.frac_full} + {self.frac_mid}")
         if self.mid_reps not in MID_REPS_OK:
             raise ValueError(f"RepTiers.mid_reps must be one of {MID_REPS_OK}, got {self.mid_reps!r}")
+        if self.split not in SPLITS or self.tables not in TABLES:
+            raise ValueError(f"RepTiers.split must be one of {SPLITS} and tables one of {TABLES}, got "
+                             f"{self.split!r} / {self.tables!r}")
+        positive_ints(self, "kmeans_iters")
+
+    def row_budgets(self, nb: int) -> Tuple[int, int]:
+        """(tier-A blocks, tier-A|B blocks) of every query block under split="per_row", clamped to NB."""
+        ka = min(nb, int(round(self.frac_full * nb)))
+        return ka, min(nb, max(ka, int(round((self.frac_full + self.frac_mid) * nb))))
 
     def budgets(self, nb: int) -> Tuple[int, int]:
         """(tier-A budget, tier-A|B budget) in pairs per (b, h), both clamped to NB * NB."""
@@ -113,15 +136,23 @@ class TierSelection:
                              ptr.to(torch.int32).contiguous(), idx.contiguous())
 
 
+def _select_tiers(C, qr, kr, blk_cnt, R, tiers: RepTiers, row_norm: int, max_score_bytes: int) -> TierSelection:
+    nb = blk_cnt.numel()
+    if tiers.split == "per_row":
+        ka, kab = tiers.row_budgets(nb)
+        return TierSelection(*C.route_tier_rows(qr, kr, blk_cnt, R, ka, kab, row_norm, max_score_bytes))
+    ba, bab = tiers.budgets(nb)
+    return TierSelection(*C.route_tiers(qr, kr, blk_cnt, R, ba, bab, row_norm, max_score_bytes))
+
+
 def route_tiers(q, k, blk_cnt, tiers: RepTiers = RepTiers(), *, R: int = 16, row_norm: str = "paper",
                 max_score_bytes: int = 2 << 30) -> TierSelection:
-    """VSA2's PSP router and exact global top-k at the two budgets of ``tiers`` (stop-gradient)."""
+    """VSA2's PSP router with the tier split of ``tiers``: exact global top-k at its two budgets, or the per-row
+    split (stop-gradient)."""
     C = ext()
-    nb = q.shape[2] // 64
     blk_cnt = blk_cnt.to(torch.int32).contiguous()
     qr, kr, _, _, _ = C.pool_fwd(q, k, k, blk_cnt, R)
-    ba, bab = tiers.budgets(nb)
-    return TierSelection(*C.route_tiers(qr, kr, blk_cnt, R, ba, bab, ROW_NORMS[row_norm], int(max_score_bytes)))
+    return _select_tiers(C, qr, kr, blk_cnt, R, tiers, ROW_NORMS[row_norm], int(max_score_bytes))
 
 
 def resolve_backend(backend: str, q: torch.Tensor) -> bool:
@@ -132,18 +163,42 @@ def resolve_backend(backend: str, q: torch.Tensor) -> bool:
     return False
 
 
-def _fine_forward(C, q, k, v, blk_cnt, sel: TierSelection, mid_reps: int, phases: int):
-    tab = C.rep_build(k, v, blk_cnt, mid_reps)
-    o, lse = C.rep_attn_fwd(q, k, v, *tab, sel.q2k_ptr, sel.q2k_idx, sel.bits_a, sel.bits_ab, blk_cnt, mid_reps,
-                            phases)
-    return tab, o, lse
+@dataclass(frozen=True)
+class _Tables:
+    """How the representative tables are built: mid_reps, "contiguous" / "kmeans", k-means rounds and seed."""
+    mid_reps: int = 4
+    kind: str = "contiguous"
+    iters: int = 5
+    seed: int = 0
+
+    @staticmethod
+    def of(tiers: RepTiers) -> "_Tables":
+        return _Tables(tiers.mid_reps, tiers.tables, tiers.kmeans_iters, tiers.seed)
 
 
-def _fine_backward(C, q, k, v, tab, dout, lse, delta, blk_cnt, sel: TierSelection, mid_reps: int, phases: int,
+def build_tables(k, v, blk_cnt, spec: "_Tables"):
+    """(tab, labels, counts): the six representative tables and, for k-means tables, each token's cluster and the
+    cluster sizes (None for contiguous tables)."""
+    C = ext()
+    if spec.kind == "kmeans":
+        tab, counts, labels = C.rep_build_kmeans(k, v, blk_cnt, spec.mid_reps, spec.iters, spec.seed)
+        return tab, labels, counts
+    return C.rep_build(k, v, blk_cnt, spec.mid_reps), None, None
+
+
+def _fine_forward(C, q, k, v, blk_cnt, sel: TierSelection, spec: _Tables, phases: int):
+    tab, labels, counts = build_tables(k, v, blk_cnt, spec)
+    o, lse = C.rep_attn_fwd(q, k, v, *tab, sel.q2k_ptr, sel.q2k_idx, sel.bits_a, sel.bits_ab, blk_cnt,
+                            spec.mid_reps, phases)
+    return (tab, labels, counts), o, lse
+
+
+def _fine_backward(C, q, k, v, built, dout, lse, delta, blk_cnt, sel: TierSelection, mid_reps: int, phases: int,
                    add_dq=None, add_dk=None, add_dv=None):
     """(dq, dk, dv): dQ over every walked tier in one deterministic pass, tier-A token dK / dV by the fine KV-owner
     kernel, representative dK / dV by the table KV-owner passes, then spread over their tokens. ``add_*`` are
     per-block gradients (the coarse branch) folded in like block means."""
+    tab, labels, counts = built
     k_mid, v_mid, lc_mid, k_tail, v_tail, lc_tail = tab
     f32 = dict(device=q.device, dtype=torch.float32)
     dk_mid, dv_mid = torch.zeros(k_mid.shape, **f32), torch.zeros(v_mid.shape, **f32)
@@ -157,17 +212,17 @@ def _fine_backward(C, q, k, v, tab, dout, lse, delta, blk_cnt, sel: TierSelectio
     if add_dk is not None:  # the coarse rows are the tail table's rows (ceil64(NB) each)
         dk_tail += add_dk
         dv_tail += add_dv
-    dk, dv = C.rep_unpool(dk_a, dv_a, dk_mid, dv_mid, dk_tail, dv_tail, blk_cnt, k, mid_reps)
+    dk, dv = C.rep_unpool(dk_a, dv_a, dk_mid, dv_mid, dk_tail, dv_tail, blk_cnt, k, mid_reps, labels, counts)
     return dq, dk, dv
 
 
 class _RepFineFunction(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, blk_cnt, sel, mid_reps, phases):
+    def forward(ctx, q, k, v, blk_cnt, sel, spec, phases):
         C = ext()
-        tab, o, lse = _fine_forward(C, q, k, v, blk_cnt, sel, mid_reps, phases)
+        tab, o, lse = _fine_forward(C, q, k, v, blk_cnt, sel, spec, phases)
         ctx.save_for_backward(q, k, v, blk_cnt, o, lse)
-        ctx.tab, ctx.sel, ctx.mid_reps, ctx.phases = tab, sel, mid_reps, phases
+        ctx.tab, ctx.sel, ctx.mid_reps, ctx.phases = tab, sel, spec.mid_reps, phases
         ctx.mark_non_differentiable(lse)
         return o, lse
 
@@ -183,9 +238,12 @@ class _RepFineFunction(torch.autograd.Function):
 
 
 def rep_fine_attention(q, k, v, blk_cnt, selection: TierSelection, *, mid_reps: int = 4, phases: int = PHASE_ALL,
-                       bwd_variant: int = 1, backend: str = "generic"):
+                       bwd_variant: int = 1, backend: str = "generic", tables: str = "contiguous",
+                       kmeans_iters: int = 5, seed: int = 0):
     """Three-tier fine attention on a frozen selection: (O_fine, lse). ``phases=PHASE_A`` is VSA2's fine attention
-    on the tier-A lists."""
+    on the tier-A lists; ``tables`` as RepTiers.tables."""
+    if tables not in TABLES:
+        raise ValueError(f"tables must be one of {TABLES}, got {tables!r}")
     if bwd_variant not in (1, 2):
         raise ValueError(f"bwd_variant must be 1 or 2, got {bwd_variant!r}")
     if mid_reps not in MID_REPS_OK:
@@ -194,7 +252,8 @@ def rep_fine_attention(q, k, v, blk_cnt, selection: TierSelection, *, mid_reps: 
         if not t.is_contiguous():
             raise ValueError(f"{name} must be contiguous [B,H,L,D]")
     resolve_backend(backend, q)
-    return _RepFineFunction.apply(q, k, v, blk_cnt.to(torch.int32).contiguous(), selection, int(mid_reps), int(phases))
+    spec = _Tables(int(mid_reps), tables, int(kmeans_iters), int(seed))
+    return _RepFineFunction.apply(q, k, v, blk_cnt.to(torch.int32).contiguous(), selection, spec, int(phases))
 
 
 class _RepAttentionFunction(torch.autograd.Function):
@@ -206,13 +265,9 @@ class _RepAttentionFunction(torch.autograd.Function):
         qr, kr, qc, kc, vc = C.pool_fwd(q, k, v, blk_cnt, R)
         c_cnt, c_ptr, c_idx = _coarse_lists(B, H, nb, qc.shape[2], q.device)
         oc, lse_c = C.attn_fwd(qc, kc, vc, c_ptr, c_idx, c_cnt)
-        if given is None:
-            ba, bab = tiers.budgets(nb)
-            sel = TierSelection(*C.route_tiers(qr, kr, blk_cnt, R, ba, bab, row_norm, max_score_bytes))
-        else:
-            sel = given
+        sel = given if given is not None else _select_tiers(C, qr, kr, blk_cnt, R, tiers, row_norm, max_score_bytes)
         del qr, kr
-        tab, of, lse_f = _fine_forward(C, q, k, v, blk_cnt, sel, tiers.mid_reps, phases)
+        tab, of, lse_f = _fine_forward(C, q, k, v, blk_cnt, sel, _Tables.of(tiers), phases)
         o = C.fuse_fwd(of, oc, gate, blk_cnt, gate_act)
         ctx.save_for_backward(q, k, v, blk_cnt, gate)
         ctx.held = dict(tab=tab, sel=sel, of=of, lse_f=lse_f, qc=qc, kc=kc, vc=vc, oc=oc, lse_c=lse_c,

@@ -173,3 +173,111 @@ def test_rep_attention_end_to_end(qkv):
     for name, gr, w in zip(("dQ", "dK", "dV", "dgate"), grads, wg):
         wn = w.numpy()
         check_close(name, f32(gr), wn, max_abs=bf16_max_abs(wn))
+
+
+# ------------------------------------------------------------- k-means tables, per-row tiers
+@pytest.mark.parametrize("RM,seed", [(4, 0), (4, 11), (1, 3), (16, 5)])
+def test_kmeans_tables_bit_exact(qkv, RM, seed):
+    """vsa_rep_build_kmeans against oracle kmeans_tables: tables, cluster sizes and labels equal bit for bit (the
+    kernel restates the float32 order with no fused multiply-add); the tail tables are rep_build's."""
+    log("kmeans tables RM", RM, "seed", seed)
+    _, k, v = qkv["gpu"]
+    tab, counts, labels = C().rep_build_kmeans(k, v, qkv["blk"], RM, iters=5, seed=seed)
+    torch.cuda.synchronize()
+    wkm, wvm, wlc, wcnt, wlab = ref.kmeans_tables(f32(qkv["cpu"][1]), f32(qkv["cpu"][2]), CNT, RM, 5, seed)
+    assert np.array_equal(counts.cpu().numpy(), wcnt)
+    lab = labels.cpu().numpy().astype(np.int64)
+    assert np.array_equal(np.where(lab == 255, -1, lab), wlab)
+    assert np.array_equal(f32(tab[0])[:, :, :NB * RM], wkm) and np.array_equal(f32(tab[1])[:, :, :NB * RM], wvm)
+    gl = tab[2].cpu().numpy()
+    assert gl.shape == (B, H, NB * RM) and np.array_equal(np.isfinite(gl), np.isfinite(wlc))
+    assert np.allclose(gl[np.isfinite(gl)], wlc[np.isfinite(wlc)], rtol=0, atol=2e-6)
+    _, _, kt, vt, _, _ = ref.rep_tables(f32(qkv["cpu"][1]), f32(qkv["cpu"][2]), CNT, RM)
+    assert np.array_equal(f32(tab[3])[:, :, :NB], kt) and np.array_equal(f32(tab[4])[:, :, :NB], vt)
+    if RM == 4:  # the seed changes the clustering of at least one block
+        _, c2, _ = C().rep_build_kmeans(k, v, qkv["blk"], RM, iters=5, seed=seed + 1)
+        assert not torch.equal(c2, counts)
+
+
+@pytest.mark.parametrize("frac_full,frac_mid", [(0.05, 0.20), (0.3, 0.0), (0.0, 0.5), (1.0, 0.0)])
+def test_row_tiers_bit_exact(qkv, frac_full, frac_mid):
+    """The per-row tier split on the GPU's own router scores: bitmaps, tier-A lists, their transpose and the tier-B
+    lists equal the oracle's (row_topk order: score desc, ties to the smaller index)."""
+    log("row tiers", frac_full, frac_mid)
+    q, k, _ = qkv["gpu"]
+    r = rep()
+    tiers = r.RepTiers(frac_full=frac_full, frac_mid=frac_mid, split="per_row")
+    sel = r.route_tiers(q, k, qkv["blk"], tiers, R=16)
+    qr, kr, _, _, _ = C().pool_fwd(q, k, k, qkv["blk"], 16)
+    lse2 = C().router_lse(qr, kr, qkv["blk"], 16)
+    s = f32(C().router_scores(qr, kr, lse2, qkv["blk"], 16, 1)).reshape(B, H, NB, NB)
+    ka, kab = tiers.row_budgets(NB)
+    wa, wab = ref.row_tiers(s, ka, kab)
+    a, b, c = (x.cpu().numpy() for x in sel.tier_masks(NB))
+    assert np.array_equal(a, wa) and np.array_equal(a | b, wab) and np.array_equal(c, ~wab)
+    rp, ri = ref.csr_from_mask(wa)
+    assert np.array_equal(sel.q2k_ptr.cpu().numpy(), rp) and np.array_equal(sel.q2k_idx.cpu().numpy()[:ri.size], ri)
+    tp, ti = ref.csr_from_mask(np.swapaxes(wa, 2, 3))
+    assert np.array_equal(sel.k2q_ptr.cpu().numpy(), tp) and np.array_equal(sel.k2q_idx.cpu().numpy()[:ti.size], ti)
+    bp, bi = ref.csr_from_mask(wab & ~wa)
+    assert np.array_equal(sel.b_ptr.cpu().numpy(), bp) and np.array_equal(sel.b_idx.cpu().numpy()[:bi.size], bi)
+
+
+def _kmeans_ref_tables(qkv, RM, seed):
+    km, vm, _, _, lab = ref.kmeans_tables(f32(qkv["cpu"][1]), f32(qkv["cpu"][2]), CNT, RM, 5, seed)
+    _, _, kt, vt, _, _ = ref.rep_tables(f32(qkv["cpu"][1]), f32(qkv["cpu"][2]), CNT, RM)
+    return (km, vm, kt, vt), lab
+
+
+@pytest.mark.parametrize("phases", [7, 2, 6])
+def test_rep_forward_backward_kmeans_tables(qkv, phases):
+    """The three-tier attention over k-means tables (per-head log2 cluster sizes, gradients spread over the
+    clusters) against the float64 graph whose representatives are the clusters' means."""
+    log("rep kmeans fwd+bwd phases", phases)
+    RM, seed = 4, 2
+    q, k, v = (t.detach().clone().requires_grad_(True) for t in qkv["gpu"])
+    a, ab = tier_masks(60 + phases)
+    sel = selection(a, ab, q.device)
+    o, lse = rep().rep_fine_attention(q, k, v, qkv["blk"], sel, mid_reps=RM, phases=phases, tables="kmeans",
+                                      kmeans_iters=5, seed=seed)
+    dout_c, dout = tokens(41, q.device)
+    grads = torch.autograd.grad(o, (q, k, v), dout)
+    torch.cuda.synchronize()
+    tables, lab = _kmeans_ref_tables(qkv, RM, seed)
+    x = [t.double().requires_grad_(True) for t in qkv["cpu"]]
+    wo, wl = ref.rep_fine_torch(*x, CNT, a, ab, RM, phases, tables=tables, labels=lab)
+    check_close("O", f32(o), wo.detach().numpy())
+    wl = wl.detach().numpy()
+    fin = np.isfinite(wl)
+    assert np.array_equal(np.isfinite(f32(lse)), fin)
+    check_close("lse", f32(lse)[fin], wl[fin])
+    wg = torch.autograd.grad(wo, x, dout_c.double())
+    for name, g, w in zip(("dQ", "dK", "dV"), grads, wg):
+        check_close(name, f32(g), w.numpy(), max_abs=bf16_max_abs(w.numpy()))
+
+
+def test_rep_attention_config4_construction(qkv):
+    """rep_attention as BASELINE config 4 states it: per-row tiers (5 % / 20 %) and seeded 5-round k-means tables,
+    forward and backward against the float64 graph on the same selection and clusters."""
+    log("rep_attention per_row + kmeans")
+    r = rep()
+    q, k, v = (t.detach().clone().requires_grad_(True) for t in qkv["gpu"])
+    tiers = r.RepTiers(frac_full=0.2, frac_mid=0.3, split="per_row", tables="kmeans", seed=7)
+    o, sel = r.rep_attention(q, k, v, None, qkv["blk"], R=16, tiers=tiers, return_selection=True)
+    dout_c, dout = tokens(52, q.device)
+    grads = torch.autograd.grad(o, (q, k, v), dout)
+    a, b, _ = (m.cpu().numpy() for m in sel.tier_masks(NB))
+    ka, kab = tiers.row_budgets(NB)
+    assert (a.sum(-1) == ka).all() and ((a | b).sum(-1) == kab).all()
+    tables, lab = _kmeans_ref_tables(qkv, 4, 7)
+    _, _, qc, kc, vc = C().pool_fwd(*qkv["gpu"], qkv["blk"], 16)
+    x = [t.double().requires_grad_(True) for t in qkv["cpu"]]
+    fine, _ = ref.rep_fine_torch(*x, CNT, a, a | b, 4, 7, tables=tables, labels=lab)
+    coarse = ref.vsa_output(*x, None, CNT, np.zeros_like(a), "tanh",
+                            pooled=[f32(t)[:, :, :NB] for t in (qc, kc, vc)])
+    want = fine + coarse
+    wg = torch.autograd.grad(want, x, dout_c.double())
+    check_close("O", f32(o), want.detach().numpy())
+    for name, gr, w in zip(("dQ", "dK", "dV"), grads, wg):
+        wn = w.numpy()
+        check_close(name, f32(gr), wn, max_abs=bf16_max_abs(wn))
