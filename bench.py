@@ -39,6 +39,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--c4", default="baseline", choices=["baseline", "reference"],
+                    help="vsa2_rep tier construction: BASELINE config 4's (per-query-block tiers, seeded 5-round "
+                         "k-means tables) or the reference's (global budgets, contiguous group means)")
     ap.add_argument("--workload", default="echosparse", choices=["echosparse", "vsa", "vsa2_rep", "split"],
                     help="echosparse: the headline sparse step (default); vsa / vsa2_rep / split: the VSA "
                          "configurations (fine fwd+bwd at 30720 tokens, three-tier at the HunyuanVideo shape, "
@@ -342,7 +345,9 @@ def run_vsa_workload(args):
     blk[-1] = Lr - 64 * (NB - 1)
     g = torch.Generator(device=dev).manual_seed(5)
     dout = torch.randn(q.shape, device=dev, generator=g).to(torch.bfloat16)
-    tiers = rep.RepTiers(frac_full=0.05, frac_mid=0.20, mid_reps=4)
+    baseline = args.c4 == "baseline"
+    tiers = rep.RepTiers(frac_full=0.05, frac_mid=0.20, mid_reps=4, split="per_row" if baseline else "global",
+                         tables="kmeans" if baseline else "contiguous", kmeans_iters=5, seed=0)
     sel = rep.route_tiers(q, k, blk, tiers, R=16)
     a, b, c = sel.tier_masks(NB)
     na, nbm, ncm = (int(m.sum()) for m in (a, b, c))
@@ -350,8 +355,9 @@ def run_vsa_workload(args):
     fl_fwd = 4.0 * 64 * D * cols
     qg, kg, vg = (x.detach().clone().requires_grad_(True) for x in (q, k, v))
 
-    def fwd():
-        return rep.rep_fine_attention(qg, kg, vg, blk, sel, mid_reps=4)
+    def fwd():   # (the representative tables are built inside, k-means included)
+        return rep.rep_fine_attention(qg, kg, vg, blk, sel, mid_reps=4, tables=tiers.tables,
+                                      kmeans_iters=tiers.kmeans_iters, seed=tiers.seed)
 
     def fwd_bwd():
         o, _ = fwd()
@@ -360,16 +366,19 @@ def run_vsa_workload(args):
     fwd_ms, _ = _timed(fwd, K, W)
     step_ms, _ = _timed(fwd_bwd, K, W)
     route_ms, _ = _timed(lambda: rep.route_tiers(q, k, blk, tiers, R=16), min(K, 3), 1)
+    tables_ms, _ = _timed(lambda: rep.build_tables(k, v, blk, rep._Tables.of(tiers)), min(K, 3), 1)
     fwd_ev = _events(fwd, min(K, 5))
     res = {"metric": "ms/layer + TFLOPS on executed blocks (% bf16 MFMA peak), VSA2 64/4/1 three-tier fine fwd+bwd",
            "value": round(fl_fwd / (fwd_ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s (executed columns, fine forward)",
            "n_gpus": 1, "steps": K, "warmup": W, "ms_per_step": round(step_ms, 3), "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
            "data": "synthetic (Fourier-field Q/K, N(0,1) V and dO, Morton order; seeded)",
-           "config": {"workload": "vsa2_rep_c4_hunyuan", "batch": B, "heads": H, "seq_len": NB * 64,
+           "config": {"workload": "vsa2_rep_c4_hunyuan", "construction": args.c4, "split": tiers.split,
+                      "tables": tiers.tables, "batch": B, "heads": H, "seq_len": NB * 64,
                       "valid_tokens": Lr, "head_dim": D, "tier_pairs": {"A": na, "B": nbm, "C": ncm},
                       "columns_per_query_block": round(cols / (B * H * NB), 1)},
            "fwd_ms": round(fwd_ms, 3), "bwd_ms": round(step_ms - fwd_ms, 3), "route_tiers_ms": round(route_ms, 3),
+           "tables_ms_in_fwd": round(tables_ms, 3),
            "roofline": {"kernel": "rep_q_kernel<false> (three-tier forward)", "bound": "mfma",
                         "achieved": round(fl_fwd / (fwd_ev * 1e-3) / 1e12, 2), "peak": PEAK_BF16 / 1e12,
                         "unit": "TFLOP/s", "frac": round(fl_fwd / (fwd_ev * 1e-3) / PEAK_BF16, 4), "traffic": None,

@@ -431,7 +431,7 @@ def kmeans_seed_tokens(seed, bh, blk, n, RM):
     return perm[:min(RM, n)]
 
 
-def kmeans_tables(k, v, blk_cnt, RM, iters=5, seed=0, rnd=round_bf16):
+def kmeans_tables(k, v, blk_cnt, RM, iters=5, seed=0, rnd=round_bf16, bh0=0, blk0=0):
     """Seeded Lloyd k-means of every block's valid keys into RM clusters: (k_mid, v_mid [B, H, NB * RM, D] rnd-ed
     cluster means (zero rows for empty clusters), lc_mid [B, H, NB * RM] log2 counts (-inf when empty), counts
     [B, H, NB * RM] int, labels [B, H, L] int (-1 on padding)).
@@ -440,7 +440,8 @@ def kmeans_tables(k, v, blk_cnt, RM, iters=5, seed=0, rnd=round_bf16):
     assigns every valid token to its nearest centroid (squared distance summed over the D columns in order,
     float32, each difference squared then added; ties to the smaller cluster) and moves every non-empty cluster's
     centroid to the float32 mean of its members' keys (summed in token order, then one division). The tables hold
-    the last round's centroids and the mean values of the same clusters."""
+    the last round's centroids and the mean values of the same clusters. bh0 / blk0: the (b, h) and block index of
+    the first given head / block (the seeds depend on them), to check samples of a larger tensor."""
     k, v = np.asarray(k, np.float32), np.asarray(v, np.float32)
     B, H, L, D = k.shape
     NB = L // BLOCK
@@ -451,11 +452,11 @@ def kmeans_tables(k, v, blk_cnt, RM, iters=5, seed=0, rnd=round_bf16):
     labels = np.full((B, H, L), -1, np.int64)
     for b in range(B):
         for h in range(H):
-            bh = b * H + h
+            bh = bh0 + b * H + h
             for blk in range(NB):
                 n = int(cnt[blk])
                 x = k[b, h, blk * BLOCK:blk * BLOCK + n]
-                seeds = kmeans_seed_tokens(seed, bh, blk, n, RM)
+                seeds = kmeans_seed_tokens(seed, bh, blk0 + blk, n, RM)
                 cent = np.zeros((RM, D), np.float32)
                 cent[:len(seeds)] = x[seeds]
                 live = np.arange(RM) < len(seeds)

@@ -1,6 +1,8 @@
 """VSA2 three tiers (64 / 4 / 1) at the full C4 HunyuanVideo shape (B = 2, H = 24, 33 x 45 x 80 grid = 118 800
 tokens in 1857 blocks, a 16-token tail block, D = 128; tiers 5 % full, 20 % as 4 representatives, the rest block
-means; the benchmark's inputs): the forward output, LSE and dQ of sampled query blocks against a float64
+means; the benchmark's inputs), in both constructions: the reference's (two global budgets, contiguous group
+means) and BASELINE config 4's (per-query-block tiers, seeded 5-round k-means tables; sampled table blocks equal
+the oracle's bit for bit). Checked: the forward output, LSE and dQ of sampled query blocks against a float64
 restatement of one softmax over the block's tier-A tokens, tier-B representatives (+ ln of the group size) and
 tier-C block means (+ ln of the block count; dQ with delta = rowsum(dO * O) of the stored bf16 O, the quantity the
 backward consumes), with the kernels' own bf16 tables (`vsa_rep_build`, bit-exact at
@@ -27,7 +29,8 @@ def log(*a):
     sys.stdout.flush()
 
 
-def test_three_tiers_full_c4_shape(dev):
+@pytest.mark.parametrize("construction", ["reference", "baseline"])
+def test_three_tiers_full_c4_shape(dev, construction):
     from self_trainable_or_free_attn_amd import synthetic
     from self_trainable_or_free_attn_amd.vsa import _C, rep
     log("C4 full shape: inputs")
@@ -43,22 +46,40 @@ def test_three_tiers_full_c4_shape(dev):
     blk[-1] = Lr - 64 * (NB - 1)
     g = torch.Generator(device=dev).manual_seed(5)
     dout = torch.randn(q.shape, device=dev, generator=g).to(torch.bfloat16)
-    tiers = rep.RepTiers(frac_full=0.05, frac_mid=0.20, mid_reps=RM)
+    kmeans = construction == "baseline"
+    tiers = rep.RepTiers(frac_full=0.05, frac_mid=0.20, mid_reps=RM, split="per_row" if kmeans else "global",
+                         tables="kmeans" if kmeans else "contiguous", kmeans_iters=5, seed=4)
     sel = rep.route_tiers(q, k, blk, tiers, R=16)
-    log("C4 full shape: kernels")
+    log("C4 full shape:", construction, "kernels")
     qg = q.detach().clone().requires_grad_(True)
-    o, lse = rep.rep_fine_attention(qg, k, v, blk, sel, mid_reps=RM)
+    o, lse = rep.rep_fine_attention(qg, k, v, blk, sel, mid_reps=RM, tables=tiers.tables, kmeans_iters=5, seed=4)
     (dq,) = torch.autograd.grad(o, (qg,), dout)
-    k_mid, v_mid, _, k_tail, v_tail, _ = _C.rep_build(k, v, blk, RM)
+    cnt = blk.cpu().numpy().astype(np.int64)
+    if kmeans:
+        (k_mid, v_mid, _, k_tail, v_tail, _), counts, _ = _C.rep_build_kmeans(k, v, blk, RM, 5, 4)
+        ng_all = counts.cpu().numpy().reshape(B, H, NB, RM)                 # cluster sizes per (b, h)
+    else:
+        k_mid, v_mid, _, k_tail, v_tail, _ = _C.rep_build(k, v, blk, RM)
+        gs = 64 // RM
+        ng_all = np.broadcast_to(np.clip(cnt[:, None] - np.arange(RM)[None, :] * gs, 0, gs), (B, H, NB, RM))
     torch.cuda.synchronize()
     ma, mb, mc = (m.cpu().numpy() for m in sel.tier_masks(NB))
-    cnt = blk.cpu().numpy().astype(np.int64)
-    gs = 64 // RM
-    ng = np.clip(cnt[:, None] - np.arange(RM)[None, :] * gs, 0, gs)  # tokens per representative group
+    if kmeans:
+        ka, kab = tiers.row_budgets(NB)
+        assert (ma.sum(-1) == ka).all() and ((ma | mb).sum(-1) == kab).all()
     sc = 1.0 / math.sqrt(D)
     go, gl, gdq = f32(o), f32(lse), f32(dq)
     for b, h, i in SAMPLES:
         log("C4 full shape: oracle batch", b, "head", h, "block", i)
+        ng = ng_all[b, h]
+        if kmeans:   # the sampled block's k-means table rows against the oracle (same seed, same (b, h, block))
+            from oracle import vsa_ref
+            sl = slice(i * 64, i * 64 + 64)
+            wk, wv, _, wc, _ = vsa_ref.kmeans_tables(f32(k[b, h, sl])[None, None], f32(v[b, h, sl])[None, None],
+                                                     [int(cnt[i])], RM, 5, 4, bh0=b * H + h, blk0=i)
+            assert np.array_equal(ng[i], wc[0, 0])
+            assert np.array_equal(f32(k_mid[b, h, i * RM:(i + 1) * RM]), wk[0, 0])
+            assert np.array_equal(f32(v_mid[b, h, i * RM:(i + 1) * RM]), wv[0, 0])
         kh, vh = k[b, h].double().cpu().numpy(), v[b, h].double().cpu().numpy()
         kmid, vmid = k_mid[b, h].double().cpu().numpy(), v_mid[b, h].double().cpu().numpy()
         ktail, vtail = k_tail[b, h].double().cpu().numpy(), v_tail[b, h].double().cpu().numpy()
