@@ -55,6 +55,26 @@ def executed_flops(ps, D=128):
     return float(4 * 128 * D * cols)
 
 
+def _host_cpu():
+    """(CPU model string, BLAS threads numpy uses) of this host."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    threads = None
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max((i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"), default=None)
+    except Exception:
+        pass
+    return model, threads or 1
+
+
 def cpu_baseline(q, k, v, attn, seconds):
     """The numpy oracle's fixed-offset sparse step on a bounded sample of (tile, head) pairs (head 0, first tiles),
     timed on this host; returned as TFLOP/s on executed blocks, like `value`."""
@@ -84,8 +104,9 @@ def cpu_baseline(q, k, v, attn, seconds):
         tiles = min(counts.shape[0], max(tiles + 1, int(tiles * seconds / max(elapsed, 1e-3) * 1.05)))
     cols = (64 * counts[:tiles].sum() + comp["mean_counts"][:tiles].sum() + 4 * comp["refine_counts"][:tiles].sum())
     flops = 4 * 128 * 128 * float(cols)
-    return {"value": flops / elapsed / 1e12, "unit": "TFLOP/s (executed blocks)", "cores": os.cpu_count(),
-            "kind": "port", "sample": f"numpy oracle fixed-offset sparse step (exact + mean + representative "
+    model, threads = _host_cpu()
+    return {"value": flops / elapsed / 1e12, "unit": "TFLOP/s (executed blocks)", "cores": threads,
+            "cpu_model": model, "kind": "port", "sample": f"numpy oracle fixed-offset sparse step (exact + mean + representative "
             f"columns), head 0, query tiles 0..{tiles - 1} of {counts.shape[0]}, one branch; {elapsed:.1f} s",
             "ms_per_layer_extrapolated": elapsed / tiles * counts.shape[0] * q.shape[1] * 2 * 1e3}
 
@@ -258,9 +279,9 @@ def _vsa_cpu_baseline(q, k, v, blk, sel, seconds):
     el = time.perf_counter() - t0
     flops = 4.0 * 64 * 64 * q.shape[-1] * cols
     return {"value": round(flops / el / 1e12, 5), "unit": "TFLOP/s (fine forward, executed blocks)",
-            "cores": 1, "kind": "port",
+            "cores": _host_cpu()[1], "cpu_model": _host_cpu()[0], "kind": "port",
             "sample": f"blockwise numpy port of the fine forward (oracle/vsa_ref.py fine_attention_blocks), head 0, "
-                      f"query blocks 0..{done - 1} of {nb}, {cols} block pairs, {el:.1f} s, one thread"}
+                      f"query blocks 0..{done - 1} of {nb}, {cols} block pairs, {el:.1f} s, numpy's BLAS threads"}
 
 
 def run_vsa_workload(args):
