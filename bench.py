@@ -42,6 +42,11 @@ def parse():
     ap.add_argument("--c4", default="baseline", choices=["baseline", "reference"],
                     help="vsa2_rep tier construction: BASELINE config 4's (per-query-block tiers, seeded 5-round "
                          "k-means tables) or the reference's (global budgets, contiguous group means)")
+    ap.add_argument("--split-policy", default="manual", choices=["manual", "auto"],
+                    help="split workload: SplitKV(chunk=64) (every list over 64 blocks) or SplitKV.auto()")
+    ap.add_argument("--split-case", default="zipf", choices=["zipf", "hot"],
+                    help="split workload lists: C5's Zipf(1.2) lengths, or 'hot' (H=8, 16 rows per head "
+                         "select every block, the other rows 8 blocks)")
     ap.add_argument("--workload", default="echosparse", choices=["echosparse", "vsa", "vsa2_rep", "split"],
                     help="echosparse: the headline sparse step (default); vsa / vsa2_rep / split: the VSA "
                          "configurations (fine fwd+bwd at 30720 tokens, three-tier at the HunyuanVideo shape, "
@@ -293,8 +298,10 @@ def run_vsa_workload(args):
     if args.workload in ("vsa", "split"):
         if args.workload == "vsa":   # C2: B1 H24 N30720, top-60 by the original-VSA router, N(0, 1) seed 1
             B, H, NB = 1, 24, 480
-        else:                        # C5: B1 H40 L75648, Zipf(1.2) lists clipped to [8, 512], seed 4
+        elif args.split_case == "zipf":  # C5: B1 H40 L75648, Zipf(1.2) lists clipped to [8, 512], seed 4
             B, H, NB = 1, 40, 1182
+        else:                        # hot rows: a few lists hold most of the work
+            B, H, NB = 1, 8, 1182
         g = torch.Generator(device=dev).manual_seed(1 if args.workload == "vsa" else 4)
         q, k, v, dout = (torch.randn(B, H, NB * 64, D, device=dev, generator=g).to(torch.bfloat16) for _ in range(4))
         blk = torch.full((NB,), 64, dtype=torch.int32, device=dev)
@@ -304,7 +311,11 @@ def run_vsa_workload(args):
             import numpy as np
             rng = np.random.default_rng(4)
             mask = np.zeros((B, H, NB, NB), bool)
-            n = np.clip(rng.zipf(1.2, size=(B, H, NB)), 8, 512)
+            if args.split_case == "zipf":
+                n = np.clip(rng.zipf(1.2, size=(B, H, NB)), 8, 512)
+            else:
+                n = np.full((B, H, NB), 8)
+                n[:, :, rng.choice(NB, size=16, replace=False)] = NB
             for h in range(H):
                 for i in range(NB):
                     mask[0, h, i, rng.choice(NB, size=int(n[0, h, i]), replace=False)] = True
@@ -312,7 +323,9 @@ def run_vsa_workload(args):
         nnz = int((sel.q2k_ptr[..., -1] - sel.q2k_ptr[..., 0]).sum())
         qg, kg, vg = (x.detach().clone().requires_grad_(True) for x in (q, k, v))
         # C5: the manual policy (every list longer than 64 blocks runs as balanced 64-block chunks + ordered merge)
-        split = ops.SplitKV(chunk=64) if args.workload == "split" else None
+        split = None
+        if args.workload == "split":
+            split = ops.SplitKV.auto() if args.split_policy == "auto" else ops.SplitKV(chunk=64)
 
         def fwd():
             return ops.fine_block_sparse_attention(qg, kg, vg, blk, sel, split_kv=split)
@@ -331,9 +344,11 @@ def run_vsa_workload(args):
                "unit": "TFLOP/s (executed blocks, fine fwd+bwd)", "n_gpus": 1, "steps": K, "warmup": W,
                "ms_per_step": round(step_ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
                "dtype": "bf16", "data": "synthetic (N(0,1) q/k/v/dO, seeded)",
-               "config": {"workload": "vsa_c2_fine_fwd_bwd" if args.workload == "vsa" else "vsa_c5_zipf_split",
+               "config": {"workload": "vsa_c2_fine_fwd_bwd" if args.workload == "vsa" else
+                          ("vsa_c5_zipf_split" if args.split_case == "zipf" else "vsa_hot_rows_split"),
                           "batch": B, "heads": H, "seq_len": NB * 64, "head_dim": D, "nnz_pairs": nnz,
-                          "split_kv": "manual chunk 64" if split else None},
+                          "split_kv": None if split is None else
+                          ("auto" if split.policy is not None else "manual chunk 64")},
                "fwd_ms": round(fwd_ms, 3), "bwd_ms": round(step_ms - fwd_ms, 3),
                "fwd_tflops": round(fl_fwd / (fwd_ms * 1e-3) / 1e12, 2),
                "roofline": {"kernel": "vsa_fwd_kernel (fine forward)", "bound": "mfma",
@@ -345,7 +360,8 @@ def run_vsa_workload(args):
                 ops.fine_block_sparse_attention(qg, kg, vg, blk, sel)[0], (qg, kg, vg), dout), K, W)
             res["unsplit_ms_per_step"] = round(unsplit_ms, 3)
             res["split_speedup"] = round(unsplit_ms / step_ms, 3)
-            res["split_plan"] = ops.describe_split(qg, sel, split)["fwd"]["info"]
+            plan = ops.describe_split(qg, sel, split)
+            res["split_plan"] = {d: plan[d]["info"] for d in plan}
         if not args.no_cpu:
             res["cpu_baseline"] = _vsa_cpu_baseline(q, k, v, blk, sel, args.cpu_seconds)
         print(json.dumps(res), flush=True)

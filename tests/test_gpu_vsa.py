@@ -337,6 +337,25 @@ def test_split_fine_equals_unsplit(qkv, policy):
         check_close(name + " split vs oracle", f32(a), w)
 
 
+def test_split_auto_declines_to_the_direct_kernels(qkv):
+    """SplitKV.auto() on a selection where the policy splits nothing runs the direct (unsplit) kernels: outputs and
+    gradients are bytes-identical to the unsplit call."""
+    log("split auto declines")
+    from self_trainable_or_free_attn_amd.vsa import ops
+    q, k, v = (x.detach().clone().requires_grad_(True) for x in qkv["gpu"])
+    sel = selection_of(random_mask(5, density=0.5), q.device)
+    split = ops.SplitKV.auto()
+    assert all(r["info"]["split_rows"] == 0 for r in ops.describe_split(q, sel, split).values())
+    dout_c, dout = tokens(32, q.device)
+    o1, l1 = ops.fine_block_sparse_attention(q, k, v, qkv["blk"], sel)
+    g1 = torch.autograd.grad(o1, (q, k, v), dout)
+    o2, l2 = ops.fine_block_sparse_attention(q, k, v, qkv["blk"], sel, split_kv=split)
+    g2 = torch.autograd.grad(o2, (q, k, v), dout)
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+
+
 # --------------------------------------------------------------------------- fusion and operators
 @pytest.mark.parametrize("gate_kind,act", [(None, 0), ("token", 0), ("elem", 1)])
 def test_fuse_forward_backward(qkv, gate_kind, act):
