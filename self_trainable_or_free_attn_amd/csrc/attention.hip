@@ -24,6 +24,8 @@ namespace es {
 
 enum { FIXED = 0, ONLINE = 1, COMPENSATE = 2 };
 
+constexpr float ONLINE_SLACK = 8.0f;  // log2 growth of a row's maximum that triggers a rescale (ONLINE)
+
 
 
 struct AttnArgs {
@@ -255,6 +257,7 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
   for (int db = 0; db < 4; ++db) o[db] = f32x16{};
   float lsum = 0.0f;        // this lane's share of the row sum (its 32 keys of every chunk)
   float mrun = -INFINITY;   // ONLINE running max (same in both half-waves)
+  bool online_biased = true;  // ONLINE: the chunk has masked columns (the tail block)
 
   // exponentials of one 32-key half (C tile sh of the chunk) packed into two B operands of O^T += V^T P^T;
   // returns this lane's share of the half's sum. FIXED / COMPENSATE only (fixed offset, no running max).
@@ -278,6 +281,44 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
     pb = pack8(&p[8]);
     return sum8_bf16(pb, sum8_bf16(pa, 0.0f));
   };
+  // ONLINE: the same for a running maximum that is raised only when a half's maximum exceeds it by more than
+  // 2^ONLINE_SLACK (then O and the row sum are rescaled first); otherwise the exponentials use the stale maximum,
+  // so p <= 2^ONLINE_SLACK and most halves skip the rescale. The result is the same softmax: the final O / sum
+  // and LSE = max + log2(sum) do not depend on which maximum the terms were taken against.
+  // (the half's row sum goes straight into lsum: a later half's rescale must scale it too)
+  // (one instantiation for both chunk kinds, within 256 VGPRs: `biased` is a wave-uniform run-time flag)
+  auto half_online = [&](const f32x16& sh, int boff, bf16x8& pa, bf16x8& pb, bool biased) {
+    float p[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = fmaf(sh[r], scale, nprior);
+    if (biased) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bias_s[0][0] + boff + 8 * i + 4 * hi);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) p[4 * i + jj] += b4[jj];
+      }
+    }
+    float mh = p[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mh = fmaxf(mh, p[r]);
+    mh = fmaxf(mh, __shfl_xor(mh, 32, 64));
+    if (mh > mrun + ONLINE_SLACK) {
+      const float alpha = exp2f_fast(mrun - mh);
+      lsum *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      mrun = mh;
+    }
+    const float msub = mrun == -INFINITY ? 0.0f : mrun;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = exp2f_fast(p[r] - msub);
+    pa = pack8(&p[0]);
+    pb = pack8(&p[8]);
+    lsum += sum8_bf16(pb, sum8_bf16(pa, 0.0f));
+  };
   auto pv = [&](const char* vb, int kk, const bf16x8& pk) {
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
@@ -287,9 +328,8 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
     }
   };
 
-  // one chunk. FIXED / COMPENSATE: two 32-key halves, so the matrix cores compute S^T of the second half while
-  // the VALU exponentiates the first, and O^T += V^T P^T of the first half while the VALU does the second.
-  // ONLINE: the running maximum needs all 64 keys first.
+  // one chunk as two 32-key halves, so the matrix cores compute S^T of the second half while the VALU
+  // exponentiates the first, and O^T += V^T P^T of the first half while the VALU does the second.
   auto compute = [&](int j, int sb, auto biased_tag) {
     const char* kb = kv_s[sb][0];
     const char* vb = kv_s[sb][1];
@@ -317,39 +357,13 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
       }
       return;
     }
-    float p[32];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bias_s[sb][8 * i + 4 * hi]);
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-        p[4 * i + jj] = fmaf(i < 4 ? s0[4 * i + jj] : s1[4 * (i - 4) + jj], scale, b4[jj]) + nprior;
-    }
-    // nprior is 0 in ONLINE mode: p holds the scaled logits here
-    float mx = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < 32; ++r) mx = fmaxf(mx, p[r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(mrun, mx);
-    const float msub = mnew == -INFINITY ? 0.0f : mnew;
-    const float alpha = exp2f_fast(mrun - msub);
-#pragma unroll
-    for (int r = 0; r < 32; ++r) p[r] = exp2f_fast(p[r] - msub);
-    lsum *= alpha;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-    mrun = mnew;
-    bf16x8 pk[4];
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) pk[kk] = pack8(&p[kk * 8]);
-    float csum = 0.0f;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) csum = sum8_bf16(pk[kk], csum);
-    lsum += csum;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) pv(vb, kk, pk[kk]);
+    bf16x8 pk0, pk1, pk2, pk3;
+    half_online(s0, sb * BK, pk0, pk1, online_biased);
+    pv(vb, 0, pk0);
+    pv(vb, 1, pk1);
+    half_online(s1, sb * BK + 32, pk2, pk3, online_biased);
+    pv(vb, 2, pk2);
+    pv(vb, 3, pk3);
   };
 
   stage_ids(0);
@@ -393,6 +407,7 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
     stage_ids(j + 3);
     pre_v = (j + 2 < n && g_ex != nullptr) ? ids_s[(j + 2) & 3][0] : j + 2;
     const bool biased = MODE == COMPENSATE || j >= n || (tail_block && cur_row == nb - 1);
+    online_biased = biased;
     if (!COMP || biased)   // (non-COMP variants: one instantiation keeps them within 256 VGPRs)
       compute(j, sb, std::true_type{});
     else
