@@ -10,7 +10,9 @@
  *                                    64-token blocks
  *   D (every entry point)            the logical head dim, 64 or 128: rows are always 128 columns wide and a
  *                                    D = 64 caller zero-fills columns 64..127 (they add exact zeros to every dot
- *                                    product and come out zero); D sets the softmax scale 1 / sqrt(D)
+ *                                    product and come out zero); D sets the softmax scale 1 / sqrt(D). The fine
+ *                                    attention entry points (vsa_attn_*) run a D = 64 kernel variant that reads
+ *                                    and computes on the first 64 columns only
  *   blk_cnt                          [NB] int32, valid tokens per block (1..64)
  *   router pools qr, kr, vr          [BH, Lr_pad, 128] bf16, Lr_pad = ceil64(NB * 64 / R)
  *   block means qc, kc, vc           [BH, NBc_pad, 128] bf16, NBc_pad = ceil64(NB)

@@ -1,6 +1,9 @@
 // VSA fine block-sparse attention over a CSR block selection (gfx950, bf16 MFMA 32x32x16).
 //
-// Tokens are [BH, L, D] bf16 (D = 128), L = NB * 64 in 64-token blocks; blk_cnt[NB] gives each block's valid
+// Tokens are [BH, L, 128] bf16 rows, L = NB * 64 in 64-token blocks. Every kernel is instantiated for the logical
+// head dim DH = 128 and DH = 64: at DH = 64 (columns 64..127 zero by contract) it stages only the first 128 bytes
+// of each row, runs half the QK^T k-steps and half the 32-column output blocks, and writes zeros past column 64
+// (C2 shape at D = 64: forward 2.21 -> 1.76 ms, forward + backward 10.2 -> 7.6 ms). blk_cnt[NB] gives each block's valid
 // tokens (valid-first). Query block i of head bh attends to the kv blocks row_ptr / col_idx list for row
 // (bh, i), with key columns >= blk_cnt[kv] masked; query rows >= blk_cnt[i] and rows with an empty list get
 // O = 0 and lse = -inf. lse is the natural-log row sum. Semantics: reference csrc/vsa/generic/attn_fwd.cu:16-24,
@@ -41,8 +44,9 @@ struct VsaFwdArgs {
 
 // (This kernel stages K / V with the compiler-visible transfer, buf2lds16: measured ~6% faster here than the
 // inline-assembly dma16 the other kernels use.)
-template <bool TASKS>
+template <bool TASKS, int DH>
 __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
+  constexpr int NKS = DH / 16, NDB = DH / 32;  // MFMA k-steps of QK^T, 32-column blocks of O (D = 64: the first half)
   __shared__ __attribute__((aligned(16))) char kv_s[2][2][BK * 256];
 
   int qb, bh, beg, end, slot = -1;
@@ -80,8 +84,8 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
   unsigned ld_off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int P = (wv * 4 + i) * 64 + l, R = P >> 4;
-    ld_off[i] = (unsigned)R * 256 + (unsigned)(((P & 15) ^ swz(R)) * 16);
+    const int P = (wv * 4 + i) * 64 + l, R = P >> 4, g = (P & 15) ^ swz(R);
+    ld_off[i] = g < DH / 8 ? (unsigned)R * 256 + (unsigned)(g * 16) : 0x80000000u;
   }
   auto issue = [&](int b, int sb) {
     const unsigned soff = (unsigned)b * (BK * 256);
@@ -98,7 +102,7 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
   {
     const e16_t* qp = a.q + (head + (size_t)qb * BK + qrow) * HD;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qreg[ks] = *reinterpret_cast<const ev8*>(qp + 16 * ks + 8 * hi);
+    for (int ks = 0; ks < NKS; ++ks) qreg[ks] = *reinterpret_cast<const ev8*>(qp + 16 * ks + 8 * hi);
   }
   int koff[8];
 #pragma unroll
@@ -138,7 +142,7 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
     const char* vb = kv_s[sb][1] + kh * 8192;
     f32x16 s = {};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) s = emfma(elds16(kb, koff[ks]), qreg[ks], s);
+    for (int ks = 0; ks < NKS; ++ks) s = emfma(elds16(kb, koff[ks]), qreg[ks], s);
     float p[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) p[r] = s[r] * scale;
@@ -167,7 +171,7 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
     const ev8 pa = epack8(&p[0]), pb = epack8(&p[8]);
     lsum += esum8(pb, esum8(pa, 0.0f));
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+    for (int db = 0; db < NDB; ++db) {
       o[db] = emfma(ecat_tr(lds_read_tr(vb, voff[0][db]), lds_read_tr(vb, voff[1][db])), pa, o[db]);
       o[db] = emfma(ecat_tr(lds_read_tr(vb + 4096, voff[0][db]), lds_read_tr(vb + 4096, voff[1][db])), pb, o[db]);
     }
@@ -184,7 +188,7 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
   const float ltot = lsum + __shfl_xor(lsum, 32, 64);
   if (kh == 1) {
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int r = 0; r < 16; ++r) xo[(db * 16 + r) * 64 + l] = o[db][r];
     xm[l] = mref;
@@ -208,10 +212,13 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         ushort4 v4;
-        v4.x = f2e((a0 * o[db][4 * i + 0] + a1 * xo[(db * 16 + 4 * i + 0) * 64 + l]) * inv);
-        v4.y = f2e((a0 * o[db][4 * i + 1] + a1 * xo[(db * 16 + 4 * i + 1) * 64 + l]) * inv);
-        v4.z = f2e((a0 * o[db][4 * i + 2] + a1 * xo[(db * 16 + 4 * i + 2) * 64 + l]) * inv);
-        v4.w = f2e((a0 * o[db][4 * i + 3] + a1 * xo[(db * 16 + 4 * i + 3) * 64 + l]) * inv);
+        v4 = ushort4{0, 0, 0, 0};
+        if (db < NDB) {
+          v4.x = f2e((a0 * o[db][4 * i + 0] + a1 * xo[(db * 16 + 4 * i + 0) * 64 + l]) * inv);
+          v4.y = f2e((a0 * o[db][4 * i + 1] + a1 * xo[(db * 16 + 4 * i + 1) * 64 + l]) * inv);
+          v4.z = f2e((a0 * o[db][4 * i + 2] + a1 * xo[(db * 16 + 4 * i + 2) * 64 + l]) * inv);
+          v4.w = f2e((a0 * o[db][4 * i + 3] + a1 * xo[(db * 16 + 4 * i + 3) * 64 + l]) * inv);
+        }
         *reinterpret_cast<ushort4*>(orow + 32 * db + 8 * i + 4 * hi) = v4;
       }
     if (hi == 0) a.lse[tok] = live ? lse2 * LN2 : -INFINITY;
@@ -221,11 +228,13 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float4 v4;
-        v4.x = (a0 * o[db][4 * i + 0] + a1 * xo[(db * 16 + 4 * i + 0) * 64 + l]) * inv;
-        v4.y = (a0 * o[db][4 * i + 1] + a1 * xo[(db * 16 + 4 * i + 1) * 64 + l]) * inv;
-        v4.z = (a0 * o[db][4 * i + 2] + a1 * xo[(db * 16 + 4 * i + 2) * 64 + l]) * inv;
-        v4.w = (a0 * o[db][4 * i + 3] + a1 * xo[(db * 16 + 4 * i + 3) * 64 + l]) * inv;
+        float4 v4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (db < NDB) {
+          v4.x = (a0 * o[db][4 * i + 0] + a1 * xo[(db * 16 + 4 * i + 0) * 64 + l]) * inv;
+          v4.y = (a0 * o[db][4 * i + 1] + a1 * xo[(db * 16 + 4 * i + 1) * 64 + l]) * inv;
+          v4.z = (a0 * o[db][4 * i + 2] + a1 * xo[(db * 16 + 4 * i + 2) * 64 + l]) * inv;
+          v4.w = (a0 * o[db][4 * i + 3] + a1 * xo[(db * 16 + 4 * i + 3) * 64 + l]) * inv;
+        }
         *reinterpret_cast<float4*>(prow + 32 * db + 8 * i + 4 * hi) = v4;
       }
     if (hi == 0) a.part_lse[(size_t)slot * BK + qrow] = lse2;
@@ -291,8 +300,9 @@ __device__ __forceinline__ float lse_to_log2(float lse) { return lse == -INFINIT
 // The KV-owner backward as two passes with half the accumulators each, so that two waves share a SIMD:
 // PART 1 = dV (S, P, dV += P^T dO), PART 2 = dK (S, dP = dO V^T with V in registers, dK += dS^T Q). S is computed
 // in both (5 products per pair instead of 4).
-template <bool TASKS, int PART>
+template <bool TASKS, int PART, int DH>
 __global__ __launch_bounds__(256, 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
+  constexpr int NKS = DH / 16, NDB = DH / 32;
   __shared__ __attribute__((aligned(16))) char qd_s[2][2][BK * 256];  // [buffer][Q | dO]
   __shared__ __attribute__((aligned(16))) float st_s[2][2][BK];       // [buffer][lse2 (+inf: P = 0) | delta]
   int kb, bh, beg, end, slot;
@@ -312,14 +322,14 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
   unsigned ld_off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int P = (wv * 4 + i) * 64 + l, R = P >> 4;
-    ld_off[i] = (unsigned)R * 256 + (unsigned)(((P & 15) ^ swz(R)) * 16);
+    const int P = (wv * 4 + i) * 64 + l, R = P >> 4, g = (P & 15) ^ swz(R);
+    ld_off[i] = g < DH / 8 ? (unsigned)R * 256 + (unsigned)(g * 16) : 0x80000000u;
   }
   ev8 kreg[8], vreg[8];
   {
     const size_t off = (head + (size_t)kb * BK + key) * HD + 8 * hi;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
+    for (int ks = 0; ks < NKS; ++ks) {
       kreg[ks] = *reinterpret_cast<const ev8*>(a.k + off + 16 * ks);
       if (PART == 2) vreg[ks] = *reinterpret_cast<const ev8*>(a.v + off + 16 * ks);
     }
@@ -382,9 +392,9 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
     const char* dt = qd_s[sb][1];
     f32x16 s = {}, dp = {};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) s = emfma(elds16(qt, aoff[ks]), kreg[ks], s);
+    for (int ks = 0; ks < NKS; ++ks) s = emfma(elds16(qt, aoff[ks]), kreg[ks], s);
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
+    for (int ks = 0; ks < NKS; ++ks)
       if (PART == 2) dp = emfma(elds16(dt, aoff[ks]), vreg[ks], dp);
     float p[16], ds[16];
 #pragma unroll
@@ -401,7 +411,7 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
     const ev8 pa = epack8(&p[0]), pb = epack8(&p[8]);
     const ev8 sa = epack8(&ds[0]), sb8 = epack8(&ds[8]);
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+    for (int db = 0; db < NDB; ++db) {
       if (PART == 1) {
         dv[db] = emfma(ecat_tr(lds_read_tr(dt, toff[0][db]), lds_read_tr(dt, toff[1][db])), pa, dv[db]);
         dv[db] = emfma(ecat_tr(lds_read_tr(dt + 4096, toff[0][db]), lds_read_tr(dt + 4096, toff[1][db])), pb, dv[db]);
@@ -424,16 +434,18 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
   float* xa = reinterpret_cast<float*>(&qd_s[0][0][0]) + kh * (64 * 64);
   if (qh == 1) {
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int r = 0; r < 16; ++r) xa[(db * 16 + r) * 64 + l] = acc[db][r];
   }
   __syncthreads();
   if (qh == 1) return;
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
+  for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[db][r] += xa[(db * 16 + r) * 64 + l];
+#pragma unroll
+  for (int db = NDB; db < 4; ++db) acc[db] = f32x16{};  // columns past D: zero
   const size_t tok = head + (size_t)kb * BK + key;
   if (TASKS && slot >= 0) {
     float* pa_out = (PART == 1 ? a.part_b : a.part_a) + ((size_t)slot * BK + key) * HD;
@@ -472,8 +484,9 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
 }
 
 
-template <bool TASKS>
+template <bool TASKS, int DH>
 __global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
+  constexpr int NKS = DH / 16, NDB = DH / 32;
   __shared__ __attribute__((aligned(16))) char kv_s[2][2][BK * 256];
   int qb, bh, beg, end, slot;
   if (!owner_of<TASKS>(a, qb, bh, beg, end, slot)) return;
@@ -489,7 +502,7 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
 
   ev8 qreg[8], dreg[8];
 #pragma unroll
-  for (int ks = 0; ks < 8; ++ks) {
+  for (int ks = 0; ks < NKS; ++ks) {
     qreg[ks] = *reinterpret_cast<const ev8*>(a.q + tok * HD + 16 * ks + 8 * hi);
     dreg[ks] = *reinterpret_cast<const ev8*>(a.dout + tok * HD + 16 * ks + 8 * hi);
   }
@@ -502,8 +515,8 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
   unsigned ld_off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int P = (wv * 4 + i) * 64 + l, R = P >> 4;
-    ld_off[i] = (unsigned)R * 256 + (unsigned)(((P & 15) ^ swz(R)) * 16);
+    const int P = (wv * 4 + i) * 64 + l, R = P >> 4, g = (P & 15) ^ swz(R);
+    ld_off[i] = g < DH / 8 ? (unsigned)R * 256 + (unsigned)(g * 16) : 0x80000000u;
   }
   auto issue = [&](int b, int sb) {
     const unsigned soff = (unsigned)b * (BK * 256);
@@ -547,9 +560,9 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
     const char* vt = kv_s[sb][1];
     f32x16 s = {}, dp = {};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) s = emfma(elds16(kt, koff[ks]), qreg[ks], s);
+    for (int ks = 0; ks < NKS; ++ks) s = emfma(elds16(kt, koff[ks]), qreg[ks], s);
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) dp = emfma(elds16(vt, koff[ks]), dreg[ks], dp);
+    for (int ks = 0; ks < NKS; ++ks) dp = emfma(elds16(vt, koff[ks]), dreg[ks], dp);
     float ds[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -559,7 +572,7 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
     }
     const ev8 sa = epack8(&ds[0]), sb8 = epack8(&ds[8]);
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+    for (int db = 0; db < NDB; ++db) {
       dq[db] = emfma(ecat_tr(lds_read_tr(kt, toff[0][db]), lds_read_tr(kt, toff[1][db])), sa, dq[db]);
       dq[db] = emfma(ecat_tr(lds_read_tr(kt + 4096, toff[0][db]), lds_read_tr(kt + 4096, toff[1][db])), sb8, dq[db]);
     }
@@ -573,16 +586,18 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_q_kernel(VsaBwdArgs a) {
   float* xq = reinterpret_cast<float*>(&kv_s[0][0][0]) + rg * (64 * 64);
   if (kh == 1) {
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int r = 0; r < 16; ++r) xq[(db * 16 + r) * 64 + l] = dq[db][r];
   }
   __syncthreads();
   if (kh == 1) return;
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
+  for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[db][r] += xq[(db * 16 + r) * 64 + l];
+#pragma unroll
+  for (int db = NDB; db < 4; ++db) dq[db] = f32x16{};  // columns past D: zero
   if (TASKS && slot >= 0) {
     float* pq = a.part_a + ((size_t)slot * BK + qrow) * HD;
 #pragma unroll
@@ -658,7 +673,8 @@ extern "C" int ES_VSA_API(vsa_attn_fwd)(const void* q, const void* k, const void
   ES_REQUIRE(balanced_launch(BH, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "VSA: row-block queues unavailable");
   a.queues = qs.counters;
   a.fixed = qs.fixed;
-  hipLaunchKernelGGL(vsa_fwd_kernel<false>, dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
+  if (D == 64) hipLaunchKernelGGL((vsa_fwd_kernel<false, 64>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((vsa_fwd_kernel<false, 128>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
   return check_launch("vsa_attn_fwd");
 }
 
@@ -679,7 +695,8 @@ extern "C" int ES_VSA_API(vsa_attn_fwd_tasks)(const void* q, const void* k, cons
   a.lse = lse;
   a.part_o = part_o;
   a.part_lse = part_lse;
-  hipLaunchKernelGGL(vsa_fwd_kernel<true>, dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
+  if (D == 64) hipLaunchKernelGGL((vsa_fwd_kernel<true, 64>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((vsa_fwd_kernel<true, 128>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
   return check_launch("vsa_attn_fwd_tasks");
 }
 
@@ -729,10 +746,12 @@ extern "C" int ES_VSA_API(vsa_attn_bwd_kv)(const void* q, const void* k, const v
   ES_REQUIRE(balanced_launch(BH, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "VSA: row-block queues unavailable");
   a.queues = qs.counters;
   a.fixed = qs.fixed;
-  hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 1>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
+  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 1, 64>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 1, 128>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
   ES_REQUIRE(balanced_launch(BH, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "VSA: row-block queues unavailable");
   a.queues = qs.counters;
-  hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 2>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
+  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 2, 64>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 2, 128>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
   return check_launch("vsa_attn_bwd_kv");
 }
 
@@ -756,8 +775,10 @@ extern "C" int ES_VSA_API(vsa_attn_bwd_kv_tasks)(const void* q, const void* k, c
   a.out_b = (e16_t*)dv;
   a.part_a = part_dk;
   a.part_b = part_dv;
-  hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<true, 1>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
-  hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<true, 2>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
+  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<true, 1, 64>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<true, 1, 128>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
+  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<true, 2, 64>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<true, 2, 128>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
   return check_launch("vsa_attn_bwd_kv_tasks");
 }
 
@@ -780,7 +801,8 @@ extern "C" int ES_VSA_API(vsa_attn_bwd_q)(const void* q, const void* k, const vo
   ES_REQUIRE(balanced_launch(BH, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "VSA: row-block queues unavailable");
   a.queues = qs.counters;
   a.fixed = qs.fixed;
-  hipLaunchKernelGGL(vsa_bwd_q_kernel<false>, dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
+  if (D == 64) hipLaunchKernelGGL((vsa_bwd_q_kernel<false, 64>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((vsa_bwd_q_kernel<false, 128>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
   return check_launch("vsa_attn_bwd_q");
 }
 
@@ -800,6 +822,7 @@ extern "C" int ES_VSA_API(vsa_attn_bwd_q_tasks)(const void* q, const void* k, co
   a.add_nb = add_nb;
   a.out_a = (e16_t*)dq;
   a.part_a = part_dq;
-  hipLaunchKernelGGL(vsa_bwd_q_kernel<true>, dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
+  if (D == 64) hipLaunchKernelGGL((vsa_bwd_q_kernel<true, 64>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((vsa_bwd_q_kernel<true, 128>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
   return check_launch("vsa_attn_bwd_q_tasks");
 }
