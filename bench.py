@@ -25,7 +25,7 @@ import torch
 PEAK_BF16 = 2.5e15
 # HBM-side bytes per es_sparse_attention launch at this workload: rocprofv3 FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0
 # (scale factors from a copy of known size), profiles/echosparse_sparse_attention_wan14b_traffic.md
-TRAFFIC_BYTES = 4.66e10
+TRAFFIC_BYTES = 4.59e10
 
 
 def parse():
