@@ -108,10 +108,14 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
 
   // Loads go through buffer resources (32-bit offsets; offsets past the end read as zero). Token tensors and the
   // mean table are row-strided by H * 256 bytes from this head's first row; representatives are contiguous rows.
+  // A token block gets a resource of its own based at its first row (64-bit address arithmetic), so q / k / v may
+  // exceed 4 GiB; its range ends after the last valid key row, so rows past Lk read as zero.
   const unsigned hstride = (unsigned)H * HD * 2;
-  const srd_t rk = make_srd(a.k + (size_t)h * HD, (unsigned)(((size_t)a.Lk * H - h) * HD * 2));
-  const srd_t rv = make_srd(a.v + (size_t)h * HD, (unsigned)(((size_t)a.Lk * H - h) * HD * 2));
-  srd_t rkm = rk, rvm = rv, rkr = rk, rvr = rv;
+  auto block_srd = [&](const bf16_t* x, int b0) -> srd_t {
+    const int rows = min(BK, a.Lk - b0);
+    return make_srd(x + ((size_t)b0 * H + h) * HD, (unsigned)(rows - 1) * hstride + HD * 2);
+  };
+  srd_t rkm = {}, rvm = {}, rkr = {}, rvr = {};
   if (COMP || MODE == COMPENSATE) {
     rkm = make_srd(a.k_mean + (size_t)h * HD, (unsigned)(((size_t)nb * H - h) * HD * 2));
     rvm = make_srd(a.v_mean + (size_t)h * HD, (unsigned)(((size_t)nb * H - h) * HD * 2));
@@ -186,12 +190,17 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
     if (MODE == COMPENSATE || cj < n) {
       // 64 consecutive rows: token block b (exact) or mean blocks 64 cj .. (compensation)
       const int b0 = MODE == COMPENSATE ? cj * BK : __builtin_amdgcn_readfirstlane(c.row[0]) * BK;
-      const unsigned soff = (unsigned)b0 * hstride;
-      d.rk = MODE == COMPENSATE ? rkm : rk;
-      d.rv = MODE == COMPENSATE ? rvm : rv;
+      if (MODE == COMPENSATE) {
+        d.rk = rkm;
+        d.rv = rvm;
+        d.soff = (unsigned)b0 * hstride;
+      } else {
+        d.rk = block_srd(a.k, b0);
+        d.rv = block_srd(a.v, b0);
+        d.soff = 0;
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) d.off[i] = tok_off[i];
-      d.soff = soff;
       if (wv == 0) {
         if (MODE == COMPENSATE) {
           const int b = b0 + l;
@@ -524,8 +533,8 @@ static int check_common(const void* q, const void* k, const void* v, int L, int 
   ES_REQUIRE(q && k && v, ES_ERR_INVALID, "q, k and v must be non-null");
   ES_REQUIRE(L > 0 && H > 0, ES_ERR_INVALID, "L and H must be positive");
   ES_REQUIRE(D == HD, ES_ERR_UNSUPPORTED, "head dimension must be 128");
-  ES_REQUIRE((size_t)L * H * D * 2 < (1ull << 31), ES_ERR_UNSUPPORTED,
-             "q / k / v larger than 2 GiB (32-bit buffer offsets)");
+  ES_REQUIRE((size_t)BK * H * D * 2 < (1ull << 31), ES_ERR_UNSUPPORTED, "too many heads (one token block's rows "
+             "must span under 2 GiB)");
   return ES_OK;
 }
 
@@ -658,7 +667,7 @@ extern "C" int es_dense_attention_kv(const void* q, const void* k, const void* v
   int st = check_common(q, k, v, Lq, H, D);
   if (st) return st;
   ES_REQUIRE(Lk > 0, ES_ERR_INVALID, "Lk must be positive");
-  ES_REQUIRE((size_t)Lk * H * D * 2 < (1ull << 31), ES_ERR_UNSUPPORTED, "k / v larger than 2 GiB (32-bit buffer offsets)");
+  ES_REQUIRE(Lk > 0, ES_ERR_INVALID, "Lk must be positive");
   ES_REQUIRE(out && lse2, ES_ERR_INVALID, "null tensor pointer");
   AttnArgs a = base_args(q, k, v, Lq, H);
   a.Lk = Lk;

@@ -456,3 +456,27 @@ def test_balanced_ring_waits_for_a_live_slot(data, plan, reps, dev):
     for o in got:
         for a, b in zip(o, want):
             assert torch.equal(a, b)
+
+
+def test_dense_attention_past_4_gib(dev):
+    """q / k / v of 4.3 GB each (L = 75 600, H = 224: row offsets past 2^32 bytes; the kernels base a buffer
+    resource at every token block, so no 32-bit offset spans the tensor): the last head's first and last (80-row)
+    query tiles against float64."""
+    Lb, Hb = 75600, 224
+    log("dense attention past 4 GiB: L", Lb, "H", Hb)
+    g = torch.Generator(device=dev).manual_seed(3)
+    qb, kb, vb = (torch.randn(Lb, Hb, D, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+    assert qb.numel() * 2 > 2 ** 32
+    out, lse = K().dense_attention(qb, kb, vb)
+    torch.cuda.synchronize()
+    h = Hb - 1
+    kh, vh = kb[:, h].double().cpu(), vb[:, h].double().cpu()
+    for r0, r1 in ((0, 128), (Lb - 80, Lb)):
+        qh = qb[r0:r1, h].double().cpu()
+        s = qh @ kh.T / math.sqrt(D)
+        want_l = torch.logsumexp(s, -1)
+        want_o = torch.softmax(s, -1) @ vh
+        check_close(f"O rows {r0}..{r1}", f32(out[r0:r1, h]), want_o.numpy())
+        check_close(f"LSE rows {r0}..{r1}", f32(lse[r0:r1, h]) / math.log2(math.e), want_l.numpy())
+    del qb, kb, vb, out, lse
+    torch.cuda.empty_cache()
