@@ -226,6 +226,18 @@ __global__ __launch_bounds__(256, 4) void kmeans_kernel(const bf16_t* __restrict
   const int j = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, hi = l >> 5, lq = l & 31;
   const int nvalid = min(L - j * BK, BK);
+  // the metric operands do not depend on the K tile: their loads are issued first, so that their latency
+  // overlaps the tile's staging instead of following it (the first half of them: registers)
+  const int tb = wv & 1, e0 = (wv >> 1) * 2, pb = wv & 1, tk = wv >> 1;
+  const bf16_t* mt = metric_t + (size_t)h * HD * HD;
+  bf16x8 mop[4][2];
+  {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int eb = 0; eb < 2; ++eb)
+        mop[ks][eb] = *reinterpret_cast<const bf16x8*>(mt + (size_t)(32 * (e0 + eb) + lq) * HD + 16 * ks + 8 * hi);
+  }
   stage_rows(k, j * BK, L, H, h, kt);
   wait_vmem();
   __syncthreads();
@@ -233,27 +245,20 @@ __global__ __launch_bounds__(256, 4) void kmeans_kernel(const bf16_t* __restrict
   // X = K Lchol: wave wv -> tokens 32 (wv & 1) .., channels 64 (wv >> 1) .. (two 32-wide C tiles); probe logits:
   // wave wv -> probes 32 (wv & 1) .., tokens 32 (wv >> 1) ..
   f32x16 ax[2] = {f32x16{}, f32x16{}}, ap = {};
-  {
-    const int tb = wv & 1, e0 = (wv >> 1) * 2;
-    const bf16_t* mt = metric_t + (size_t)h * HD * HD;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      const bf16x8 a = lds_read16(kt, tile_off(32 * tb + lq, 2 * ks + hi));
+  for (int ks = 0; ks < 8; ++ks) {
+    const bf16x8 a = lds_read16(kt, tile_off(32 * tb + lq, 2 * ks + hi));
 #pragma unroll
-      for (int eb = 0; eb < 2; ++eb) {
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(mt + (size_t)(32 * (e0 + eb) + lq) * HD + 16 * ks + 8 * hi);
-        ax[eb] = mfma32(a, b, ax[eb]);
-      }
-    }
-    const int pb = wv & 1, tk = wv >> 1;
-    const bf16_t* pr = probes + ((size_t)h * NPROBE + 32 * pb + lq) * HD;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(pr + 16 * ks + 8 * hi);
-      const bf16x8 b = lds_read16(kt, tile_off(32 * tk + lq, 2 * ks + hi));
-      ap = mfma32(a, b, ap);
-    }
+    for (int eb = 0; eb < 2; ++eb)
+      ax[eb] = mfma32(a, ks < 4 ? mop[ks & 3][eb]
+                                : *reinterpret_cast<const bf16x8*>(mt + (size_t)(32 * (e0 + eb) + lq) * HD + 16 * ks + 8 * hi),
+                      ax[eb]);
   }
+  const bf16_t* pr = probes + ((size_t)h * NPROBE + 32 * pb + lq) * HD;
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks)
+    ap = mfma32(*reinterpret_cast<const bf16x8*>(pr + 16 * ks + 8 * hi), lds_read16(kt, tile_off(32 * tk + lq, 2 * ks + hi)),
+                ap);
   __syncthreads();  // every wave is done with the K tile: region A takes the probe logits
   {
     const int pb = wv & 1, tk = wv >> 1;
@@ -305,21 +310,15 @@ __global__ __launch_bounds__(256, 4) void kmeans_kernel(const bf16_t* __restrict
 #pragma unroll
       for (int r = 0; r < 16; ++r) X[32 * tb + 8 * (r / 4) + 4 * hi + (r % 4)][32 * (e0 + eb) + lq] = ax[eb][r];
   }
-  // token weights, the initial labels (four contiguous 16-token groups), per-cluster weights
-  auto set_weights = [&](int lb) {  // wave 0, lane = token: aw and cw of the labels lb
+  // token weights and the initial labels (four contiguous 16-token groups); the per-cluster weights cw are
+  // summed by the centroid pass
+  auto set_weights = [&](int lb) {  // wave 0, lane = token: aw and lab of the labels lb
     const float w = wgt[l];
     f32x4 a4;
 #pragma unroll
     for (int c = 0; c < 4; ++c) a4[c] = lb == c ? w : 0.0f;
     aw[l] = a4;
     lab[l] = lb;
-    float s[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) s[c] = wave_sum_dpp(a4[c]);
-    if (l == 0) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) cw[c] = s[c];
-    }
   };
   if (wv == 0) {
     const float s = wpart[0][l] + wpart[1][l] + wpart[2][l] + wpart[3][l];
@@ -331,25 +330,38 @@ __global__ __launch_bounds__(256, 4) void kmeans_kernel(const bf16_t* __restrict
 #pragma unroll
   for (int i = 0; i < 32; ++i) xd[i] = X[l][32 * wv + i];
 
-  // weighted centroids of the current labels (threads 0..127, channel = tid); a cluster with zero weight keeps
-  // its previous centroid unless `init`; also the squared centroid norms (per wave, nnp)
+  // weighted centroids of the current labels and the cluster weights cw: thread (channel tid % 128, token half
+  // tid / 128) sums its 32 tokens, the second halves are added through LDS (`part`, free at this point); a cluster
+  // with zero weight keeps its previous centroid unless `init`; also the squared centroid norms (per wave, nnp).
+  // Every thread of the workgroup calls it (it holds a barrier).
   auto centroids = [&](bool init) {
-    if (tid >= HD) return;
-    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    const int ch = tid & (HD - 1), hh = tid >> 7;
+    float s[4] = {0.f, 0.f, 0.f, 0.f}, ws[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
-    for (int t = 0; t < BK; ++t) {
+    for (int t = 32 * hh; t < 32 * hh + 32; ++t) {
       const f32x4 a4 = aw[t];
-      const float x = X[t][tid];
+      const float x = X[t][ch];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) s[c] = fmaf(a4[c], x, s[c]);
+      for (int c = 0; c < 4; ++c) {
+        s[c] = fmaf(a4[c], x, s[c]);
+        ws[c] += a4[c];
+      }
     }
-    f32x4 c4 = init ? f32x4{} : cen[tid];
+    if (hh == 1) {
+      part[ch] = f32x4{s[0], s[1], s[2], s[3]};
+      part[HD + ch] = f32x4{ws[0], ws[1], ws[2], ws[3]};
+    }
+    __syncthreads();
+    if (hh == 1) return;
+    const f32x4 s1 = part[ch], w1 = part[HD + ch];
+    f32x4 c4 = init ? f32x4{} : cen[ch];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const float w = cw[c];
-      if (init || w > 0.0f) c4[c] = s[c] / fmaxf(w, 1e-6f);
+      const float w = ws[c] + w1[c];
+      if (init || w > 0.0f) c4[c] = (s[c] + s1[c]) / fmaxf(w, 1e-6f);
+      if (ch == 0) cw[c] = w;
     }
-    cen[tid] = c4;
+    cen[ch] = c4;
     float q[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) q[c] = wave_sum_dpp(c4[c] * c4[c]);
@@ -386,15 +398,16 @@ __global__ __launch_bounds__(256, 4) void kmeans_kernel(const bf16_t* __restrict
           best = c;
         }
       }
-      const int changed = wave_sum_i((l < nvalid) && best != lab[l]);
+      const int changed = __popcll(__builtin_amdgcn_ballot_w64((l < nvalid) && best != lab[l]));
       set_weights(best);
       if (l == 0) red_i[0] = changed;
     }
     __syncthreads();
-    const int total = red_i[0];
+    // converged, or the last round: the labels are final and the representatives are plain means over them, so
+    // the centroids of these labels are not needed
+    if (red_i[0] == 0 || it == iters - 1) break;
     centroids(false);
     __syncthreads();
-    if (total == 0) break;
   }
 
   // representatives: plain means of K and V over each cluster's valid tokens (both tiles in LDS, region A)
