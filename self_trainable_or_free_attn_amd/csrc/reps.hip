@@ -6,9 +6,10 @@
 //   chol_kernel    G = Gram * scale^2 / L + 1e-3 * mean(diag) * I; right-looking Cholesky in LDS with the pivot
 //                  clamped at trace/D * 1e-12; writes the factor transposed (metric_t[e][d] = Lchol[d][e]), bf16
 //   probe_kernel   64 probe queries: scale * mean of the valid q rows of block round(i * (nb - 1) / 63)
-//   kmeans_kernel  per (block, head): X = K Lchol (MFMA), probe softmax weights (MFMA + LDS), weighted Lloyd from
-//                  the four contiguous 16-token groups with early exit, plain K / V means per cluster and log2
-//                  cluster sizes (-inf if empty); optionally the block means
+//   kmeans_kernel  one wave per (block, head): probe softmax weights (MFMA), the token Gram matrix X X^T of
+//                  X = K Lchol (MFMA), weighted Lloyd on it from the four contiguous 16-token groups with early
+//                  exit, plain K / V means per cluster (MFMA over one-hot labels) and log2 cluster sizes (-inf if
+//                  empty); optionally the block means
 #include "../../include/echosparse_hip.h"
 #include "common.h"
 
@@ -18,7 +19,7 @@
 namespace es {
 
 constexpr int NPROBE = 64;
-constexpr int MAX_SPLITS = 16;
+constexpr int MAX_SPLITS = 48;
 
 struct RepWorkspace {
   float* gram;       // (H, S, D, D)
@@ -141,9 +142,10 @@ __global__ __launch_bounds__(256) void chol_kernel(const float* __restrict__ gra
   bf16_t* mt = metric_t + (size_t)h * HD * HD;
   // Register-resident right-looking factorisation: thread (cc = tid % 128, half = tid / 128) holds column cc at
   // rows 64 half .. 64 half + 63. Step j: the owners of column j publish it into column buffer j % 2 (16-byte
-  // LDS writes), one barrier, then every thread reads the pivot column with 16-byte broadcast reads and subtracts
-  // the rank-1 update from its own entries. (Two buffers: step j+1 writes the other one while step j's readers
-  // may still be reading.)
+  // LDS writes) with its rows above j as zeros, one barrier, then every thread reads the pivot column with 16-byte
+  // broadcast reads and subtracts the rank-1 update col * (col[cc] / pivot) from its own entries: the zeros leave
+  // the finished rows alone, and the columns left of j (already published) are never read again, so no entry
+  // needs a mask. (Two buffers: step j+1 writes the other one while step j's readers may still be reading.)
   const int cc = tid & (HD - 1), rb = 64 * (tid >> 7);
   float a[64];
 #pragma unroll
@@ -154,22 +156,23 @@ __global__ __launch_bounds__(256) void chol_kernel(const float* __restrict__ gra
     float* cb = colbuf + (j & 1) * HD;
     if (cc == j) {
 #pragma unroll
-      for (int q4 = 0; q4 < 16; ++q4)
-        *reinterpret_cast<f32x4*>(cb + rb + 4 * q4) = f32x4{a[4 * q4], a[4 * q4 + 1], a[4 * q4 + 2], a[4 * q4 + 3]};
+      for (int q4 = 0; q4 < 16; ++q4) {
+        f32x4 c4;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) c4[k] = rb + 4 * q4 + k >= j ? a[4 * q4 + k] : 0.0f;
+        *reinterpret_cast<f32x4*>(cb + rb + 4 * q4) = c4;
+      }
     }
     __syncthreads();
-    const float inv = 1.0f / sqrtf(fmaxf(cb[j], eps));
-    const float cv = cc >= j ? cb[cc] * inv : 0.0f;
-    if (tid < HD) mt[j * HD + tid] = f2bf(tid >= j ? cb[tid] * inv : 0.0f);  // metric_t[j][d] = Lchol[d][j]
+    const float piv = fmaxf(cb[j], eps);
+    const float inv = 1.0f / sqrtf(piv);
+    const float sc = cb[cc] / piv;
+    if (tid < HD) mt[j * HD + tid] = f2bf(cb[tid] * inv);  // metric_t[j][d] = Lchol[d][j] (zero above j)
 #pragma unroll
     for (int q4 = 0; q4 < 16; ++q4) {
       const f32x4 c4 = *reinterpret_cast<const f32x4*>(cb + rb + 4 * q4);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int r = rb + 4 * q4 + k;
-        const float cr = r >= j ? c4[k] * inv : 0.0f;
-        a[4 * q4 + k] = fmaf(-cr, cv, a[4 * q4 + k]);
-      }
+      for (int k = 0; k < 4; ++k) a[4 * q4 + k] = fmaf(-c4[k], sc, a[4 * q4 + k]);
     }
   }
 }
@@ -191,270 +194,404 @@ __global__ __launch_bounds__(64) void probe_kernel(const bf16_t* __restrict__ q,
   p[1] = f2bf(b * scale / d);
 }
 
-// kmeans_kernel: one (block, head) per 256-thread workgroup; under 40 KB of LDS so four workgroups share a CU.
-//   LDS region A (33 KB): the K tile, then the probe logits, then X (fp32, padded rows), then the K and V tiles
-//                         for the final means (X waits in registers while the probe softmax reads the logits)
-//   LDS region B (7 KB):  the softmax partials, then the dot partials / centroids / weights
-// Thread (wave w, lane l) keeps X[l][32 w ..] in registers for the distances; the centroid sums (threads 0..127,
-// channel = tid) read X's columns from LDS.
+// stage rows [r0, r0 + 64) of one head of an (L, H, D) tensor into a swizzled LDS tile with one wave (16 transfers
+// of 1 KB); rows >= L are clamped to L - 1 (callers mask them)
+__device__ __forceinline__ void stage_rows_wave(const bf16_t* x, int r0, int L, int H, int h, char* tile) {
+  const int l = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int P = i * 64 + l;
+    const int R = P >> 4, c = (P & 15) ^ swz(R);
+    const int row = min(r0 + R, L - 1);
+    g2lds16(x + ((size_t)row * H + h) * HD + c * 8, tile + i * 1024);
+  }
+}
+
+// x + the value of lane (lane ^ M) within each 32-lane half (ds_swizzle bit mode, no LDS traffic)
+// the same staging through the compiler-invisible transfer (dma16): the caller waits (dma_wait) before reading, and
+// LDS accesses in between are not held back behind it. A buffer resource per block keeps the offsets 32-bit.
+__device__ __forceinline__ void stage_rows_wave_dma(const bf16_t* x, int r0, int L, int H, int h, char* tile) {
+  const int l = threadIdx.x & 63, rows = min(BK, L - r0);
+  const srd_t rs = make_srd(x + ((size_t)r0 * H + h) * HD, (unsigned)((rows - 1) * H * HD * 2 + 256));
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int P = i * 64 + l;
+    const int R = P >> 4, c = (P & 15) ^ swz(R);
+    dma16(rs, tile + i * 1024, (unsigned)(min(R, rows - 1) * H * HD * 2 + c * 16), 0u);
+  }
+}
+
+// orders this wave's LDS accesses against each other across lanes (the wave runs in lockstep and the LDS serves a
+// wave's instructions in order: only the compiler has to be kept from moving them)
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+template <int M>
+__device__ __forceinline__ float swz_xor(float x) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), (M << 10) | 0x1F));
+}
+
+// kmeans_kernel: one wave (64-thread workgroup) per (block, head), no cross-wave synchronisation; 17.3 KB of LDS
+// (the K tile, later the V tile, and per-token weights).
+//
+// The clustering works on the token Gram matrix P = X X^T (64 x 64, X = K Lchol) instead of X: a weighted centroid
+// is a combination of tokens, mu_c = S_c / m_c with S_c = sum_s a_sc x_s, a_sc = w_s [lab_s == c] and
+// m_c = max(sum_s a_sc, 1e-6), so with U[t][c] = sum_s a_sc P[s][t] = x_t . S_c
+//   x_t . mu_c = U[t][c] / m_c   and   |mu_c|^2 = sum_t a_tc U[t][c] / m_c^2,
+// the same distances |mu_c|^2 - 2 x_t . mu_c as the reference's Lloyd step (representatives.py:103-118) for 64 x 4
+// x 64 multiply-adds per round instead of two 64 x 4 x 128 products. A cluster left without weight gets distance
+// +inf in the next round, so the centroid it keeps in the reference is never used; the representatives are plain
+// means over the final labels.
+//   1. probe logits S^T = K probes^T (MFMA, tokens in registers, probes across lanes), the softmax over tokens in
+//      registers, the sum over probes by a 32-lane reduce-scatter: token weights w (LDS)
+//   2. X^T = Lchol^T K^T per 32-channel slice (MFMA, tokens across lanes), split into bf16 high + low parts, and
+//      P += Xh Xh^T + Xh Xl^T + Xl Xh^T (relative error ~2^-16); P stays in registers (lane: token t, registers:
+//      tokens s)
+//   3. Lloyd from the four contiguous 16-token groups with early exit: each lane sums U over its registers' tokens
+//      (the per-token cluster weights come from LDS), the two lane halves are added, |mu|^2 and m by wave sums
+//   4. cluster sums of K and V: one-hot labels times the transposed tile on MFMA; the block means (MEANS) as the
+//      same sequential fp32 sums as means_kernel
+constexpr int KM_WAVES = 4;  // independent waves (blocks) per workgroup
+
 template <bool MEANS>
-__global__ __launch_bounds__(256, 4) void kmeans_kernel(const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-                                                        const bf16_t* __restrict__ metric_t,
-                                                        const bf16_t* __restrict__ probes, bf16_t* __restrict__ k4,
-                                                        bf16_t* __restrict__ v4, float* __restrict__ lc4,
-                                                        bf16_t* __restrict__ km, bf16_t* __restrict__ vm, int L,
-                                                        int H, int NB, int iters) {
-  __shared__ __attribute__((aligned(16))) float regA[BK * (HD + 1)];
-  __shared__ __attribute__((aligned(16))) float regB[(4 * BK + HD + BK) * 4];
-  __shared__ float wgt[BK];
-  __shared__ int lab[BK];
-  __shared__ float cw[4];
-  __shared__ float nnp[2][4];
-  __shared__ int red_i[1];
-  float(*X)[HD + 1] = reinterpret_cast<float(*)[HD + 1]>(regA);
-  char* kt2 = reinterpret_cast<char*>(regA);  // K tile for the means (after the clustering)
-  char* vt2 = kt2 + BK * 256;                 // V tile for the means
-  char* kt = reinterpret_cast<char*>(regA);   // K tile for X and the probe logits
-  float(*sp)[BK + 1] = reinterpret_cast<float(*)[BK + 1]>(regA);
-  float(*wpart)[BK] = reinterpret_cast<float(*)[BK]>(regB);  // softmax partials [4][BK]
-  float* pmax = regB + 4 * BK;
-  float* pinv = pmax + NPROBE;
-  f32x4* part = reinterpret_cast<f32x4*>(regB);            // [4 waves][BK] partial dots
-  f32x4* cen = reinterpret_cast<f32x4*>(regB) + 4 * BK;    // [HD] centroids, (channel, cluster)
-  f32x4* aw = reinterpret_cast<f32x4*>(regB) + 4 * BK + HD;  // [BK] token weight per cluster
+__global__ __launch_bounds__(64 * KM_WAVES, 2) void kmeans_kernel(const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+                                                    const bf16_t* __restrict__ metric_t,
+                                                    const bf16_t* __restrict__ probes, bf16_t* __restrict__ k4,
+                                                    bf16_t* __restrict__ v4, float* __restrict__ lc4,
+                                                    bf16_t* __restrict__ km, bf16_t* __restrict__ vm, int L, int H,
+                                                    int NB, int iters) {
+  __shared__ __attribute__((aligned(16))) char tiles[KM_WAVES][BK * 256];
+  __shared__ __attribute__((aligned(16))) float wtoks[KM_WAVES][BK];
+  __shared__ __attribute__((aligned(16))) f32x4 atoks[KM_WAVES][BK];
 
-  const int j = blockIdx.x, h = blockIdx.y;
-  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, hi = l >> 5, lq = l & 31;
+  const int wv = threadIdx.x >> 6;
+  const int j = blockIdx.x * KM_WAVES + wv, h = blockIdx.y;
+  if (j >= NB) return;  // (no workgroup barrier below: the waves are independent)
+  char* tile = tiles[wv];
+  float* wtok = wtoks[wv];
+  f32x4* atok = atoks[wv];
+  const int l = threadIdx.x & 63, hi = l >> 5, lq = l & 31;
   const int nvalid = min(L - j * BK, BK);
-  // the metric operands do not depend on the K tile: their loads are issued first, so that their latency
-  // overlaps the tile's staging instead of following it (the first half of them: registers)
-  const int tb = wv & 1, e0 = (wv >> 1) * 2, pb = wv & 1, tk = wv >> 1;
   const bf16_t* mt = metric_t + (size_t)h * HD * HD;
-  bf16x8 mop[4][2];
-  {
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int eb = 0; eb < 2; ++eb)
-        mop[ks][eb] = *reinterpret_cast<const bf16x8*>(mt + (size_t)(32 * (e0 + eb) + lq) * HD + 16 * ks + 8 * hi);
-  }
-  stage_rows(k, j * BK, L, H, h, kt);
-  wait_vmem();
-  __syncthreads();
+  const bf16_t* pr = probes + (size_t)h * NPROBE * HD;
+  // token of register r of a 32 x 32 C tile whose rows are tokens (tile tb)
+  auto row_tok = [&](int tb, int r) { return 32 * tb + 8 * (r >> 2) + 4 * hi + (r & 3); };
 
-  // X = K Lchol: wave wv -> tokens 32 (wv & 1) .., channels 64 (wv >> 1) .. (two 32-wide C tiles); probe logits:
-  // wave wv -> probes 32 (wv & 1) .., tokens 32 (wv >> 1) ..
-  f32x16 ax[2] = {f32x16{}, f32x16{}}, ap = {};
-#pragma unroll
-  for (int ks = 0; ks < 8; ++ks) {
-    const bf16x8 a = lds_read16(kt, tile_off(32 * tb + lq, 2 * ks + hi));
-#pragma unroll
-    for (int eb = 0; eb < 2; ++eb)
-      ax[eb] = mfma32(a, ks < 4 ? mop[ks & 3][eb]
-                                : *reinterpret_cast<const bf16x8*>(mt + (size_t)(32 * (e0 + eb) + lq) * HD + 16 * ks + 8 * hi),
-                      ax[eb]);
-  }
-  const bf16_t* pr = probes + ((size_t)h * NPROBE + 32 * pb + lq) * HD;
+  stage_rows_wave(k, j * BK, L, H, h, tile);
+  bf16x8 pop[8][2];  // probe operands (B: probe 32 pb + lq, channels 16 ks + 8 hi ..), loaded under the staging
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks)
-    ap = mfma32(*reinterpret_cast<const bf16x8*>(pr + 16 * ks + 8 * hi), lds_read16(kt, tile_off(32 * tk + lq, 2 * ks + hi)),
-                ap);
-  __syncthreads();  // every wave is done with the K tile: region A takes the probe logits
-  {
-    const int pb = wv & 1, tk = wv >> 1;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sp[32 * pb + 8 * (r / 4) + 4 * hi + (r % 4)][32 * tk + lq] = ap[r];
-  }
-  __syncthreads();
+    for (int pb = 0; pb < 2; ++pb)
+      pop[ks][pb] = *reinterpret_cast<const bf16x8*>(pr + (size_t)(32 * pb + lq) * HD + 16 * ks + 8 * hi);
+  wait_vmem();
+  wave_lds_sync();
 
-  // probe softmax weights w_t = sum_p softmax_p(t). (a) thread (probe tid % 64, token quarter tid / 64): row max
-  // and row sum over its 16 tokens, combined through LDS; (b) wave wv, lane = token: its 16 probes. Plain loops
-  // and LDS instead of one cross-lane reduction per probe.
+  bf16x8 mop[8];  // metric operands of the first 32-channel slice (A: metric_t row 32 eb + lq, channels 16 ks + 8 hi ..)
+  // 1. probe logits: sp[tb][pb][r] = K[row_tok(tb, r)] . probe[32 pb + lq]
   {
-    const int pp = tid & 63, q4 = tid >> 6;
-    float mx = -INFINITY;
+    f32x16 sp[2][2] = {{f32x16{}, f32x16{}}, {f32x16{}, f32x16{}}};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) {
+        const bf16x8 kf = lds_read16(tile, tile_off(32 * tb + lq, 2 * ks + hi));
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) sp[tb][pb] = mfma32(kf, pop[ks][pb], sp[tb][pb]);
+      }
+    if (nvalid < BK) {  // the last block: tokens past L get logit -inf, i.e. weight 0
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (row_tok(tb, r) >= nvalid) sp[tb][pb][r] = -INFINITY;
+    }
+    float ew[32];  // [16 tb + r]: sum over this lane's probes of the normalised exponentials
+#pragma unroll
+    for (int i = 0; i < 32; ++i) ew[i] = 0.0f;
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb) {
+      // max(x, m) as med3(x, m, +inf): one instruction, no operand canonicalisation
+      float mx = -INFINITY;
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = __builtin_amdgcn_fmed3f(sp[tb][pb][r], mx, INFINITY);
+      mx = __builtin_amdgcn_fmed3f(__shfl_xor(mx, 32), mx, INFINITY);
+      const float nmx = -mx * LOG2E;
+      float e[32], sm = 0.0f;
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          e[16 * tb + r] = exp2f_fast(fmaf(sp[tb][pb][r], LOG2E, nmx));
+          sm += e[16 * tb + r];
+        }
+      sm += __shfl_xor(sm, 32);
+      const float inv = 1.0f / sm;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) ew[i] = fmaf(e[i], inv, ew[i]);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)  // (loaded under the reduction)
+      mop[ks] = *reinterpret_cast<const bf16x8*>(mt + (size_t)lq * HD + 16 * ks + 8 * hi);
+    // reduce-scatter over the 32 lanes of each half: lane lq ends with the total of value index lq
+    float r16[16], r8[8], r4[4], r2[2];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int tk = 16 * q4 + i;
-      mx = fmaxf(mx, tk < nvalid ? sp[pp][tk] : -INFINITY);
+      const bool up = lq & 16;
+      r16[i] = (up ? ew[i + 16] : ew[i]) + swz_xor<16>(up ? ew[i] : ew[i + 16]);
     }
-    wpart[q4][pp] = mx;
-    __syncthreads();
-    const float m = fmaxf(fmaxf(wpart[0][pp], wpart[1][pp]), fmaxf(wpart[2][pp], wpart[3][pp]));
-    float sm = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int tk = 16 * q4 + i;
-      sm += tk < nvalid ? exp2f_fast((sp[pp][tk] - m) * LOG2E) : 0.0f;
+    for (int i = 0; i < 8; ++i) {
+      const bool up = lq & 8;
+      r8[i] = (up ? r16[i + 8] : r16[i]) + swz_xor<8>(up ? r16[i] : r16[i + 8]);
     }
-    __syncthreads();  // the maxima are read
-    wpart[q4][pp] = sm;
-    __syncthreads();
-    if (tid < NPROBE) {
-      pmax[tid] = m;
-      pinv[tid] = 1.0f / (wpart[0][tid] + wpart[1][tid] + wpart[2][tid] + wpart[3][tid]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool up = lq & 4;
+      r4[i] = (up ? r8[i + 4] : r8[i]) + swz_xor<4>(up ? r8[i] : r8[i + 4]);
     }
-    __syncthreads();
-    float wsum = 0.0f;
-    if (l < nvalid) {
-#pragma unroll 4
-      for (int p = 16 * wv; p < 16 * wv + 16; ++p) wsum = fmaf(exp2f_fast((sp[p][l] - pmax[p]) * LOG2E), pinv[p], wsum);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const bool up = lq & 2;
+      r2[i] = (up ? r4[i + 2] : r4[i]) + swz_xor<2>(up ? r4[i] : r4[i + 2]);
     }
-    wpart[wv][l] = wsum;  // (every read of wpart above precedes the last barrier)
+    const bool up = lq & 1;
+    const float tot = (up ? r2[1] : r2[0]) + swz_xor<1>(up ? r2[0] : r2[1]);
+    const int t = row_tok(lq >> 4, lq & 15);
+    wtok[t] = t < nvalid ? tot * ((float)nvalid / (float)NPROBE) : 0.0f;
   }
-  __syncthreads();  // the probe logits are consumed: region A takes X
-  {
-    const int tb = wv & 1, e0 = (wv >> 1) * 2;
-#pragma unroll
-    for (int eb = 0; eb < 2; ++eb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) X[32 * tb + 8 * (r / 4) + 4 * hi + (r % 4)][32 * (e0 + eb) + lq] = ax[eb][r];
-  }
-  // token weights and the initial labels (four contiguous 16-token groups); the per-cluster weights cw are
-  // summed by the centroid pass
-  auto set_weights = [&](int lb) {  // wave 0, lane = token: aw and lab of the labels lb
-    const float w = wgt[l];
-    f32x4 a4;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) a4[c] = lb == c ? w : 0.0f;
-    aw[l] = a4;
-    lab[l] = lb;
-  };
-  if (wv == 0) {
-    const float s = wpart[0][l] + wpart[1][l] + wpart[2][l] + wpart[3][l];
-    wgt[l] = l < nvalid ? s * ((float)nvalid / (float)NPROBE) : 0.0f;
-    set_weights(l / (BK / 4));
-  }
-  __syncthreads();
-  float xd[32];  // X[l][32 wv + i]
-#pragma unroll
-  for (int i = 0; i < 32; ++i) xd[i] = X[l][32 * wv + i];
 
-  // weighted centroids of the current labels and the cluster weights cw: thread (channel tid % 128, token half
-  // tid / 128) sums its 32 tokens, the second halves are added through LDS (`part`, free at this point); a cluster
-  // with zero weight keeps its previous centroid unless `init`; also the squared centroid norms (per wave, nnp).
-  // Every thread of the workgroup calls it (it holds a barrier).
-  auto centroids = [&](bool init) {
-    const int ch = tid & (HD - 1), hh = tid >> 7;
-    float s[4] = {0.f, 0.f, 0.f, 0.f}, ws[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int t = 32 * hh; t < 32 * hh + 32; ++t) {
-      const f32x4 a4 = aw[t];
-      const float x = X[t][ch];
+  // 2. P = X X^T, X^T built 32 channels at a time
+  f32x16 P[2][2] = {{f32x16{}, f32x16{}}, {f32x16{}, f32x16{}}};  // [sb][tb]: P[row_tok(sb, r)][32 tb + lq]
+#pragma unroll 1
+  for (int eb = 0; eb < 4; ++eb) {
+    f32x16 xt[2] = {f32x16{}, f32x16{}};  // X^T[32 eb + row][32 tb + lq]
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        s[c] = fmaf(a4[c], x, s[c]);
-        ws[c] += a4[c];
-      }
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb)
+        xt[tb] = mfma32(mop[ks], lds_read16(tile, tile_off(32 * tb + lq, 2 * ks + hi)), xt[tb]);
+    bf16x8 xh[2][2], xl[2][2];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float x = xt[tb][8 * q + i];
+          const __bf16 b = (__bf16)x;
+          xh[tb][q][i] = b;
+          xl[tb][q][i] = (__bf16)(x - (float)b);
+        }
+    if (eb < 3) {  // the next slice's metric operands load under this slice's P products
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks)
+        mop[ks] = *reinterpret_cast<const bf16x8*>(mt + (size_t)(32 * (eb + 1) + lq) * HD + 16 * ks + 8 * hi);
     }
-    if (hh == 1) {
-      part[ch] = f32x4{s[0], s[1], s[2], s[3]};
-      part[HD + ch] = f32x4{ws[0], ws[1], ws[2], ws[3]};
-    }
-    __syncthreads();
-    if (hh == 1) return;
-    const f32x4 s1 = part[ch], w1 = part[HD + ch];
-    f32x4 c4 = init ? f32x4{} : cen[ch];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float w = ws[c] + w1[c];
-      if (init || w > 0.0f) c4[c] = (s[c] + s1[c]) / fmaxf(w, 1e-6f);
-      if (ch == 0) cw[c] = w;
-    }
-    cen[ch] = c4;
-    float q[4];
+    for (int q = 0; q < 2; ++q)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) q[c] = wave_sum_dpp(c4[c] * c4[c]);
-    if (l == 0) {
+      for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) nnp[wv][c] = q[c];
-    }
-  };
-  centroids(true);
-  __syncthreads();
-  for (int it = 0; it < iters; ++it) {
-    {  // partial dots over channels 32 wv .. 32 wv + 31 for token l
-      float d[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int tb = 0; tb < 2; ++tb) {
+          P[sb][tb] = mfma32(xh[sb][q], xh[tb][q], P[sb][tb]);
+          P[sb][tb] = mfma32(xh[sb][q], xl[tb][q], P[sb][tb]);
+          P[sb][tb] = mfma32(xl[sb][q], xh[tb][q], P[sb][tb]);
+        }
+  }
+  wave_lds_sync();  // wtok is written
+
+  // the K tile's last uses: its transposed operands for the cluster sums (kept in registers) and the block mean;
+  // then the V tile streams into the same LDS under the clustering
+  auto block_mean = [&](bf16_t* dst) {  // the same sequential fp32 sum and division as means_kernel
+    const int e = 2 * l;
+    float a = 0.f, b = 0.f;
+    if (nvalid == BK) {  // reads issued 16 rows ahead of the sums
 #pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        const f32x4 c4 = cen[32 * wv + i];
+      for (int r0 = 0; r0 < BK; r0 += 16) {
+        unsigned w[16];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) d[c] = fmaf(xd[i], c4[c], d[c]);
-      }
-      part[wv * BK + l] = f32x4{d[0], d[1], d[2], d[3]};
-    }
-    __syncthreads();
-    if (wv == 0) {
-      const f32x4 p0 = part[l], p1 = part[BK + l], p2 = part[2 * BK + l], p3 = part[3 * BK + l];
-      int best = 0;
-      float bd = INFINITY;
+        for (int r = 0; r < 16; ++r)
+          w[r] = *reinterpret_cast<const unsigned*>(tile + tile_off(r0 + r, e / 8) + (e % 8) * 2);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float xcd = p0[c] + p1[c] + p2[c] + p3[c];
-        const float nn = nnp[0][c] + nnp[1][c];
-        const float dc = cw[c] > 0.0f ? nn - 2.0f * xcd : INFINITY;
-        if (c == 0 || dc < bd) {  // first minimum, like argmin
-          bd = dc;
-          best = c;
+        for (int r = 0; r < 16; ++r) {
+          a += __uint_as_float(w[r] << 16);
+          b += __uint_as_float(w[r] & 0xffff0000u);
         }
       }
-      const int changed = __popcll(__builtin_amdgcn_ballot_w64((l < nvalid) && best != lab[l]));
-      set_weights(best);
-      if (l == 0) red_i[0] = changed;
-    }
-    __syncthreads();
-    // converged, or the last round: the labels are final and the representatives are plain means over them, so
-    // the centroids of these labels are not needed
-    if (red_i[0] == 0 || it == iters - 1) break;
-    centroids(false);
-    __syncthreads();
-  }
-
-  // representatives: plain means of K and V over each cluster's valid tokens (both tiles in LDS, region A)
-  stage_rows(k, j * BK, L, H, h, kt2);
-  stage_rows(v, j * BK, L, H, h, vt2);
-  wait_vmem();
-  __syncthreads();
-  {
-    const int c = tid >> 6, e = 2 * (tid & 63);
-    float k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
-    int n = 0;
+    } else {
 #pragma unroll 4
-    for (int t = 0; t < nvalid; ++t) {
-      const int off = tile_off(t, e / 8) + (e % 8) * 2;
-      const unsigned kw = *reinterpret_cast<const unsigned*>(kt2 + off);
-      const unsigned vw = *reinterpret_cast<const unsigned*>(vt2 + off);
-      const float m = lab[t] == c ? 1.0f : 0.0f;
-      n += lab[t] == c;
-      k0 = fmaf(m, __uint_as_float(kw << 16), k0);
-      k1 = fmaf(m, __uint_as_float(kw & 0xffff0000u), k1);
-      v0 = fmaf(m, __uint_as_float(vw << 16), v0);
-      v1 = fmaf(m, __uint_as_float(vw & 0xffff0000u), v1);
-    }
-    const float inv = 1.0f / fmaxf((float)n, 1.0f);
-    const size_t o = ((size_t)h * (NB + 1) * 4 + (size_t)j * 4 + c) * HD + e;
-    k4[o] = f2bf(k0 * inv);
-    k4[o + 1] = f2bf(k1 * inv);
-    v4[o] = f2bf(v0 * inv);
-    v4[o + 1] = f2bf(v1 * inv);
-    if ((tid & 63) == 0) lc4[(size_t)h * (NB + 1) * 4 + (size_t)j * 4 + c] = n > 0 ? log2f((float)n) : -INFINITY;
-  }
-  if (MEANS && tid < 128) {  // block means: the same sequential fp32 sum and division as means_kernel
-    const char* src = tid < 64 ? kt2 : vt2;
-    bf16_t* dst = tid < 64 ? km : vm;
-    const int e = 2 * (tid & 63);
-    float a = 0.f, b = 0.f;
-#pragma unroll 4
-    for (int r = 0; r < nvalid; ++r) {
-      const unsigned w = *reinterpret_cast<const unsigned*>(src + tile_off(r, e / 8) + (e % 8) * 2);
-      a += __uint_as_float(w << 16);
-      b += __uint_as_float(w & 0xffff0000u);
+      for (int r = 0; r < nvalid; ++r) {
+        const unsigned w = *reinterpret_cast<const unsigned*>(tile + tile_off(r, e / 8) + (e % 8) * 2);
+        a += __uint_as_float(w << 16);
+        b += __uint_as_float(w & 0xffff0000u);
+      }
     }
     const float n = (float)nvalid;
     const size_t o = ((size_t)j * H + h) * HD + e;
     dst[o] = f2bf(a / n);
     dst[o + 1] = f2bf(b / n);
+  };
+  if (MEANS) block_mean(km);
+  bf16x8 kT[4][4];  // [db][ks]: K[16 ks + 8 hi + i][32 db + lq]
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int base = 16 * ks + 8 * hi;
+      kT[db][ks] = cat_tr(tr4(tile, base, db), tr4(tile, base + 4, db));
+    }
+  wave_lds_sync();  // the K tile is consumed
+  stage_rows_wave_dma(v, j * BK, L, H, h, tile);
+
+  // 3. weighted Lloyd
+  const bool tv[2] = {lq < nvalid, 32 + lq < nvalid};
+  const float wt[2] = {wtok[lq], wtok[32 + lq]};
+  int lab[2] = {lq >> 4, 2 + (lq >> 4)};  // the four contiguous 16-token groups
+  // U summed over all four clusters does not depend on the labels; each round sums only the tokens whose label
+  // has bit 0, bit 1, or both set, and the four cluster sums follow from those and the total
+  float uall[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 w4 = *reinterpret_cast<const f32x4*>(wtok + 32 * sb + 8 * g + 4 * hi);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) uall[tb] = fmaf(w4[i], P[sb][tb][4 * g + i], uall[tb]);
+    }
+#pragma unroll
+  for (int tb = 0; tb < 2; ++tb) uall[tb] += __shfl_xor(uall[tb], 32);
+  float u[2][4], cw[4], r2m[4], nn[4];
+  auto update = [&]() {  // u, cw, r2m, nn of the labels `lab`
+    if (hi == 0) {
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) {
+        const float w = wt[tb];
+        atok[32 * tb + lq] = f32x4{lab[tb] & 1 ? w : 0.0f, lab[tb] & 2 ? w : 0.0f, lab[tb] == 3 ? w : 0.0f, 0.0f};
+      }
+    }
+    wave_lds_sync();
+    float ub[2][3] = {{0.f, 0.f, 0.f}, {0.f, 0.f, 0.f}};  // sums over the tokens with label bit 0 / bit 1 / both
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const f32x4 a = atok[row_tok(sb, r)];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+          for (int c = 0; c < 3; ++c) ub[tb][c] = fmaf(a[c], P[sb][tb][r], ub[tb][c]);
+      }
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+#pragma unroll
+      for (int c = 0; c < 3; ++c) ub[tb][c] += __shfl_xor(ub[tb][c], 32);
+      u[tb][3] = ub[tb][2];
+      u[tb][1] = ub[tb][0] - ub[tb][2];
+      u[tb][2] = ub[tb][1] - ub[tb][2];
+      u[tb][0] = uall[tb] - ub[tb][0] - ub[tb][1] + ub[tb][2];
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float wsum = 0.0f, usum = 0.0f;
+      if (hi == 0) {
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+          const float a = lab[tb] == c ? wt[tb] : 0.0f;
+          wsum += a;
+          usum = fmaf(a, u[tb][c], usum);
+        }
+      }
+      cw[c] = wave_sum_dpp(wsum);
+      const float rm = __builtin_amdgcn_rcpf(fmaxf(cw[c], 1e-6f));
+      nn[c] = wave_sum_dpp(usum) * rm * rm;
+      r2m[c] = 2.0f * rm;
+    }
+    wave_lds_sync();  // every lane has read atok before the next update rewrites it
+  };
+  update();
+  for (int it = 0; it < iters; ++it) {
+    int changed = 0;
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      int best = 0;
+      float bd = INFINITY;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float dc = cw[c] > 0.0f ? fmaf(-u[tb][c], r2m[c], nn[c]) : INFINITY;
+        if (c == 0 || dc < bd) {  // first minimum, like argmin
+          bd = dc;
+          best = c;
+        }
+      }
+      changed += __popcll(__builtin_amdgcn_ballot_w64(tv[tb] && best != lab[tb]) & 0xffffffffull);
+      lab[tb] = best;
+    }
+    // converged, or the last round: the labels are final and the centroids of these labels are not needed
+    if (changed == 0 || it == iters - 1) break;
+    update();
   }
+
+  // 4. cluster sums: S[c][d] = sum_t [lab_t == c] x[t][d] with one-hot bf16 (exact) times the tile on MFMA
+  const unsigned long long vmask = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1);
+  const unsigned long long b0 = (__builtin_amdgcn_ballot_w64(lab[0] & 1) & 0xffffffffull) |
+                                (__builtin_amdgcn_ballot_w64(lab[1] & 1) << 32);
+  const unsigned long long b1 = (__builtin_amdgcn_ballot_w64(lab[0] & 2) & 0xffffffffull) |
+                                (__builtin_amdgcn_ballot_w64(lab[1] & 2) << 32);
+  unsigned long long member[4];
+  member[0] = ~b0 & ~b1 & vmask;
+  member[1] = b0 & ~b1 & vmask;
+  member[2] = ~b0 & b1 & vmask;
+  member[3] = b0 & b1 & vmask;
+  float inv[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) inv[c] = 1.0f / fmaxf((float)__popcll(member[c]), 1.0f);
+  // one-hot operand: lane (hi, lq) holds [lab_t == lq] for t = 16 ks + 8 hi + i (zero for lanes lq >= 4)
+  bf16x8 oh[4];
+  {
+    const unsigned long long mine =
+        (lq == 0 ? member[0] : lq == 1 ? member[1] : lq == 2 ? member[2] : lq == 3 ? member[3] : 0ull) >> (8 * hi);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) oh[ks][i] = ((mine >> (16 * ks + i)) & 1ull) ? (__bf16)1.0f : (__bf16)0.0f;
+  }
+  const size_t rep0 = (size_t)h * (NB + 1) * 4 + (size_t)j * 4;
+  auto cluster_means = [&](bf16_t* out, const bf16x8 (*xt)[4]) {  // xt: transposed operands, or null: the tile
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      f32x16 s = {};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int base = 16 * ks + 8 * hi;
+        s = mfma32(oh[ks], xt ? xt[db][ks] : cat_tr(tr4(tile, base, db), tr4(tile, base + 4, db)), s);
+      }
+      if (hi == 0) {  // rows 0..3 of the C tile are the four clusters
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const __bf16 b = (__bf16)(s[c] * inv[c]);
+          out[(rep0 + c) * HD + 32 * db + lq] = __builtin_bit_cast(bf16_t, b);
+        }
+      }
+    }
+  };
+  cluster_means(k4, kT);
+  if (l < 4) {
+    const int n = __popcll(member[l == 0 ? 0 : l == 1 ? 1 : l == 2 ? 2 : 3]);
+    lc4[rep0 + l] = n > 0 ? log2f((float)n) : -INFINITY;
+  }
+  dma_wait();  // the V tile has arrived
+  wave_lds_sync();
+  cluster_means(v4, nullptr);
+  if (MEANS) block_mean(vm);
 }
 
 static void run_representatives(const void* q, const void* k, const void* v, void* k_rep, void* v_rep,
@@ -470,11 +607,11 @@ static void run_representatives(const void* q, const void* k, const void* v, voi
   hipLaunchKernelGGL(probe_kernel, dim3(NPROBE, H), dim3(64), 0, stream, (const bf16_t*)q, w.probes, L, H, nb,
                      scale);
   if (k_mean)
-    hipLaunchKernelGGL(kmeans_kernel<true>, dim3(nb, H), dim3(256), 0, stream, (const bf16_t*)k, (const bf16_t*)v,
+    hipLaunchKernelGGL(kmeans_kernel<true>, dim3((nb + KM_WAVES - 1) / KM_WAVES, H), dim3(64 * KM_WAVES), 0, stream, (const bf16_t*)k, (const bf16_t*)v,
                        w.metric_t, w.probes, (bf16_t*)k_rep, (bf16_t*)v_rep, log_counts, (bf16_t*)k_mean,
                        (bf16_t*)v_mean, L, H, nb, iters);
   else
-    hipLaunchKernelGGL(kmeans_kernel<false>, dim3(nb, H), dim3(256), 0, stream, (const bf16_t*)k,
+    hipLaunchKernelGGL(kmeans_kernel<false>, dim3((nb + KM_WAVES - 1) / KM_WAVES, H), dim3(64 * KM_WAVES), 0, stream, (const bf16_t*)k,
                        (const bf16_t*)v, w.metric_t, w.probes, (bf16_t*)k_rep, (bf16_t*)v_rep, log_counts,
                        nullptr, nullptr, L, H, nb, iters);
 }
