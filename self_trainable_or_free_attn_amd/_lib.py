@@ -1,11 +1,16 @@
-"""ctypes binding of the C ABI in include/echosparse_hip.h and include/vsa_hip.h (libechosparse_hip.so, built
-in-tree by build_lib).
+"""Bindings of the C ABI in include/echosparse_hip.h and include/vsa_hip.h (libechosparse_hip.so, built in-tree by
+build_lib).
 
-There is no fallback: if the library is missing or fails to load, every kernel call raises. Arguments are torch
-tensors (device pointers taken with data_ptr) or Python scalars; each call is enqueued on the current HIP stream
-of torch, so the kernels order with the surrounding torch work exactly like the reference's launches do.
+Kernel calls (`call`) go through the torch operators torch.ops.echosparse_gfx950.<entry point> (torch_ops.py,
+lib/libechosparse_torch.so): arguments are tensors (None = NULL) and Python scalars in the header's order, and each
+call is enqueued on torch's current HIP stream of the tensors' device, so the kernels order with the surrounding
+torch work exactly like the reference's launches do. The ctypes handle (`lib`) serves the entry points without a
+stream (workspace sizes, limits, the error string) and tests that drive the C ABI directly.
+
+There is no fallback: if either library is missing or fails to load, every kernel call raises.
 """
 import ctypes
+import numbers
 import os
 
 import torch
@@ -13,6 +18,7 @@ import torch
 # ECHOSPARSE_HIP_LIB: load another build of the same ABI (development A/B measurements)
 LIB_PATH = os.environ.get("ECHOSPARSE_HIP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib",
                                                                 "libechosparse_hip.so")
+TORCH_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libechosparse_torch.so")
 
 P, I, F, Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
 LL, DB = ctypes.c_longlong, ctypes.c_double
@@ -75,6 +81,7 @@ NO_STREAM = {"es_representatives_workspace": ([I, I, I], Z), "es_representatives
              "es_abi_version": ([], I), "vsa_topk_workspace": ([I, I], Z)}
 
 _lib = None
+_ops = None
 
 
 def lib():
@@ -83,7 +90,8 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} is not built; run `python -m self_trainable_or_free_attn_amd.build_lib`")
-        so = ctypes.CDLL(LIB_PATH)
+        # RTLD_GLOBAL: the torch operator library resolves its C symbols against this copy
+        so = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
         for name, args in SIGNATURES.items():
             fn = getattr(so, name)
             fn.argtypes = [*args, P]
@@ -96,26 +104,37 @@ def lib():
     return _lib
 
 
+def ops():
+    """torch.ops.echosparse_gfx950 (loaded on first use, after the C library; raises if it is not built)."""
+    global _ops
+    if _ops is None:
+        lib()
+        if not os.path.exists(TORCH_LIB_PATH):
+            raise RuntimeError(f"{TORCH_LIB_PATH} is not built; run `python -m self_trainable_or_free_attn_amd.build_lib`")
+        torch.ops.load_library(TORCH_LIB_PATH)
+        _ops = torch.ops.echosparse_gfx950
+    return _ops
+
+
 def ptr(x):
-    """Device pointer of a tensor (None -> NULL)."""
+    """Device pointer of a tensor (None -> NULL), for direct ctypes calls."""
     if x is None:
         return None
     return ctypes.c_void_p(x.data_ptr())
 
 
 def call(name, *args):
-    """Call an entry point on torch's current stream; raise RuntimeError with the library's message on failure."""
-    so = lib()
-    for a in args:
-        # a host tensor's address handed to a kernel faults the GPU: refuse it before the launch
-        if isinstance(a, torch.Tensor) and not a.is_cuda:
-            raise RuntimeError(f"{name}: every tensor argument must live on the GPU (got a {a.device} tensor)")
-    conv = [ptr(a) if isinstance(a, torch.Tensor) or a is None else a for a in args]
-    stream = torch.cuda.current_stream().cuda_stream
-    status = getattr(so, name)(*conv, ctypes.c_void_p(stream))
-    if status != 0:
-        msg = so.es_last_error_string().decode()
-        raise RuntimeError(f"{name} failed (status {status}): {msg}")
+    """Call an entry point through its torch operator on torch's current stream. A failing status raises
+    RuntimeError with the library's message; a host tensor is refused before the launch (its address handed to a
+    kernel would fault the GPU)."""
+    getattr(ops(), name)(*map(_plain, args))
+
+
+def _plain(a):
+    """Tensors, None and Python scalars pass as they are; other numbers (numpy scalars) become int / float."""
+    if a is None or isinstance(a, (torch.Tensor, bool, int, float)):
+        return a
+    return int(a) if isinstance(a, numbers.Integral) else float(a)
 
 
 def workspace_bytes(L, H, D):

@@ -1,4 +1,5 @@
-"""Build libechosparse_hip.so in-tree with hipcc for gfx950 (python -m self_trainable_or_free_attn_amd.build_lib).
+"""Build libechosparse_hip.so in-tree with hipcc for gfx950 (python -m self_trainable_or_free_attn_amd.build_lib), then
+the torch operator library over it (torch_ops.py, lib/libechosparse_torch.so).
 
 Every HIP source under csrc/ is compiled to an object in parallel and linked into lib/libechosparse_hip.so; the
 VSA sources (vsa_*.hip) are compiled a second time with -DES_ELEM_F16 for their fp16 entry points (suffix _f16).
@@ -63,6 +64,9 @@ def build(verbose=False, out=None):
     os.replace(tmp, lib_path)
     if verbose:
         print(f"built {lib_path} from {len(srcs)} compilations")
+    if out is None:  # the torch operators over the default build
+        from . import torch_ops
+        torch_ops.build(verbose=verbose)
     return lib_path
 
 

@@ -19,7 +19,7 @@
 namespace es {
 
 constexpr int NPROBE = 64;
-constexpr int MAX_SPLITS = 48;
+constexpr int MAX_SPLITS = 16;
 
 struct RepWorkspace {
   float* gram;       // (H, S, D, D)
@@ -67,18 +67,34 @@ __device__ __forceinline__ s16x4 tr4(const char* tile, int base, int db) {
   return lds_read_tr(tile, tile_off(row, c) + (l & 1) * 8);
 }
 
+// stage_rows through the compiler-invisible transfer (dma16), one buffer resource per block: the caller waits
+// (dma_wait) and synchronises before reading, and LDS reads of the other buffer are not held back behind it
+__device__ __forceinline__ void stage_rows_dma(const bf16_t* x, int r0, int L, int H, int h, char* tile) {
+  const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, rows = min(BK, L - r0);
+  const srd_t rs = make_srd(x + ((size_t)r0 * H + h) * HD, (unsigned)((rows - 1) * H * HD * 2 + 256));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int P = (wv * 4 + i) * 64 + l;
+    const int R = P >> 4, c = (P & 15) ^ swz(R);
+    dma16(rs, tile + (wv * 4 + i) * 1024, (unsigned)(min(R, rows - 1) * H * HD * 2 + c * 16), 0u);
+  }
+}
+
+// partial Gram matrix of one (row split, head): 64-row chunks double-buffered in LDS, the next chunk's transfer
+// in flight under the current chunk's products
 __global__ __launch_bounds__(256) void gram_kernel(const bf16_t* __restrict__ q, float* __restrict__ gram, int L,
                                                    int H, int rps, int splits) {
-  __shared__ __attribute__((aligned(16))) char tile[BK * 256];
+  __shared__ __attribute__((aligned(16))) char tiles[2][BK * 256];
   const int s = blockIdx.x, h = blockIdx.y;
   const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, hi = l >> 5, lq = l & 31;
   f32x16 acc[4] = {f32x16{}, f32x16{}, f32x16{}, f32x16{}};
   const int r_end = min(L, (s + 1) * rps);
-  for (int r0 = s * rps; r0 < r_end; r0 += BK) {
-    __syncthreads();
-    stage_rows(q, r0, L, H, h, tile);
-    wait_vmem();
-    __syncthreads();
+  if (s * rps < r_end) stage_rows_dma(q, s * rps, L, H, h, tiles[0]);
+  for (int r0 = s * rps, buf = 0; r0 < r_end; r0 += BK, buf ^= 1) {
+    dma_wait();
+    __syncthreads();  // chunk r0 has landed for every wave, and every wave is done with the other buffer
+    if (r0 + BK < r_end) stage_rows_dma(q, r0 + BK, L, H, h, tiles[buf ^ 1]);
+    const char* tile = tiles[buf];
     // rows >= r_end hold clamped copies: they are not part of this split, so zero their contribution by
     // restricting the k steps; the last chunk of a split may be partial only at L (rps is a multiple of 64)
     const int valid_rows = min(BK, r_end - r0);
@@ -164,9 +180,8 @@ __global__ __launch_bounds__(256) void chol_kernel(const float* __restrict__ gra
       }
     }
     __syncthreads();
-    const float piv = fmaxf(cb[j], eps);
-    const float inv = 1.0f / sqrtf(piv);
-    const float sc = cb[cc] / piv;
+    const float inv = __builtin_amdgcn_rsqf(fmaxf(cb[j], eps));  // 1 / sqrt(pivot), hardware rsq (1 ulp)
+    const float sc = cb[cc] * (inv * inv);
     if (tid < HD) mt[j * HD + tid] = f2bf(cb[tid] * inv);  // metric_t[j][d] = Lchol[d][j] (zero above j)
 #pragma unroll
     for (int q4 = 0; q4 < 16; ++q4) {

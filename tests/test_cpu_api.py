@@ -147,3 +147,36 @@ def test_host_tensors_are_refused_before_any_launch():
     x = torch.zeros(4)
     with pytest.raises(RuntimeError, match="must live on the GPU"):
         _lib.call("vsa_finalize", None, None, 0, x, x, 1, 64, 128)
+
+
+def test_torch_operators_are_generated_from_the_header():
+    """csrc/torch/ops.cpp is the generator's output for the current headers, and every stream-taking entry point is
+    an operator with the header's argument names, non-const pointers declared as written (Tensor(x!)?)."""
+    from self_trainable_or_free_attn_amd import _lib, torch_ops
+    assert open(torch_ops.SOURCE).read() == torch_ops.source(), "run build_lib: ops.cpp is stale"
+    if not os.path.exists(_lib.TORCH_LIB_PATH):
+        from self_trainable_or_free_attn_amd import build_lib
+        build_lib.build()
+    ops = _lib.ops()
+    eps = torch_ops.entry_points()
+    assert {n for n, _ in eps} == set(_lib.SIGNATURES)
+    for name, params in eps:
+        schema = getattr(ops, name).default._schema
+        assert [a.name for a in schema.arguments] == [p for _, p in params], name
+        for a, (ctype, _) in zip(schema.arguments, params):
+            written = a.alias_info is not None and a.alias_info.is_write
+            assert written == ("*" in ctype and not ctype.startswith("const")), (name, a.name)
+        assert len(schema.returns) == 0
+
+
+def test_torch_operators_trace_with_meta_tensors_and_refuse_host_tensors():
+    """Meta tensors run the no-op Meta kernel (fake-tensor tracing); host tensors are refused by name."""
+    import torch
+    from self_trainable_or_free_attn_amd import _lib
+    ops = _lib.ops()
+    m = torch.empty(64, 1, 128, dtype=torch.bfloat16, device="meta")
+    mm = torch.empty(1, 1, 128, dtype=torch.bfloat16, device="meta")
+    assert ops.es_block_means(m, m, mm, mm, 64, 1, 128) is None
+    c = torch.zeros(64, 1, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="es_block_means: every tensor argument must live on the GPU"):
+        ops.es_block_means(c, c, c[:1], c[:1], 64, 1, 128)

@@ -1,5 +1,5 @@
 """Parity of every gfx950 kernel of the EchoSparse set with the CPU oracle (oracle/echosparse_ref.py), through the
-C ABI (the kernels.gfx950 wrappers are thin ctypes calls). Floating-point outputs: max-abs 2e-2 and rel-L2 1e-2;
+C ABI (the kernels.gfx950 wrappers are thin calls of its torch operators, torch.ops.echosparse_gfx950). Floating-point outputs: max-abs 2e-2 and rel-L2 1e-2;
 plan outputs (keep, lists, counts, bit masks): bit-exact. Shapes follow the reference's own GPU tests
 (L = 4152: 65 kv blocks with a 56-token tail, 33 query tiles with a 56-row tail)."""
 import math
@@ -54,6 +54,34 @@ def test_library_loads_and_reports_errors(dev):
     q = torch.zeros(64, 1, 64, device=dev, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="head dimension must be 128"):
         _lib.call("es_block_means", q, q, q, q, 64, 1, 64)
+
+
+def test_torch_operator_matches_the_direct_c_call_and_compiles(data):
+    """The torch operator and a direct ctypes call of the same entry point write the same bytes; under
+    torch.compile (AOT autograd: functionalisation of the declared writes, fake tensors through the Meta kernel)
+    the compiled function returns the eager result."""
+    import ctypes
+    from self_trainable_or_free_attn_amd import _lib
+    kd, vd = data["kd"], data["vd"]
+    a = [torch.full((NB, H, D), 7.0, device=kd.device, dtype=torch.bfloat16) for _ in range(4)]
+    _lib.ops().es_block_means(kd, vd, a[0], a[1], L, H, D)
+    st = _lib.lib().es_block_means(_lib.ptr(kd), _lib.ptr(vd), _lib.ptr(a[2]), _lib.ptr(a[3]), L, H, D,
+                                   ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st == 0
+    torch.cuda.synchronize()
+    assert torch.equal(a[0].view(torch.int16), a[2].view(torch.int16))
+    assert torch.equal(a[1].view(torch.int16), a[3].view(torch.int16))
+
+    def f(k, v):
+        km = torch.zeros(NB, H, D, device=k.device, dtype=torch.bfloat16)
+        vm = torch.zeros_like(km)
+        torch.ops.echosparse_gfx950.es_block_means(k, v, km, vm, L, H, D)
+        return km.float() * 2.0 + vm.float()
+
+    log("torch.compile(aot_eager) of es_block_means")
+    got = torch.compile(f, backend="aot_eager", fullgraph=True)(kd, vd)
+    torch.cuda.synchronize()
+    assert torch.equal(got, a[0].float() * 2.0 + a[1].float())
 
 
 def test_dense_attention(data, dense):
