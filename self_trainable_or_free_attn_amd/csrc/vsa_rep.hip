@@ -348,13 +348,14 @@ struct TabArgs {
   float scale_log2, scale;
 };
 
-// 64-bit mask of the tier blocks of query-block row i among the workgroup's blocks fb .. fb + nblk - 1
+// 64-bit mask of the tier blocks of query-block row `row` among the workgroup's blocks fb .. fb + nblk - 1 (plain
+// per-thread loads: each thread of a refill looks at its own query block)
 __device__ __forceinline__ unsigned long long tier_mask(const TabArgs& a, size_t row, int fb, int nblk) {
   const int w0 = fb >> 5;
   auto word = [&](int w) -> unsigned long long {
     if (w >= a.W) return 0ull;
-    const unsigned abv = sload(a.bits_ab + row * a.W + w);
-    unsigned m = a.tier == PH_B ? (abv & ~sload(a.bits_a + row * a.W + w)) : ~abv;
+    const unsigned abv = a.bits_ab[row * a.W + w];
+    unsigned m = a.tier == PH_B ? (abv & ~a.bits_a[row * a.W + w]) : ~abv;
     const int lo = w * 32;
     if (a.NB - lo < 32) m &= (1u << (a.NB - lo)) - 1u;
     return m;
@@ -371,6 +372,13 @@ template <int PART>
 __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
   __shared__ __attribute__((aligned(16))) char qd_s[2][2][BK * 256];
   __shared__ __attribute__((aligned(16))) float st_s[2][2][BK];
+  // ring of the query blocks with at least one tier pair among this workgroup's blocks, and their masks, filled
+  // 256 query blocks at a time by the whole workgroup (one mask per thread, ballot compaction), so the loop reads
+  // its next block from LDS instead of scanning the bitmaps block by block
+  constexpr int RING = 512;
+  __shared__ int act_s[RING];
+  __shared__ unsigned long long am_s[RING];
+  __shared__ int wcnt_s[4];
   int grp, bh;
   if (!balanced_head_item(a.queues, a.fixed, a.rows_pad / BK, a.BH, bh, grp)) return;
   const int tid = threadIdx.x, l = tid & 63, hi = l >> 5, lq = l & 31;
@@ -416,13 +424,32 @@ __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
       dl = a.delta[t];
     }
   };
-  // the next query block at or after i with at least one tier pair among this workgroup's blocks
-  auto next_active = [&](int i, unsigned long long& m) -> int {
-    for (; i < a.NB; ++i) {
-      m = tier_mask(a, (size_t)bh * a.NB + i, fb, nblk);
-      if (m != 0ull) return i;
+  int produced = 0, chunk = 0;  // ring entries written so far, query-block chunks (of 256) scanned so far
+  auto refill = [&]() {         // every thread; ends with a barrier
+    const int i = chunk * 256 + tid;
+    const unsigned long long m = i < a.NB ? tier_mask(a, (size_t)bh * a.NB + i, fb, nblk) : 0ull;
+    const unsigned long long bal = __builtin_amdgcn_ballot_w64(m != 0ull);
+    if (l == 0) wcnt_s[wv] = __popcll(bal);
+    __syncthreads();
+    int before = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int c = wcnt_s[w];
+      before += w < wv ? c : 0;
+      total += c;
     }
-    return a.NB;
+    if (m != 0ull) {
+      const int slot = (produced + before + __popcll(bal & ((1ull << l) - 1ull))) & (RING - 1);
+      act_s[slot] = i;
+      am_s[slot] = m;
+    }
+    produced += total;
+    ++chunk;
+    __syncthreads();
+  };
+  // at least `need` entries written, or every query block scanned (wave-uniform)
+  auto ensure = [&](int need) {
+    while (produced < need && chunk * 256 < a.NB) refill();
   };
   int aoff[8];
 #pragma unroll
@@ -441,9 +468,9 @@ __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
   for (int db = 0; db < 4; ++db) dk[db] = dv[db] = f32x16{};
 
   float ls = 0.0f, dl = 0.0f;
-  unsigned long long mcur = 0, mnext = 0;
-  int icur = next_active(0, mcur);
-  int inext = icur < a.NB ? next_active(icur + 1, mnext) : a.NB;
+  ensure(1);
+  int icur = produced > 0 ? act_s[0] : a.NB;
+  unsigned long long mcur = produced > 0 ? am_s[0] : 0ull;
   if (icur < a.NB) {
     issue(icur, 0, ls, dl);
     dma_wait();
@@ -456,12 +483,10 @@ __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
   __syncthreads();
   for (int j = 0; icur < a.NB; ++j) {
     const int sb = j & 1;
-    unsigned long long mnn = 0;
-    int inn = a.NB;
-    if (inext < a.NB) {
-      issue(inext, sb ^ 1, ls, dl);
-      inn = next_active(inext + 1, mnn);
-    }
+    ensure(j + 2);  // (entries j and j + 1 stay in the ring: a refill writes at most 256 past the last one)
+    const int inext = j + 1 < produced ? act_s[(j + 1) & (RING - 1)] : a.NB;
+    const unsigned long long mnext = j + 1 < produced ? am_s[(j + 1) & (RING - 1)] : 0ull;
+    if (inext < a.NB) issue(inext, sb ^ 1, ls, dl);
     // this lane's key: bias log2(c) when its block's pair with query block icur is in the tier, else -inf
     const float kb = ((mcur >> lblk) & 1ull) ? kbias : -INFINITY;
     const char* qt = qd_s[sb][0];
@@ -504,8 +529,6 @@ __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
     __syncthreads();
     icur = inext;
     mcur = mnext;
-    inext = inn;
-    mnext = mnn;
   }
 
   f32x16* acc = PART == 1 ? dv : dk;
