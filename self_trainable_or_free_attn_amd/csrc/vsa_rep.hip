@@ -570,39 +570,44 @@ __global__ __launch_bounds__(256) void rep_unpool_kernel(const float* __restrict
   const size_t bh = blockIdx.y;
   const int cnt = blk_cnt[blk], gs = BK / RM;
   const float invc = 1.0f / (float)cnt;
+  // the block-mean gradient is the same for every token of the block: loaded once, already divided by the count
   const size_t tail = (bh * tail_rows + blk) * HD + c8;
+  f32x4 tk[2], tv[2];
+#pragma unroll
+  for (int h2 = 0; h2 < 2; ++h2) {
+    tk[h2] = *reinterpret_cast<const f32x4*>(dk_tail + tail + 4 * h2) * invc;
+    tv[h2] = *reinterpret_cast<const f32x4*>(dv_tail + tail + 4 * h2) * invc;
+  }
+  const bool has_k = acc_k != nullptr, has_v = acc_v != nullptr;
+  auto pack = [](const f32x4& x0, const f32x4& x1) {
+    uint4 u;
+    u.x = (unsigned)f2e(x0[0]) | ((unsigned)f2e(x0[1]) << 16);
+    u.y = (unsigned)f2e(x0[2]) | ((unsigned)f2e(x0[3]) << 16);
+    u.z = (unsigned)f2e(x1[0]) | ((unsigned)f2e(x1[1]) << 16);
+    u.w = (unsigned)f2e(x1[2]) | ((unsigned)f2e(x1[3]) << 16);
+    return u;
+  };
+#pragma unroll 4
   for (int r = s; r < BK; r += 4) {
-    const size_t tok = (bh * L + (size_t)blk * BK + r) * HD + c8;
-    // the token's representative: its contiguous group, or (k-means tables) its cluster
     const size_t lrow = bh * L + (size_t)blk * BK + r;
-    const int g = labels ? (r < cnt ? (int)labels[lrow] : 0) : r / gs;
-    const int n = labels ? mid_counts[(bh * NB + blk) * RM + g] : min(max(cnt - g * gs, 0), gs);
-    const size_t mid = (bh * mid_rows + (size_t)blk * RM + g) * HD + c8;
-    float xk[8], xv[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      xk[e] = 0.0f;
-      xv[e] = 0.0f;
-    }
+    const size_t tok = lrow * HD + c8;
+    f32x4 xk[2] = {f32x4{}, f32x4{}}, xv[2] = {f32x4{}, f32x4{}};
     if (r < cnt) {
+      // the token's representative: its contiguous group, or (k-means tables) its cluster
+      const int g = labels ? (int)labels[lrow] : r / gs;
+      const int n = labels ? mid_counts[(bh * NB + blk) * RM + g] : min(max(cnt - g * gs, 0), gs);
       const float invg = 1.0f / (float)n;
+      const size_t mid = (bh * mid_rows + (size_t)blk * RM + g) * HD + c8;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        xk[e] = (acc_k ? acc_k[tok + e] : 0.0f) + dk_mid[mid + e] * invg + dk_tail[tail + e] * invc;
-        xv[e] = (acc_v ? acc_v[tok + e] : 0.0f) + dv_mid[mid + e] * invg + dv_tail[tail + e] * invc;
+      for (int h2 = 0; h2 < 2; ++h2) {  // (acc + mid / n) + tail / c, in that order
+        const f32x4 ak = has_k ? *reinterpret_cast<const f32x4*>(acc_k + tok + 4 * h2) : f32x4{};
+        const f32x4 av = has_v ? *reinterpret_cast<const f32x4*>(acc_v + tok + 4 * h2) : f32x4{};
+        xk[h2] = (ak + *reinterpret_cast<const f32x4*>(dk_mid + mid + 4 * h2) * invg) + tk[h2];
+        xv[h2] = (av + *reinterpret_cast<const f32x4*>(dv_mid + mid + 4 * h2) * invg) + tv[h2];
       }
     }
-    uint4 uk, uv;
-    uk.x = (unsigned)f2e(xk[0]) | ((unsigned)f2e(xk[1]) << 16);
-    uk.y = (unsigned)f2e(xk[2]) | ((unsigned)f2e(xk[3]) << 16);
-    uk.z = (unsigned)f2e(xk[4]) | ((unsigned)f2e(xk[5]) << 16);
-    uk.w = (unsigned)f2e(xk[6]) | ((unsigned)f2e(xk[7]) << 16);
-    uv.x = (unsigned)f2e(xv[0]) | ((unsigned)f2e(xv[1]) << 16);
-    uv.y = (unsigned)f2e(xv[2]) | ((unsigned)f2e(xv[3]) << 16);
-    uv.z = (unsigned)f2e(xv[4]) | ((unsigned)f2e(xv[5]) << 16);
-    uv.w = (unsigned)f2e(xv[6]) | ((unsigned)f2e(xv[7]) << 16);
-    *reinterpret_cast<uint4*>(dk + tok) = uk;
-    *reinterpret_cast<uint4*>(dv + tok) = uv;
+    *reinterpret_cast<uint4*>(dk + tok) = pack(xk[0], xk[1]);
+    *reinterpret_cast<uint4*>(dv + tok) = pack(xv[0], xv[1]);
   }
 }
 
