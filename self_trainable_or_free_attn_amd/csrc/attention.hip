@@ -397,7 +397,44 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
   // exact block id of chunk j + 1, read from the ring one chunk early so that the LDS latency of the read is
   // spent under the previous chunk's compute rather than in front of the next transfers
   int pre_v = (nc > 1 && 1 < n && g_ex != nullptr) ? ids_s[1][0] : 1;
-  for (int j = 0; j < nc; ++j) {
+  int j = 0;
+  // the exact-block stretch of a listed stream (chunks j .. j + 3 all exact blocks): the same steps as the general
+  // loop below with the chunk kinds known, so none of its kind tests and list-source selections run per chunk
+  if (MODE == FIXED && g_ex != nullptr) {
+    const srd_t rex = make_srd(g_ex, (unsigned)n * 4u);
+    for (; j + 3 < n; ++j) {
+      const int sb = j & 1;
+      const int next_row = __builtin_amdgcn_readfirstlane(pre_v);
+      const int b0 = next_row * BK;
+      Dma dn;
+      dn.rk = block_srd(a.k, b0);
+      dn.rv = block_srd(a.v, b0);
+      dn.soff = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dn.off[i] = tok_off[i];
+      dma_k(dn, sb ^ 1);
+      dma_v(dn, sb ^ 1);
+      if (wv == 0) dma4(rex, ids_s[(j + 3) & 3], 0, (unsigned)(j + 3) * 4u);
+      pre_v = ids_s[(j + 2) & 3][0];
+      const bool biased = tail_block && cur_row == nb - 1;
+      if (!COMP || biased)
+        compute(j, sb, std::true_type{});
+      else
+        compute(j, sb, std::false_type{});
+      dma_wait();
+      if (wv == 0) bias_s[sb ^ 1][l] = b0 + l < a.Lk ? 0.0f : -INFINITY;
+      __syncthreads();
+      if (MASS && ((j & 63) == 63) && tid < 64) {
+        const int idx = (j & ~63) + tid;
+        float m = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) m += mass_s[r][idx & 127];
+        a.mass[((size_t)h * a.nq + t) * nb + g_ex[idx]] = m;
+      }
+      cur_row = next_row;
+    }
+  }
+  for (; j < nc; ++j) {
     const int sb = j & 1;
     float bnext = 0.0f;
     int next_row = 0;
