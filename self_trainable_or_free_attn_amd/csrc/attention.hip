@@ -398,11 +398,13 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
   // spent under the previous chunk's compute rather than in front of the next transfers
   int pre_v = (nc > 1 && 1 < n && g_ex != nullptr) ? ids_s[1][0] : 1;
   int j = 0;
-  // the exact-block stretch of a listed stream (chunks j .. j + 3 all exact blocks): the same steps as the general
-  // loop below with the chunk kinds known, so none of its kind tests and list-source selections run per chunk
+  // the exact-block stretch of a listed stream (chunks j .. j + 3 all exact blocks, chunk j not the partial last
+  // token block, which a sorted list holds last if at all): the same steps as the general loop below with the chunk
+  // kinds known, so none of its kind tests and list-source selections run per chunk, and one compute variant
   if (MODE == FIXED && g_ex != nullptr) {
     const srd_t rex = make_srd(g_ex, (unsigned)n * 4u);
-    for (; j + 3 < n; ++j) {
+    cur_row = __builtin_amdgcn_readfirstlane(cur_row);  // (wave-uniform: keeps the loop test scalar)
+    for (; j + 3 < n && !(tail_block && cur_row == nb - 1); ++j) {
       const int sb = j & 1;
       const int next_row = __builtin_amdgcn_readfirstlane(pre_v);
       const int b0 = next_row * BK;
@@ -416,8 +418,7 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
       dma_v(dn, sb ^ 1);
       if (wv == 0) dma4(rex, ids_s[(j + 3) & 3], 0, (unsigned)(j + 3) * 4u);
       pre_v = ids_s[(j + 2) & 3][0];
-      const bool biased = tail_block && cur_row == nb - 1;
-      if (!COMP || biased)
+      if (!COMP)
         compute(j, sb, std::true_type{});
       else
         compute(j, sb, std::false_type{});
