@@ -404,6 +404,7 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
   if (MODE == FIXED && g_ex != nullptr) {
     const srd_t rex = make_srd(g_ex, (unsigned)n * 4u);
     cur_row = __builtin_amdgcn_readfirstlane(cur_row);  // (wave-uniform: keeps the loop test scalar)
+    const unsigned kv_lds = uni(lds_addr(kv_s[0][0]) + (unsigned)wv * 4096u);
     for (; j + 3 < n && !(tail_block && cur_row == nb - 1); ++j) {
       const int sb = j & 1;
       const int next_row = __builtin_amdgcn_readfirstlane(pre_v);
@@ -414,8 +415,13 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
       dn.soff = 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) dn.off[i] = tok_off[i];
-      dma_k(dn, sb ^ 1);
-      dma_v(dn, sb ^ 1);
+      {
+        const unsigned kd = kv_lds + (unsigned)(sb ^ 1) * (2u * BK * 256u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dma16_at(dn.rk, kd + i * 1024, dn.off[i], 0u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dma16_at(dn.rv, kd + BK * 256 + i * 1024, dn.off[i], 0u);
+      }
       if (wv == 0) dma4(rex, ids_s[(j + 3) & 3], 0, (unsigned)(j + 3) * 4u);
       pre_v = ids_s[(j + 2) & 3][0];
       if (!COMP)
@@ -423,7 +429,8 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
       else
         compute(j, sb, std::false_type{});
       dma_wait();
-      if (wv == 0) bias_s[sb ^ 1][l] = b0 + l < a.Lk ? 0.0f : -INFINITY;
+      // (the compensated variants read the bias of an exact chunk only for the partial last block)
+      if (wv == 0 && (!COMP || (tail_block && next_row == nb - 1))) bias_s[sb ^ 1][l] = b0 + l < a.Lk ? 0.0f : -INFINITY;
       __syncthreads();
       if (MASS && ((j & 63) == 63) && tid < 64) {
         const int idx = (j & ~63) + tid;

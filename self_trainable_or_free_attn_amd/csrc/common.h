@@ -115,6 +115,14 @@ __device__ __forceinline__ void dma16(srd_t r, const void* lds_base, unsigned vo
                : "memory");
 }
 
+// dma16 with the LDS destination given as a 32-bit LDS address (no pointer conversion)
+__device__ __forceinline__ void dma16_at(srd_t r, unsigned lds, unsigned voff, unsigned soff) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(uni(r)), "s"(uni(soff)), "{m0}"(uni(lds))
+               : "memory");
+}
+
 // every lane moves 4 bytes at srd + voff + soff to lds_base + 4 * lane
 __device__ __forceinline__ void dma4(srd_t r, const void* lds_base, unsigned voff, unsigned soff) {
   asm volatile("buffer_load_dword %0, %1, %2 offen lds"
