@@ -156,9 +156,14 @@ class EchoSparseAttention:
         self._plan_scratch = None
         self._plan_stream = None        # branch 0's next-step selection runs here, overlapping later work
         self.overlap_selection = True   # False: the selection runs on the caller's stream (A/B measurements)
+        # True: branch 0's selection is enqueued when the next call launches its sparse attention (and starts with
+        # it), so it shares the GPU with that long kernel instead of with the next branch's representative build
+        self.defer_selection = True
         self._plan_done = None          # event after the last selection's kernels
+        self._pending = None            # a deferred selection: (enqueue function, event it must follow)
 
     def reset(self):
+        self._flush_selection()
         for st in self._states.values():
             st.ready.clear()
             st.current = st.pending = None
@@ -178,9 +183,19 @@ class EchoSparseAttention:
             return dense_attention(q, k, v)
         return self._call_compact(q, k, v, step, branch, layer, sink, rows)
 
+    def _flush_selection(self, start=None):
+        """Enqueue a deferred selection on the plan stream, after the event its inputs were ready at and, if given,
+        after `start` (recorded on the caller's stream just before a sparse-attention launch)."""
+        if self._pending is None:
+            return
+        enqueue, ready = self._pending
+        self._pending = None
+        enqueue(ready, start)
+
     def _join_plan(self):
         """Order the current stream after the last selection issued on the plan stream (before anything that
         writes what it reads: the plan scratch, branch 0's block means, flags and offset)."""
+        self._flush_selection()
         if self._plan_done is not None:
             torch.cuda.current_stream().wait_event(self._plan_done)
             self._plan_done = None
@@ -254,10 +269,15 @@ class EchoSparseAttention:
             buf.reps.build(q, k, v, k_mean, v_mean)
             if branch == 0:
                 ps.mass.zero_()
+            start = None
+            if self._pending is not None:
+                start = torch.cuda.Event()
+                start.record()
             K.sparse_attention(q, k, v, k_mean, v_mean, ps.means, ps.mean_counts, out, ps.counts, ps.blocks,
                                offset, nxt, flags, ps.refine, ps.refine_counts, buf.reps.k, buf.reps.v,
                                buf.reps.log_counts, mass=ps.mass if branch == 0 else None, threshold=self.threshold,
                                rows=rows)
+            self._flush_selection(start)
             K.exact_fallback(q, k, v, out, ps.counts, ps.blocks, nxt, flags)
             K.compensate_fallback(q, k_mean, v_mean, ps.keep, nxt, out, flags)
         if branch != 0:
@@ -270,17 +290,29 @@ class EchoSparseAttention:
         if self._plan_stream is None and self.overlap_selection:
             self._plan_stream = torch.cuda.Stream(device=q.device)
         side = self._plan_stream if self.overlap_selection else main
-        side.wait_stream(main)
-        q.record_stream(side)
-        with torch.cuda.stream(side):
-            if sparse:
-                K.estimate_skipped(q, k_mean, ps.keep, offset, nxt, ps.mass, ps.scale_exact, ps.scale_skip)
-            K.select_blocks(ps.mass, ps.keep, ps.scale_exact, ps.scale_skip, ps.next_keep, ps.sel_counts,
-                            ps.sel_blocks, flags, skip, ps.sel_refine, top, refined, L,
-                            sink=1 << 30 if sink is None else sink)
-            K.pack_plan(ps.next_keep, exact)
-            offset.copy_(nxt)
-            self._plan_done = torch.cuda.Event()
-            self._plan_done.record(side)
+
+        def enqueue(ready, start):
+            # (holds q until its kernels are enqueued; record_stream keeps its memory until they have run)
+            for ev in (ready, start):
+                if ev is not None:
+                    side.wait_event(ev)
+            q.record_stream(side)
+            with torch.cuda.stream(side):
+                if sparse:
+                    K.estimate_skipped(q, k_mean, ps.keep, offset, nxt, ps.mass, ps.scale_exact, ps.scale_skip)
+                K.select_blocks(ps.mass, ps.keep, ps.scale_exact, ps.scale_skip, ps.next_keep, ps.sel_counts,
+                                ps.sel_blocks, flags, skip, ps.sel_refine, top, refined, L,
+                                sink=1 << 30 if sink is None else sink)
+                K.pack_plan(ps.next_keep, exact)
+                offset.copy_(nxt)
+                self._plan_done = torch.cuda.Event()
+                self._plan_done.record(side)
+
+        ready = torch.cuda.Event()
+        ready.record(main)
+        if self.defer_selection and self.overlap_selection:
+            self._pending = (enqueue, ready)
+        else:
+            enqueue(ready, None)
         st.pending = (plan, step + 1)
         return out[None]

@@ -35,12 +35,14 @@ def run(attn, inputs, branches=1, layer=1):
     for step, (q, k, v) in enumerate(inputs):
         for branch in range(branches):
             outs.append(attn(q, k, v, step, branch, layer=layer))
-    torch.cuda.synchronize()      # branch 0's selection runs on a side stream: settle it before reading state
+    attn._flush_selection()       # a deferred selection is enqueued now,
+    torch.cuda.synchronize()      # and settled (it runs on a side stream) before any state is read
     return outs
 
 
 def call_with_selection(attn, q, k, v, step, branch=0, layer=1):
     """One sparse call; returns its output and the block selection it used (counts, blocks, refine list)."""
+    attn._flush_selection()
     torch.cuda.synchronize()
     st = attn._states[layer]
     exact, skip = (x.clone() for x in st.plan(st.pending[0] if branch == 0 else st.current[0]))
@@ -183,6 +185,7 @@ def test_rows_skip_only_unused_tiles():
     st, ps, buf = attn._states[1], None, attn._buffers
     exact, skip = st.plan(st.pending[0])
     attn(*inputs[2], 2, 0, layer=1)          # builds scratch and representatives for this shape
+    attn._flush_selection()
     torch.cuda.synchronize()
     ps = attn._plan_scratch
     K.rebuild_plan(exact, skip, ps.keep, ps.counts, ps.blocks, ps.refine, ps.refine_counts, ps.means,

@@ -34,6 +34,7 @@ def test_sparse_step_full_shape_sampled_tiles(dev):
     for step in range(2):
         attn(prev[0][None], prev[1][None], prev[2][None], step, 0, 1)
     attn(q[None], k[None], v[None], 2, 0, 1)
+    attn._flush_selection()
     torch.cuda.synchronize()
     K, ps, buf, st = attn.K, attn._plan_scratch, attn._buffers, attn._states[1]
     L = q.shape[0]
