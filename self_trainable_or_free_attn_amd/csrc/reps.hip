@@ -134,13 +134,16 @@ __global__ __launch_bounds__(256) void gram_reduce_kernel(float* __restrict__ gr
   g[0] = s;
 }
 
-__global__ __launch_bounds__(256) void chol_kernel(const float* __restrict__ gram, bf16_t* __restrict__ metric_t,
-                                                   int splits, float gscale) {
+constexpr int CHOL_T = 1024;                 // threads of the Cholesky workgroup
+constexpr int CHOL_R = HD * HD / CHOL_T;     // rows of one column per thread
+
+__global__ __launch_bounds__(CHOL_T) void chol_kernel(const float* __restrict__ gram, bf16_t* __restrict__ metric_t,
+                                                      int splits, float gscale) {
   __shared__ float A[HD][HD + 1];
-  __shared__ float red[4];
+  __shared__ float red[CHOL_T / 64];
   const int h = blockIdx.x, tid = threadIdx.x;
   // the split partials were summed into split 0 by gram_reduce_kernel
-  for (int i = tid; i < HD * HD; i += 256) A[i / HD][i % HD] = gram[(size_t)h * splits * HD * HD + i] * gscale;
+  for (int i = tid; i < HD * HD; i += CHOL_T) A[i / HD][i % HD] = gram[(size_t)h * splits * HD * HD + i] * gscale;
   __syncthreads();
   float dsum = tid < HD ? A[tid][tid] : 0.0f;
   dsum = wave_sum(dsum);
@@ -156,23 +159,24 @@ __global__ __launch_bounds__(256) void chol_kernel(const float* __restrict__ gra
   __syncthreads();
   const float eps = (red[0] + red[1]) / (float)HD * 1e-12f;
   bf16_t* mt = metric_t + (size_t)h * HD * HD;
-  // Register-resident right-looking factorisation: thread (cc = tid % 128, half = tid / 128) holds column cc at
-  // rows 64 half .. 64 half + 63. Step j: the owners of column j publish it into column buffer j % 2 (16-byte
-  // LDS writes) with its rows above j as zeros, one barrier, then every thread reads the pivot column with 16-byte
+  // Register-resident right-looking factorisation: thread (cc = tid % 128, part = tid / 128) holds column cc at
+  // rows 16 part .. 16 part + 15 (1024 threads, so a step's own arithmetic is short against its barrier and LDS
+  // round trip). Step j: the owners of column j publish it into column buffer j % 2 (16-byte LDS writes) with its
+  // rows above j as zeros, one barrier, then every thread reads the pivot column with 16-byte
   // broadcast reads and subtracts the rank-1 update col * (col[cc] / pivot) from its own entries: the zeros leave
   // the finished rows alone, and the columns left of j (already published) are never read again, so no entry
   // needs a mask. (Two buffers: step j+1 writes the other one while step j's readers may still be reading.)
-  const int cc = tid & (HD - 1), rb = 64 * (tid >> 7);
-  float a[64];
+  const int cc = tid & (HD - 1), rb = CHOL_R * (tid >> 7);
+  float a[CHOL_R];
 #pragma unroll
-  for (int i = 0; i < 64; ++i) a[i] = A[rb + i][cc];
+  for (int i = 0; i < CHOL_R; ++i) a[i] = A[rb + i][cc];
   __syncthreads();
   float* colbuf = &A[0][0];  // the matrix now lives in registers; reuse the LDS as two column buffers
   for (int j = 0; j < HD; ++j) {
     float* cb = colbuf + (j & 1) * HD;
     if (cc == j) {
 #pragma unroll
-      for (int q4 = 0; q4 < 16; ++q4) {
+      for (int q4 = 0; q4 < CHOL_R / 4; ++q4) {
         f32x4 c4;
 #pragma unroll
         for (int k = 0; k < 4; ++k) c4[k] = rb + 4 * q4 + k >= j ? a[4 * q4 + k] : 0.0f;
@@ -184,7 +188,7 @@ __global__ __launch_bounds__(256) void chol_kernel(const float* __restrict__ gra
     const float sc = cb[cc] * (inv * inv);
     if (tid < HD) mt[j * HD + tid] = f2bf(cb[tid] * inv);  // metric_t[j][d] = Lchol[d][j] (zero above j)
 #pragma unroll
-    for (int q4 = 0; q4 < 16; ++q4) {
+    for (int q4 = 0; q4 < CHOL_R / 4; ++q4) {
       const f32x4 c4 = *reinterpret_cast<const f32x4*>(cb + rb + 4 * q4);
 #pragma unroll
       for (int k = 0; k < 4; ++k) a[4 * q4 + k] = fmaf(-c4[k], sc, a[4 * q4 + k]);
@@ -617,7 +621,7 @@ static void run_representatives(const void* q, const void* k, const void* v, voi
   hipLaunchKernelGGL(gram_kernel, dim3(w.splits, H), dim3(256), 0, stream, (const bf16_t*)q, w.gram, L, H,
                      w.rows_per_split, w.splits);
   hipLaunchKernelGGL(gram_reduce_kernel, dim3(HD * HD / 256, H), dim3(256), 0, stream, w.gram, w.splits);
-  hipLaunchKernelGGL(chol_kernel, dim3(H), dim3(256), 0, stream, w.gram, w.metric_t, w.splits,
+  hipLaunchKernelGGL(chol_kernel, dim3(H), dim3(CHOL_T), 0, stream, w.gram, w.metric_t, w.splits,
                      scale * scale / (float)L);
   hipLaunchKernelGGL(probe_kernel, dim3(NPROBE, H), dim3(64), 0, stream, (const bf16_t*)q, w.probes, L, H, nb,
                      scale);
