@@ -401,13 +401,15 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
   // the exact-block stretch of a listed stream (chunks j .. j + 3 all exact blocks, chunk j not the partial last
   // token block, which a sorted list holds last if at all): the same steps as the general loop below with the chunk
   // kinds known, so none of its kind tests and list-source selections run per chunk, and one compute variant
-  if (MODE == FIXED && g_ex != nullptr) {
-    const srd_t rex = make_srd(g_ex, (unsigned)n * 4u);
+  // (also the dense and full-block launches, whose block of chunk j is j itself)
+  if (MODE != COMPENSATE && (MODE == ONLINE || g_ex != nullptr)) {
+    const bool listed = MODE == FIXED || g_ex != nullptr;  // (a constant for the FIXED variants)
+    const srd_t rex = make_srd(g_ex, listed ? (unsigned)n * 4u : 0u);
     cur_row = __builtin_amdgcn_readfirstlane(cur_row);  // (wave-uniform: keeps the loop test scalar)
     const unsigned kv_lds = uni(lds_addr(kv_s[0][0]) + (unsigned)wv * 4096u);
     for (; j + 3 < n && !(tail_block && cur_row == nb - 1); ++j) {
       const int sb = j & 1;
-      const int next_row = __builtin_amdgcn_readfirstlane(pre_v);
+      const int next_row = listed ? __builtin_amdgcn_readfirstlane(pre_v) : j + 1;
       const int b0 = next_row * BK;
       Dma dn;
       dn.rk = block_srd(a.k, b0);
@@ -422,22 +424,24 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
 #pragma unroll
         for (int i = 0; i < 4; ++i) dma16_at(dn.rv, kd + BK * 256 + i * 1024, dn.off[i], 0u);
       }
-      if (wv == 0) dma4(rex, ids_s[(j + 3) & 3], 0, (unsigned)(j + 3) * 4u);
-      pre_v = ids_s[(j + 2) & 3][0];
+      if (listed && wv == 0) dma4(rex, ids_s[(j + 3) & 3], 0, (unsigned)(j + 3) * 4u);
+      pre_v = listed ? ids_s[(j + 2) & 3][0] : j + 2;  // (the general loop below starts from it)
+      online_biased = false;
       if (!COMP)
         compute(j, sb, std::true_type{});
       else
         compute(j, sb, std::false_type{});
       dma_wait();
-      // (the compensated variants read the bias of an exact chunk only for the partial last block)
-      if (wv == 0 && (!COMP || (tail_block && next_row == nb - 1))) bias_s[sb ^ 1][l] = b0 + l < a.Lk ? 0.0f : -INFINITY;
+      // (the compensated and online variants read the bias of an exact chunk only for the partial last block)
+      if (wv == 0 && ((MODE == FIXED && !COMP) || (tail_block && next_row == nb - 1)))
+        bias_s[sb ^ 1][l] = b0 + l < a.Lk ? 0.0f : -INFINITY;
       __syncthreads();
       if (MASS && ((j & 63) == 63) && tid < 64) {
         const int idx = (j & ~63) + tid;
         float m = 0.0f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) m += mass_s[r][idx & 127];
-        a.mass[((size_t)h * a.nq + t) * nb + g_ex[idx]] = m;
+        a.mass[((size_t)h * a.nq + t) * nb + (listed ? g_ex[idx] : idx)] = m;
       }
       cur_row = next_row;
     }
