@@ -446,7 +446,8 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
       cur_row = next_row;
     }
   }
-  for (; j < nc; ++j) {
+  // one chunk of any kind (the general step)
+  auto general_step = [&](int j) {
     const int sb = j & 1;
     float bnext = 0.0f;
     int next_row = 0;
@@ -484,7 +485,43 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
       }
     }
     cur_row = next_row;
+    };
+  if (MODE == FIXED && COMP) {
+    for (; j < nc && !(j >= n + cm && j + 3 < nc); ++j) general_step(j);
+    // the representative stretch (chunks j .. j + 3 all representative columns): the same steps with the kind known
+    const srd_t rlc = make_srd(a.log_counts + (size_t)h * nb4, (unsigned)nb4 * 4u);
+    const srd_t rrf = make_srd(g_rf, (unsigned)nr * 4u);
+    const unsigned kv_lds = uni(lds_addr(kv_s[0][0]) + (unsigned)wv * 4096u);
+    for (; j + 3 < nc; ++j) {
+      const int sb = j & 1;
+      const int* src = ids_s[(j + 1) & 3];
+      const int c0 = (j + 1 - n - cm) * BK;
+      unsigned off[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int col = c0 + rbase + 4 * i;
+        off[i] = col < 4 * nr ? (unsigned)(src[rbase + 4 * i] * 4 + (col & 3)) * (HD * 2) + chb[i] : 0x80000000u;
+      }
+      int brow = -1;
+      if (wv == 0) {
+        brow = c0 + l < 4 * nr ? src[l] * 4 + ((c0 + l) & 3) : -1;
+        dma4(rlc, lc_s, brow < 0 ? 0x80000000u : (unsigned)brow * 4u, 0u);
+      }
+      {
+        const unsigned kd = kv_lds + (unsigned)(sb ^ 1) * (2u * BK * 256u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dma16_at(rkr, kd + i * 1024, off[i], 0u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dma16_at(rvr, kd + BK * 256 + i * 1024, off[i], 0u);
+      }
+      if (wv == 0) dma4(rrf, ids_s[(j + 3) & 3], (unsigned)((((j + 3 - n - cm) * BK + l) >> 2) * 4), 0u);
+      compute(j, sb, std::true_type{});
+      dma_wait();
+      if (wv == 0) bias_s[sb ^ 1][l] = brow >= 0 ? lc_s[l] : -INFINITY;
+      __syncthreads();
+    }
   }
+  for (; j < nc; ++j) general_step(j);
 
   // ---------------------------------------------------------------- epilogue
   const float tot = lsum + __shfl_xor(lsum, 32, 64);
