@@ -368,8 +368,9 @@ def test_fallback_and_compensation(data, plan, reps, dev):
 
 def test_sparse_attention_stream_edges(data, plan, reps, dev):
     """Column streams that start with representative or mean chunks, a stream of 65 exact blocks (mass flush
-    after block 63 and at the end), one chunk of each kind, against the oracle on the same lists: exercises the
-    kernel's staged list ring and its first-chunk bias paths."""
+    after block 63 and at the end), one chunk of each kind, unsorted exact lists with the partial tail block first
+    or in the middle, lists of 4 and 5 exact blocks, against the oracle on the same lists: exercises the kernel's
+    staged list ring, its first-chunk bias paths and the bounds of its exact-stretch loop."""
     p = plan
     R, km, vm = reps
     t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
@@ -382,6 +383,17 @@ def test_sparse_attention_stream_edges(data, plan, reps, dev):
     blocks[2, 0, :NB] = np.arange(NB)
     counts[3, 1], mc[3, 1], rc[3, 1] = 1, 1, 1            # one chunk of each kind, the tail block exact
     blocks[3, 1, 0], means[3, 1, 0], refine[3, 1, 0] = NB - 1, 0, 2
+    # unsorted lists around the kernel's exact-stretch loop (chunks j .. j + 3 exact, chunk j not the tail block):
+    # every block in descending order (the partial tail block first), the tail block in the middle of a list, and
+    # lists of exactly 4 and 5 blocks
+    counts[4, 0] = NB
+    blocks[4, 0, :NB] = np.arange(NB)[::-1]
+    counts[5, 1] = 20
+    blocks[5, 1, :20] = [3, 10, 17, 24, 31, 38, 45, NB - 1, 1, 12, 23, 34, 56, 14, 25, 36, 47, 58, 0, 2]
+    counts[6, 0] = 4
+    blocks[6, 0, :4] = [0, 5, 9, NB - 1]
+    counts[7, 1] = 5
+    blocks[7, 1, :5] = [NB - 1, 2, 30, 31, 40]
     offset = t(p["lse"])
     out = torch.full_like(data["qd"], 7.0)
     lse = torch.full((NQ * 128, H), 7.0, device=dev)
