@@ -95,6 +95,20 @@ __global__ __launch_bounds__(256) void estimate_kernel(const bf16_t* __restrict_
     bf16x8 bc[8];
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) bc[ks] = bn[ks];
+    // this chunk's keep flags and current map values, loaded before the products so that their latency is spent
+    // under them (the map holds the exact blocks' masses from the attention, read for the kept blocks), and before
+    // the next chunk's operands, so that waiting for them leaves those in flight
+    uint8_t kp[4] = {1, 1, 1, 1};
+    float mv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (hi == 0 && kvalid) {
+#pragma unroll
+      for (int tl = 0; tl < 4; ++tl) {
+        if (t0 + tl >= nq) continue;
+        const size_t o = ((size_t)h * nq + t0 + tl) * NB + key;
+        kp[tl] = keep[o];
+        mv[tl] = map[o];
+      }
+    }
     if (c + 4 < nchunks) load_b(c + 4, bn);
     f32x16 acc[2] = {f32x16{}, f32x16{}};
 #pragma unroll
@@ -120,10 +134,10 @@ __global__ __launch_bounds__(256) void estimate_kernel(const bf16_t* __restrict_
         if (tt >= nq) continue;
         const float e = est[tl] / fmaxf((float)nsv[tl], 1.0f);
         const size_t o = ((size_t)h * nq + tt) * NB + key;
-        if (keep[o] == 0) {
+        if (kp[tl] == 0) {
           map[o] = e;
         } else {
-          num[tl] += map[o];
+          num[tl] += mv[tl];
           den[tl] += e;
         }
       }
