@@ -1,6 +1,6 @@
 """Headline benchmark: the EchoSparse sparse step on one MI355X at the Wan2.1-14B shape.
 
-Workload: per layer two CFG branch calls (B = 2), H = 40, D = 128, bf16, tokens on a
+Workload (the Wan2.1-14B sparse-step configuration): per layer two CFG branch calls (B = 2), H = 40, D = 128, bf16, tokens on a
 21 x 45 x 80 latent grid (L = 75 600, 1182 kv blocks of 64, 591 query tiles of 128), Morton order; Q / K a
 low-frequency random Fourier field plus 0.3 N(0, 1), scaled per head so the mean row-softmax entropy is 20 % of
 ln L; V ~ N(0, 1). The previous step's LSE comes from a dense pass on inputs perturbed by 1 % Gaussian noise, and a
@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--c4", default="baseline", choices=["baseline", "reference"],
-                    help="vsa2_rep tier construction: BASELINE config 4's (per-query-block tiers, seeded 5-round "
+                    help="vsa2_rep tier construction: the benchmark's (per-query-block tiers, seeded 5-round "
                          "k-means tables) or the reference's (global budgets, contiguous group means)")
     ap.add_argument("--split-policy", default="manual", choices=["manual", "auto"],
                     help="split workload: SplitKV(chunk=64) (every list over 64 blocks) or SplitKV.auto()")

@@ -181,7 +181,7 @@ int vsa_split_merge_sum(const float* part, const int* merges, const int* info, i
 int vsa_rep_build(const void* k, const void* v, const int* blk_cnt, void* k_mid, void* v_mid, float* lc_mid,
                   void* k_tail, void* v_tail, float* lc_tail, int BH, int L, int D, int RM, hipStream_t stream);
 
-/* Seeded k-means tier-B tables (no reference counterpart, whose tables are contiguous means):
+/* Seeded k-means tier-B tables (the three-tier benchmark construction; no reference counterpart, whose tables are contiguous means):
  * every block's valid keys clustered into RM groups by `iters` Lloyd rounds from seed tokens drawn with `seed`;
  * k_mid / v_mid rows (blk * RM + c, as vsa_rep_build) = the clusters' key / value means (zero when empty),
  * lc_mid / counts [BH, NB * RM] per head = log2 cluster sizes (-inf when empty) / sizes, labels [BH, L] uint8 =
@@ -191,7 +191,7 @@ int vsa_rep_build_kmeans(const void* k, const void* v, const int* blk_cnt, void*
                          int* counts, uint8_t* labels, int BH, int L, int D, int RM, int iters, unsigned seed,
                          hipStream_t stream);
 
-/* Per-query-block tiers (BASELINE config 4's split; the reference splits by global budgets, rep_api.cpp
+/* Per-query-block tiers (the three-tier benchmark construction's split; the reference splits by global budgets, rep_api.cpp
  * route_tiers): for every row i of the fp32 scores [bh_count, NB, NB] of (b, h) rows bh0.., the ka (tier A) and
  * kab (tiers A and B) best blocks, score desc, ties to the smaller index, -0 == +0, as ascending CSR lists with
  * offsets (bh * NB + i) * K and as selection bitmaps [BH, NB, ceil(NB / 32)]. 0 <= ka <= kab <= NB <= 2048. */

@@ -402,7 +402,7 @@ def fine_attention_blocks(q, k, v, blk_cnt, ptr, idx, bh, qblocks):
 
 # --------------------------------------------------------------------- seeded k-means representative tables
 # Not in the reference (its tables are contiguous group means, vsa2_rep/reference.py:23-50); this is the
-# construction BASELINE.json's config 4 names ("tables built from seeded k-means, 5 iterations"), defined here and
+# construction the HunyuanVideo-shape three-tier benchmark names ("tables built from seeded k-means, 5 iterations"), defined here and
 # built by vsa_rep_build_kmeans. The arithmetic is float32 in a fixed order with no fused multiply-add, so the GPU
 # tables, counts and labels equal these bit for bit.
 _M32 = 0xFFFFFFFF
@@ -493,7 +493,7 @@ def kmeans_tables(k, v, blk_cnt, RM, iters=5, seed=0, rnd=round_bf16, bh0=0, blk
 
 
 def row_tiers(scores, ka, kab):
-    """Per-query-block tier split (BASELINE.json config 4's wording; the reference splits by two global budgets,
+    """Per-query-block tier split (the three-tier benchmark's wording; the reference splits by two global budgets,
     vsa2_rep/ops.py:50-85): tier A = the min(ka, NB) best kv blocks of each row, A|B = the min(kab, NB) best, under
     row_topk_mask's order (score desc, ties to the smaller index). Returns the two bool masks."""
     return row_topk_mask(scores, ka), row_topk_mask(scores, max(ka, kab))

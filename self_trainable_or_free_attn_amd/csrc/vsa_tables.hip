@@ -1,4 +1,4 @@
-// Tier construction for the VSA2 three-tier attention as BASELINE config 4 states it (gfx950):
+// Tier construction for the VSA2 three-tier attention as the HunyuanVideo-shape benchmark states it (gfx950):
 //
 //   kmeans_tab_kernel  seeded Lloyd k-means of every block's valid keys into RM clusters: the tier-B table rows are
 //                      the clusters' key / value means, with per-(b, h) log2 cluster sizes, cluster sizes and each

@@ -478,7 +478,8 @@ def _lc_stride(lc_mid):
 def rep_build_kmeans(k, v, blk_cnt, mid_reps, iters=5, seed=0):
     """Seeded k-means tier-B tables with the block-mean tail tables: [k_mid, v_mid, lc_mid [B, H, NB * RM] (per
     head), k_tail, v_tail, lc_tail [NB]] as rep_build, plus (counts [B, H, NB * RM] int32, labels [B, H, L]
-    uint8). BASELINE config 4's construction; the reference has only the contiguous tables."""
+    uint8). The three-tier benchmark construction at the HunyuanVideo shape; the reference has only the contiguous
+    tables."""
     tab = rep_build(k, v, blk_cnt, mid_reps)
     B, H, L, D = k.shape
     NB, RM = L // BLOCK, int(mid_reps)
@@ -495,7 +496,7 @@ def rep_build_kmeans(k, v, blk_cnt, mid_reps, iters=5, seed=0):
 
 def route_tier_rows(qr, kr, blk_cnt, R, ka, kab, row_norm, max_score_bytes=2 << 30):
     """Per-query-block tiers over VSA2's PSP router scores: the ka best kv blocks of every query block are tier A,
-    the next kab - ka tier B; same outputs as route_tiers (BASELINE config 4's split)."""
+    the next kab - ka tier B; same outputs as route_tiers (the benchmark construction's per-query-block split)."""
     _i32(blk_cnt, "blk_cnt")
     B, H = qr.shape[:2]
     NB, BH = blk_cnt.numel(), B * H

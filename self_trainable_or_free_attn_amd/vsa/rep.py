@@ -41,11 +41,11 @@ class RepTiers:
     """Three-tier budget; defaults 10 % full blocks, 20 % with 4 representatives, the rest as block means.
 
     split="global" (the reference's): fractions of all NB * NB pairs of a (b, h), taken by two exact global top-k
-    selections; ``frac_full`` alone is VSA2's budget (topk = frac_full * NB). split="per_row":
+    selections; ``frac_full`` alone is VSA2's budget (topk = frac_full * NB). split="per_row" (the benchmark construction):
     every query block takes round(frac_full * NB) tier-A and round(frac_mid * NB) tier-B blocks of its own row.
     tables="contiguous" (the reference's): tier-B representatives are means of the mid_reps contiguous
     64 / mid_reps-token groups; tables="kmeans": means of mid_reps clusters of the block's keys from
-    ``kmeans_iters`` Lloyd rounds started at seed tokens drawn with ``seed`` (5 rounds)."""
+    ``kmeans_iters`` Lloyd rounds started at seed tokens drawn with ``seed`` (the benchmark construction: 5 rounds)."""
 
     frac_full: float = 0.10
     frac_mid: float = 0.20

@@ -175,7 +175,7 @@ def test_rep_attention_end_to_end(qkv):
         check_close(name, f32(gr), wn, max_abs=bf16_max_abs(wn))
 
 
-# ------------------------------------------------------------- k-means tables, per-row tiers
+# ------------------------------------------------- the three-tier benchmark construction: k-means tables, per-row tiers
 @pytest.mark.parametrize("RM,seed", [(4, 0), (4, 11), (1, 3), (16, 5)])
 def test_kmeans_tables_bit_exact(qkv, RM, seed):
     """vsa_rep_build_kmeans against oracle kmeans_tables: tables, cluster sizes and labels equal bit for bit (the
@@ -257,7 +257,7 @@ def test_rep_forward_backward_kmeans_tables(qkv, phases):
 
 
 def test_rep_attention_config4_construction(qkv):
-    """rep_attention as BASELINE config 4 states it: per-row tiers (5 % / 20 %) and seeded 5-round k-means tables,
+    """rep_attention as the three-tier benchmark states it: per-row tiers (5 % / 20 %) and seeded 5-round k-means tables,
     forward and backward against the float64 graph on the same selection and clusters."""
     log("rep_attention per_row + kmeans")
     r = rep()

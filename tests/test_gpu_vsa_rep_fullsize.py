@@ -1,7 +1,7 @@
 """VSA2 three tiers (64 / 4 / 1) at the full C4 HunyuanVideo shape (B = 2, H = 24, 33 x 45 x 80 grid = 118 800
 tokens in 1857 blocks, a 16-token tail block, D = 128; tiers 5 % full, 20 % as 4 representatives, the rest block
 means; the benchmark's inputs), in both constructions: the reference's (two global budgets, contiguous group
-means) and BASELINE config 4's (per-query-block tiers, seeded 5-round k-means tables; sampled table blocks equal
+means) and the benchmark's (per-query-block tiers, seeded 5-round k-means tables; sampled table blocks equal
 the oracle's bit for bit). Checked: the forward output, LSE and dQ of sampled query blocks against a float64
 restatement of one softmax over the block's tier-A tokens, tier-B representatives (+ ln of the group size) and
 tier-C block means (+ ln of the block count; dQ with delta = rowsum(dO * O) of the stored bf16 O, the quantity the
