@@ -64,18 +64,6 @@ __device__ __forceinline__ void g2lds16(const void* gsrc, char* lds_base) {
   __builtin_amdgcn_global_load_lds(gsrc, LDS_PTR(void, lds_base), 16, 0, 0);
 }
 
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-
-// raw buffer resource over `bytes` bytes from `base` (offsets past it read as zero)
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, unsigned bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
-}
-
-// one wave instruction: every lane moves 16 bytes at rsrc + voff + soff to lds_base + 16 * lane
-__device__ __forceinline__ void buf2lds16(rsrc_t r, char* lds_base, unsigned voff, unsigned soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, LDS_PTR(void, lds_base), 16, (int)voff, (int)soff, 0, 0);
-}
-
 // The same global -> LDS transfer written as inline assembly: the compiler does not see these LDS writes, so it
 // adds no conservative vmcnt waits before LDS reads of the other buffer (it would otherwise drain the prefetch).
 // Visibility is the caller's job: dma_wait() then a barrier before any wave reads what was transferred.
@@ -131,8 +119,15 @@ __device__ __forceinline__ void dma4(srd_t r, const void* lds_base, unsigned vof
                : "memory");
 }
 
-// every vector memory operation of this wave (dma16 / dma4 included) has completed; also a compiler memory barrier
-__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// every vector memory operation of this wave (dma16 / dma4 included) has completed; also a compiler memory barrier.
+// The wait is the builtin, not inline assembly: the compiler then knows that its own earlier loads (the query rows
+// loaded ahead of a loop, say) have completed too. Behind an assembly wait it still counts them as outstanding and
+// places partial vmcnt waits for them in the loop body, where they also wait for the transfers issued by the
+// assembly above, which it does not count.
+__device__ __forceinline__ void dma_wait() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt / lgkmcnt at their maxima
+  asm volatile("" ::: "memory");
+}
 
 // uniform load through the scalar cache (the value must not change during the kernel)
 template <typename T>

@@ -42,8 +42,9 @@ struct VsaFwdArgs {
   float scale;  // log2(e) / sqrt(D)
 };
 
-// (This kernel stages K / V with the compiler-visible transfer, buf2lds16: measured ~6% faster here than the
-// inline-assembly dma16 the other kernels use.)
+// (K / V are staged with the inline-assembly transfer dma16. With the compiler-visible buffer-to-LDS builtin the
+// compiler cannot tell the next chunk's buffer from this one's and waits for the next chunk's transfers before
+// this chunk's V^T reads.)
 template <bool TASKS, int DH>
 __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
   constexpr int NKS = DH / 16, NDB = DH / 32;  // MFMA k-steps of QK^T, 32-column blocks of O (D = 64: the first half)
@@ -78,8 +79,8 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
   const size_t head = (size_t)bh * a.L;
 
   const unsigned head_bytes = (unsigned)((size_t)a.L * HD * 2);
-  const rsrc_t rk = make_rsrc(a.k + head * HD, head_bytes);
-  const rsrc_t rv = make_rsrc(a.v + head * HD, head_bytes);
+  const srd_t rk = make_srd(a.k + head * HD, head_bytes);
+  const srd_t rv = make_srd(a.v + head * HD, head_bytes);
   // this lane's four load rows R = 16 wv + 4 i + l / 16 of a chunk and its swizzled 16-byte chunk in them
   unsigned ld_off[4];
 #pragma unroll
@@ -93,8 +94,8 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
     char* vd = kv_s[sb][1] + wv * 4096;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      buf2lds16(rk, kd + i * 1024, ld_off[i], soff);
-      buf2lds16(rv, vd + i * 1024, ld_off[i], soff);
+      dma16(rk, kd + i * 1024, ld_off[i], soff);
+      dma16(rv, vd + i * 1024, ld_off[i], soff);
     }
   };
 

@@ -410,7 +410,10 @@ __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
       if (PART == 2) vreg[ks] = *reinterpret_cast<const ev8*>(a.v_tab + off + 16 * ks);
     }
   }
-  auto issue = [&](int i, int sb, float& ls, float& dl) {
+  // (wave 0 also loads the block's raw LSE and delta; `stats` turns them into what st_s holds once the transfers
+  // have been waited for, so that the compiler's wait for these loads does not come first and wait for the
+  // transfers as well)
+  auto issue = [&](int i, int sb, float& lv, float& dl) {
     const unsigned soff = (unsigned)i * (BK * 256);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -419,10 +422,14 @@ __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
     }
     if (wv == 0) {
       const size_t t = head + (size_t)i * BK + l;
-      const float lv = a.lse[t];
-      ls = lv == -INFINITY ? INFINITY : lv * LOG2E;
+      lv = a.lse[t];
       dl = a.delta[t];
     }
+  };
+  auto stats = [&](int sb, float lv, float dl) {  // wave 0, after dma_wait()
+    asm volatile("" : "+v"(lv), "+v"(dl));
+    st_s[sb][0][l] = lv == -INFINITY ? INFINITY : lv * LOG2E;
+    st_s[sb][1][l] = dl;
   };
   int produced = 0, chunk = 0;  // ring entries written so far, query-block chunks (of 256) scanned so far
   auto refill = [&]() {         // every thread; ends with a barrier
@@ -474,10 +481,7 @@ __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
   if (icur < a.NB) {
     issue(icur, 0, ls, dl);
     dma_wait();
-    if (wv == 0) {
-      st_s[0][0][l] = ls;
-      st_s[0][1][l] = dl;
-    }
+    if (wv == 0) stats(0, ls, dl);
   }
   dma_wait();
   __syncthreads();
@@ -522,10 +526,7 @@ __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
       }
     }
     dma_wait();
-    if (inext < a.NB && wv == 0) {
-      st_s[sb ^ 1][0][l] = ls;
-      st_s[sb ^ 1][1][l] = dl;
-    }
+    if (inext < a.NB && wv == 0) stats(sb ^ 1, ls, dl);
     __syncthreads();
     icur = inext;
     mcur = mnext;
