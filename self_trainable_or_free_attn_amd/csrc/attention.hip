@@ -296,22 +296,30 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
   // and LSE = max + log2(sum) do not depend on which maximum the terms were taken against.
   // (the half's row sum goes straight into lsum: a later half's rescale must scale it too)
   // (one instantiation for both chunk kinds, within 256 VGPRs: `biased` is a wave-uniform run-time flag)
+  // (an unbiased half takes its maximum on the raw products, max(s) * scale + prior being the maximum of the
+  // logits, and folds the subtraction of the running maximum into the exponent's multiply-add)
   auto half_online = [&](const f32x16& sh, int boff, bf16x8& pa, bf16x8& pb, bool biased) {
     float p[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) p[r] = fmaf(sh[r], scale, nprior);
+    float mh;
     if (biased) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) p[r] = fmaf(sh[r], scale, nprior);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bias_s[0][0] + boff + 8 * i + 4 * hi);
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) p[4 * i + jj] += b4[jj];
       }
-    }
-    float mh = p[0];
+      mh = p[0];
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mh = fmaxf(mh, p[r]);
-    mh = fmaxf(mh, __shfl_xor(mh, 32, 64));
+      for (int r = 1; r < 16; ++r) mh = fmaxf(mh, p[r]);
+    } else {
+      float mr = sh[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mr = fmaxf(mr, sh[r]);
+      mh = fmaf(mr, scale, nprior);
+    }
+    mh = max_xor32(mh);
     if (mh > mrun + ONLINE_SLACK) {
       const float alpha = exp2f_fast(mrun - mh);
       lsum *= alpha;
@@ -322,8 +330,14 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
       mrun = mh;
     }
     const float msub = mrun == -INFINITY ? 0.0f : mrun;
+    if (biased) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) p[r] = exp2f_fast(p[r] - msub);
+      for (int r = 0; r < 16; ++r) p[r] = exp2f_fast(p[r] - msub);
+    } else {
+      const float c = nprior - msub;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) p[r] = exp2f_fast(fmaf(sh[r], scale, c));
+    }
     pa = pack8(&p[0]);
     pb = pack8(&p[8]);
     lsum += sum8_bf16(pb, sum8_bf16(pa, 0.0f));
@@ -524,7 +538,7 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
   for (; j < nc; ++j) general_step(j);
 
   // ---------------------------------------------------------------- epilogue
-  const float tot = lsum + __shfl_xor(lsum, 32, 64);
+  const float tot = sum_xor32(lsum);
   bf16_t* orow = a.out + ((size_t)(rvalid ? row : 0) * H + h) * HD;
   float* lrow = a.lse + (size_t)row * H + h;
   auto store_rows = [&](float inv) {

@@ -138,6 +138,22 @@ __device__ __forceinline__ T sload(const T* p) {
 // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima)
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// this lane's value and lane (l ^ 32)'s, the lower half's first, on both lanes (v_permlane32_swap_b32: one VALU
+// instruction, where a shuffle across the two 32-lane halves is an LDS round trip). A commutative x op x' is then
+// op(.x, .y), the same on both lanes of the pair.
+__device__ __forceinline__ float2 lane_pair32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const float2 h = lane_pair32(x);
+  return fmaxf(h.x, h.y);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const float2 h = lane_pair32(x);
+  return h.x + h.y;
+}
+
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);

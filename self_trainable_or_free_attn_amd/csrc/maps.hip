@@ -126,7 +126,7 @@ __global__ __launch_bounds__(256) void estimate_kernel(const bf16_t* __restrict_
         est[2 * mb + (r / 8)] += exp2f_fast(x);
       }
 #pragma unroll
-    for (int tl = 0; tl < 4; ++tl) est[tl] += __shfl_xor(est[tl], 32, 64);
+    for (int tl = 0; tl < 4; ++tl) est[tl] = sum_xor32(est[tl]);
     if (hi == 0 && kvalid) {
 #pragma unroll
       for (int tl = 0; tl < 4; ++tl) {

@@ -340,7 +340,10 @@ __global__ __launch_bounds__(64 * KM_WAVES, 2) void kmeans_kernel(const bf16_t* 
       for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = __builtin_amdgcn_fmed3f(sp[tb][pb][r], mx, INFINITY);
-      mx = __builtin_amdgcn_fmed3f(__shfl_xor(mx, 32), mx, INFINITY);
+      {
+        const float2 hm = lane_pair32(mx);
+        mx = __builtin_amdgcn_fmed3f(hm.x, hm.y, INFINITY);
+      }
       const float nmx = -mx * LOG2E;
       float e[32], sm = 0.0f;
 #pragma unroll
@@ -350,7 +353,7 @@ __global__ __launch_bounds__(64 * KM_WAVES, 2) void kmeans_kernel(const bf16_t* 
           e[16 * tb + r] = exp2f_fast(fmaf(sp[tb][pb][r], LOG2E, nmx));
           sm += e[16 * tb + r];
         }
-      sm += __shfl_xor(sm, 32);
+      sm = sum_xor32(sm);
       const float inv = 1.0f / sm;
 #pragma unroll
       for (int i = 0; i < 32; ++i) ew[i] = fmaf(e[i], inv, ew[i]);
@@ -487,7 +490,7 @@ __global__ __launch_bounds__(64 * KM_WAVES, 2) void kmeans_kernel(const bf16_t* 
         for (int tb = 0; tb < 2; ++tb) uall[tb] = fmaf(w4[i], P[sb][tb][4 * g + i], uall[tb]);
     }
 #pragma unroll
-  for (int tb = 0; tb < 2; ++tb) uall[tb] += __shfl_xor(uall[tb], 32);
+  for (int tb = 0; tb < 2; ++tb) uall[tb] = sum_xor32(uall[tb]);
   float u[2][4], cw[4], r2m[4], nn[4];
   auto update = [&]() {  // u, cw, r2m, nn of the labels `lab`
     if (hi == 0) {
@@ -512,7 +515,7 @@ __global__ __launch_bounds__(64 * KM_WAVES, 2) void kmeans_kernel(const bf16_t* 
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {
 #pragma unroll
-      for (int c = 0; c < 3; ++c) ub[tb][c] += __shfl_xor(ub[tb][c], 32);
+      for (int c = 0; c < 3; ++c) ub[tb][c] = sum_xor32(ub[tb][c]);
       u[tb][3] = ub[tb][2];
       u[tb][1] = ub[tb][0] - ub[tb][2];
       u[tb][2] = ub[tb][1] - ub[tb][2];

@@ -155,7 +155,7 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
     float mx = p[0];
 #pragma unroll
     for (int r = 1; r < 16; ++r) mx = fmaxf(mx, p[r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = max_xor32(mx);
     if (__builtin_amdgcn_ballot_w64(mx > mref + RESCALE_SLACK) != 0) {
       const float mnew = fmaxf(mref, mx);
       const float alpha = mref == -INFINITY ? 0.0f : exp2f_fast(mref - mnew);
@@ -186,7 +186,7 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
   // merge the two key halves of each row group: kh = 1 waves hand (m, l, O) to the kh = 0 waves through LDS
   float* xo = reinterpret_cast<float*>(&kv_s[0][0][0]) + rg * (64 * 64);        // [64 regs][64 lanes]
   float* xm = reinterpret_cast<float*>(&kv_s[1][0][0]) + rg * 128;              // [m | l][64 lanes]
-  const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+  const float ltot = sum_xor32(lsum);
   if (kh == 1) {
 #pragma unroll
     for (int db = 0; db < NDB; ++db)

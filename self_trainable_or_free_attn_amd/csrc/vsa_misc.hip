@@ -195,7 +195,7 @@ __global__ __launch_bounds__(256) void fuse_bwd_kernel(FuseArgs a) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     dc[e] += __shfl_xor(dc[e], 16);
-    dc[e] += __shfl_xor(dc[e], 32);
+    dc[e] = sum_xor32(dc[e]);
   }
   float part = 0.f;
   if (s == 0) {

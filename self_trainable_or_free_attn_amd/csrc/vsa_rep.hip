@@ -244,7 +244,7 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
       float mx = x[0];
 #pragma unroll
       for (int r = 1; r < 16; ++r) mx = fmaxf(mx, x[r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = max_xor32(mx);
       if (__builtin_amdgcn_ballot_w64(mx > mref + SLACK) != 0) {
         const float mnew = fmaxf(mref, mx);
         const float alpha = mref == -INFINITY ? 0.0f : exp2f_fast(mref - mnew);
@@ -288,7 +288,7 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
   // combine the two key halves of each row group through LDS
   float* xo = reinterpret_cast<float*>(&kv_s[0][0][0]) + rg * (64 * 64);
   float* xm = reinterpret_cast<float*>(&kv_s[1][0][0]) + rg * 128;
-  const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+  const float ltot = sum_xor32(lsum);
   if (kh == 1) {
 #pragma unroll
     for (int db = 0; db < 4; ++db)
