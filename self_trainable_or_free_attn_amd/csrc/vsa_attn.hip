@@ -298,11 +298,12 @@ __device__ __forceinline__ bool owner_of(const VsaBwdArgs& a, int& blk, int& bh,
 // lse (natural) -> log2 domain, +inf for rows that must get P = 0
 __device__ __forceinline__ float lse_to_log2(float lse) { return lse == -INFINITY ? INFINITY : lse * LOG2E; }
 
-// The KV-owner backward as two passes with half the accumulators each, so that two waves share a SIMD:
-// PART 1 = dV (S, P, dV += P^T dO), PART 2 = dK (S, dP = dO V^T with V in registers, dK += dS^T Q). S is computed
-// in both (5 products per pair instead of 4).
+// The KV-owner backward with half the accumulators per wave, so that two waves share a SIMD: a dV group of four
+// waves (S, P, dV += P^T dO) and a dK group (S, dP = dO V^T with V in registers, dK += dS^T Q); S is computed in
+// both (5 products per pair instead of 4). PART 3: both groups in one 512-thread workgroup (one per CU), which
+// stage each query block's Q / dO once for both; PART 1 / 2: the dV or dK group alone (256 threads, two per CU).
 template <bool TASKS, int PART, int DH>
-__global__ __launch_bounds__(256, 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
+__global__ __launch_bounds__(PART == 3 ? 512 : 256, PART == 3 ? 1 : 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
   constexpr int NKS = DH / 16, NDB = DH / 32;
   __shared__ __attribute__((aligned(16))) char qd_s[2][2][BK * 256];  // [buffer][Q | dO]
   __shared__ __attribute__((aligned(16))) float st_s[2][2][BK];       // [buffer][lse2 (+inf: P = 0) | delta]
@@ -311,7 +312,9 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
   const int nc = end - beg;
   const int tid = threadIdx.x, l = tid & 63, hi = l >> 5, lq = l & 31;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kh = wv & 1, qh = wv >> 1;
+  const int wl = wv & 3;                                       // wave within its group
+  const int grp = PART == 3 ? (wv >> 2) : (PART == 2 ? 1 : 0);  // 0: dV, 1: dK (wave-uniform)
+  const int kh = wl & 1, qh = wl >> 1;
   const int key = 32 * kh + lq;
   const int kcnt = sload(a.blk_cnt + kb);
   const bool kvalid = key < kcnt;
@@ -323,7 +326,7 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
   unsigned ld_off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int P = (wv * 4 + i) * 64 + l, R = P >> 4, g = (P & 15) ^ swz(R);
+    const int P = (wl * 4 + i) * 64 + l, R = P >> 4, g = (P & 15) ^ swz(R);
     ld_off[i] = g < DH / 8 ? (unsigned)R * 256 + (unsigned)(g * 16) : 0x80000000u;
   }
   ev8 kreg[8], vreg[8];
@@ -332,16 +335,22 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
       kreg[ks] = *reinterpret_cast<const ev8*>(a.k + off + 16 * ks);
-      if (PART == 2) vreg[ks] = *reinterpret_cast<const ev8*>(a.v + off + 16 * ks);
+      if (grp == 1) vreg[ks] = *reinterpret_cast<const ev8*>(a.v + off + 16 * ks);
     }
   }
-  // stage query block i (Q, dO); wave 0 returns lane l's lse2 / delta of row i * 64 + l
+  // stage query block i (Q, dO; with both groups the dV group stages Q and the dK group dO); wave 0 returns lane
+  // l's lse2 / delta of row i * 64 + l
   auto issue = [&](int i, int sb, float& ls, float& dl) {
     const unsigned soff = (unsigned)i * (BK * 256);
+    if (PART == 3) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      dma16(rq, qd_s[sb][0] + wv * 4096 + r * 1024, ld_off[r], soff);
-      dma16(rd, qd_s[sb][1] + wv * 4096 + r * 1024, ld_off[r], soff);
+      for (int r = 0; r < 4; ++r) dma16(grp ? rd : rq, qd_s[sb][grp] + wl * 4096 + r * 1024, ld_off[r], soff);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        dma16(rq, qd_s[sb][0] + wl * 4096 + r * 1024, ld_off[r], soff);
+        dma16(rd, qd_s[sb][1] + wl * 4096 + r * 1024, ld_off[r], soff);
+      }
     }
     if (wv == 0) {
       const size_t t = head + (size_t)i * BK + l;
@@ -364,9 +373,9 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
       toff[1][db] = qh * 8192 + tile_off(rowA + 8, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
     }
   }
-  f32x16 dk[4], dv[4];
+  f32x16 acc[4];  // dV (group 0) or dK (group 1)
 #pragma unroll
-  for (int db = 0; db < 4; ++db) dk[db] = dv[db] = f32x16{};
+  for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
 
   float ls = 0.0f, dl = 0.0f;
   int inext = nc > 1 ? sload(a.col_idx + beg + 1) : 0;
@@ -394,9 +403,10 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
     f32x16 s = {}, dp = {};
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) s = emfma(elds16(qt, aoff[ks]), kreg[ks], s);
+    if (grp == 1) {
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks)
-      if (PART == 2) dp = emfma(elds16(dt, aoff[ks]), vreg[ks], dp);
+      for (int ks = 0; ks < NKS; ++ks) dp = emfma(elds16(dt, aoff[ks]), vreg[ks], dp);
+    }
     float p[16], ds[16];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -411,15 +421,13 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
     }
     const ev8 pa = epack8(&p[0]), pb = epack8(&p[8]);
     const ev8 sa = epack8(&ds[0]), sb8 = epack8(&ds[8]);
+    // dV += P^T dO (group 0) or dK += dS^T Q (group 1): the same products on the other tile and operand
+    const char* xt = grp == 0 ? dt : qt;
+    const ev8 xa8 = grp == 0 ? pa : sa, xb8 = grp == 0 ? pb : sb8;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
-      if (PART == 1) {
-        dv[db] = emfma(ecat_tr(lds_read_tr(dt, toff[0][db]), lds_read_tr(dt, toff[1][db])), pa, dv[db]);
-        dv[db] = emfma(ecat_tr(lds_read_tr(dt + 4096, toff[0][db]), lds_read_tr(dt + 4096, toff[1][db])), pb, dv[db]);
-      } else {
-        dk[db] = emfma(ecat_tr(lds_read_tr(qt, toff[0][db]), lds_read_tr(qt, toff[1][db])), sa, dk[db]);
-        dk[db] = emfma(ecat_tr(lds_read_tr(qt + 4096, toff[0][db]), lds_read_tr(qt + 4096, toff[1][db])), sb8, dk[db]);
-      }
+      acc[db] = emfma(ecat_tr(lds_read_tr(xt, toff[0][db]), lds_read_tr(xt, toff[1][db])), xa8, acc[db]);
+      acc[db] = emfma(ecat_tr(lds_read_tr(xt + 4096, toff[0][db]), lds_read_tr(xt + 4096, toff[1][db])), xb8, acc[db]);
     }
     dma_wait();
     if (j + 1 < nc && wv == 0) {
@@ -430,9 +438,9 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
     inext = inn;
   }
 
-  // sum the query-half partials: qh = 1 waves hand theirs to the qh = 0 waves of the same key half
-  f32x16* acc = PART == 1 ? dv : dk;
-  float* xa = reinterpret_cast<float*>(&qd_s[0][0][0]) + kh * (64 * 64);
+  // sum the query-half partials: qh = 1 waves hand theirs to the qh = 0 waves of the same key half (each group in
+  // its own half of the staging buffers)
+  float* xa = reinterpret_cast<float*>(&qd_s[0][0][0]) + (PART == 3 ? grp : 0) * (2 * 64 * 64) + kh * (64 * 64);
   if (qh == 1) {
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
@@ -449,7 +457,7 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
   for (int db = NDB; db < 4; ++db) acc[db] = f32x16{};  // columns past D: zero
   const size_t tok = head + (size_t)kb * BK + key;
   if (TASKS && slot >= 0) {
-    float* pa_out = (PART == 1 ? a.part_b : a.part_a) + ((size_t)slot * BK + key) * HD;
+    float* pa_out = (grp == 0 ? a.part_b : a.part_a) + ((size_t)slot * BK + key) * HD;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -461,10 +469,10 @@ __global__ __launch_bounds__(256, 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
   // valid keys: dK or dV + add / cnt; padding keys: 0
   const float inv = kvalid ? 1.0f / (float)kcnt : 0.0f;
   const float keep = kvalid ? 1.0f : 0.0f;
-  const float* add = PART == 1 ? a.add_b : a.add_a;
+  const float* add = grp == 0 ? a.add_b : a.add_a;
   const float* adp = add + ((size_t)bh * a.add_nb + kb) * HD;
-  float* out32 = PART == 1 ? a.out_b32 : a.out_a32;
-  e16_t* out16 = PART == 1 ? a.out_b : a.out_a;
+  float* out32 = grp == 0 ? a.out_b32 : a.out_a32;
+  e16_t* out16 = grp == 0 ? a.out_b : a.out_a;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -747,12 +755,8 @@ extern "C" int ES_VSA_API(vsa_attn_bwd_kv)(const void* q, const void* k, const v
   ES_REQUIRE(balanced_launch(BH, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "VSA: row-block queues unavailable");
   a.queues = qs.counters;
   a.fixed = qs.fixed;
-  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 1, 64>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 1, 128>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
-  ES_REQUIRE(balanced_launch(BH, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "VSA: row-block queues unavailable");
-  a.queues = qs.counters;
-  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 2, 64>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 2, 128>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
+  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 3, 64>), dim3((unsigned)qs.grid), dim3(512), 0, stream, a);
+  else hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 3, 128>), dim3((unsigned)qs.grid), dim3(512), 0, stream, a);
   return check_launch("vsa_attn_bwd_kv");
 }
 
@@ -776,10 +780,8 @@ extern "C" int ES_VSA_API(vsa_attn_bwd_kv_tasks)(const void* q, const void* k, c
   a.out_b = (e16_t*)dv;
   a.part_a = part_dk;
   a.part_b = part_dv;
-  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<true, 1, 64>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<true, 1, 128>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
-  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<true, 2, 64>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<true, 2, 128>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
+  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<true, 3, 64>), dim3((unsigned)max_tasks), dim3(512), 0, stream, a);
+  else hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<true, 3, 128>), dim3((unsigned)max_tasks), dim3(512), 0, stream, a);
   return check_launch("vsa_attn_bwd_kv_tasks");
 }
 
