@@ -307,6 +307,7 @@ __global__ __launch_bounds__(PART == 3 ? 512 : 256, PART == 3 ? 1 : 2) void vsa_
   constexpr int NKS = DH / 16, NDB = DH / 32;
   __shared__ __attribute__((aligned(16))) char qd_s[2][2][BK * 256];  // [buffer][Q | dO]
   __shared__ __attribute__((aligned(16))) float st_s[2][2][BK];       // [buffer][lse2 (+inf: P = 0) | delta]
+  __shared__ f32x4 p_s[PART == 3 ? 4 : 1][4 * 64];  // PART 3: P of each dV wave for the dK wave of the same tiles
   int kb, bh, beg, end, slot;
   if (!owner_of<TASKS>(a, kb, bh, beg, end, slot)) return;
   const int nc = end - beg;
@@ -401,29 +402,63 @@ __global__ __launch_bounds__(PART == 3 ? 512 : 256, PART == 3 ? 1 : 2) void vsa_
     const char* qt = qd_s[sb][0];
     const char* dt = qd_s[sb][1];
     f32x16 s = {}, dp = {};
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) s = emfma(elds16(qt, aoff[ks]), kreg[ks], s);
-    if (grp == 1) {
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) dp = emfma(elds16(dt, aoff[ks]), vreg[ks], dp);
-    }
     float p[16], ds[16];
+    ev8 xa8, xb8;  // the B operands of this wave's last product: P (dV) or dS (dK), bf16
+    if (PART == 3) {
+      // the dV wave computes S and P and hands P (fp32) to the dK wave of the same tiles through LDS, which computes
+      // dP meanwhile: four products per pair, sixteen matrix instructions per wave and chunk in both groups
+      f32x4* pex = p_s[PART == 3 ? wl : 0];
+      if (grp == 0) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f32x4 l4 = *reinterpret_cast<const f32x4*>(&st_s[sb][0][32 * qh + 8 * g + 4 * hi]);
-      const f32x4 d4 = *reinterpret_cast<const f32x4*>(&st_s[sb][1][32 * qh + 8 * g + 4 * hi]);
+        for (int ks = 0; ks < NKS; ++ks) s = emfma(elds16(qt, aoff[ks]), kreg[ks], s);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = 4 * g + e;
-        p[r] = exp2f_fast(fmaf(s[r], a.scale_log2, -(l4[e] + kmask)));
-        ds[r] = p[r] * (dp[r] - d4[e]) * a.scale;
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 l4 = *reinterpret_cast<const f32x4*>(&st_s[sb][0][32 * qh + 8 * g + 4 * hi]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) p[4 * g + e] = exp2f_fast(fmaf(s[4 * g + e], a.scale_log2, -(l4[e] + kmask)));
+          pex[g * 64 + l] = f32x4{p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]};
+        }
+        xa8 = epack8(&p[0]);
+        xb8 = epack8(&p[8]);
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) dp = emfma(elds16(dt, aoff[ks]), vreg[ks], dp);
       }
+      __syncthreads();  // P is in LDS
+      if (grp == 1) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&st_s[sb][1][32 * qh + 8 * g + 4 * hi]);
+          const f32x4 pv = pex[g * 64 + l];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ds[4 * g + e] = pv[e] * (dp[4 * g + e] - d4[e]) * a.scale;
+        }
+        xa8 = epack8(&ds[0]);
+        xb8 = epack8(&ds[8]);
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) s = emfma(elds16(qt, aoff[ks]), kreg[ks], s);
+      if (grp == 1) {
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) dp = emfma(elds16(dt, aoff[ks]), vreg[ks], dp);
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&st_s[sb][0][32 * qh + 8 * g + 4 * hi]);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&st_s[sb][1][32 * qh + 8 * g + 4 * hi]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g + e;
+          p[r] = exp2f_fast(fmaf(s[r], a.scale_log2, -(l4[e] + kmask)));
+          ds[r] = p[r] * (dp[r] - d4[e]) * a.scale;
+        }
+      }
+      xa8 = grp == 0 ? epack8(&p[0]) : epack8(&ds[0]);
+      xb8 = grp == 0 ? epack8(&p[8]) : epack8(&ds[8]);
     }
-    const ev8 pa = epack8(&p[0]), pb = epack8(&p[8]);
-    const ev8 sa = epack8(&ds[0]), sb8 = epack8(&ds[8]);
     // dV += P^T dO (group 0) or dK += dS^T Q (group 1): the same products on the other tile and operand
     const char* xt = grp == 0 ? dt : qt;
-    const ev8 xa8 = grp == 0 ? pa : sa, xb8 = grp == 0 ? pb : sb8;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
       acc[db] = emfma(ecat_tr(lds_read_tr(xt, toff[0][db]), lds_read_tr(xt, toff[1][db])), xa8, acc[db]);
