@@ -298,23 +298,24 @@ __device__ __forceinline__ bool owner_of(const VsaBwdArgs& a, int& blk, int& bh,
 // lse (natural) -> log2 domain, +inf for rows that must get P = 0
 __device__ __forceinline__ float lse_to_log2(float lse) { return lse == -INFINITY ? INFINITY : lse * LOG2E; }
 
-// The KV-owner backward with half the accumulators per wave, so that two waves share a SIMD: a dV group of four
-// waves (S, P, dV += P^T dO) and a dK group (S, dP = dO V^T with V in registers, dK += dS^T Q); S is computed in
-// both (5 products per pair instead of 4). PART 3: both groups in one 512-thread workgroup (one per CU), which
-// stage each query block's Q / dO once for both; PART 1 / 2: the dV or dK group alone (256 threads, two per CU).
-template <bool TASKS, int PART, int DH>
-__global__ __launch_bounds__(PART == 3 ? 512 : 256, PART == 3 ? 1 : 2) void vsa_bwd_kv_part_kernel(VsaBwdArgs a) {
+// The KV-owner backward: one 512-thread workgroup per (kv block, head), one per CU, in two groups of four waves
+// with one accumulator set each, so that two waves share a SIMD: the dV group computes S and P and dV += P^T dO,
+// the dK group dP = dO V^T (V in registers), dS from the dV group's P (handed over through LDS) and dK += dS^T Q.
+// Each query block's Q / dO is staged once for both (the dV group stages Q, the dK group dO): four products per
+// pair, sixteen matrix instructions per wave and chunk in both groups.
+template <bool TASKS, int DH>
+__global__ __launch_bounds__(512, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
   constexpr int NKS = DH / 16, NDB = DH / 32;
   __shared__ __attribute__((aligned(16))) char qd_s[2][2][BK * 256];  // [buffer][Q | dO]
   __shared__ __attribute__((aligned(16))) float st_s[2][2][BK];       // [buffer][lse2 (+inf: P = 0) | delta]
-  __shared__ f32x4 p_s[PART == 3 ? 4 : 1][4 * 64];  // PART 3: P of each dV wave for the dK wave of the same tiles
+  __shared__ f32x4 p_s[4][4 * 64];  // P of each dV wave, for the dK wave of the same tiles
   int kb, bh, beg, end, slot;
   if (!owner_of<TASKS>(a, kb, bh, beg, end, slot)) return;
   const int nc = end - beg;
   const int tid = threadIdx.x, l = tid & 63, hi = l >> 5, lq = l & 31;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wl = wv & 3;                                       // wave within its group
-  const int grp = PART == 3 ? (wv >> 2) : (PART == 2 ? 1 : 0);  // 0: dV, 1: dK (wave-uniform)
+  const int wl = wv & 3;    // wave within its group
+  const int grp = wv >> 2;  // 0: dV, 1: dK (wave-uniform)
   const int kh = wl & 1, qh = wl >> 1;
   const int key = 32 * kh + lq;
   const int kcnt = sload(a.blk_cnt + kb);
@@ -339,20 +340,11 @@ __global__ __launch_bounds__(PART == 3 ? 512 : 256, PART == 3 ? 1 : 2) void vsa_
       if (grp == 1) vreg[ks] = *reinterpret_cast<const ev8*>(a.v + off + 16 * ks);
     }
   }
-  // stage query block i (Q, dO; with both groups the dV group stages Q and the dK group dO); wave 0 returns lane
-  // l's lse2 / delta of row i * 64 + l
+  // stage query block i (the dV group Q, the dK group dO); wave 0 returns lane l's lse2 / delta of row i * 64 + l
   auto issue = [&](int i, int sb, float& ls, float& dl) {
     const unsigned soff = (unsigned)i * (BK * 256);
-    if (PART == 3) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dma16(grp ? rd : rq, qd_s[sb][grp] + wl * 4096 + r * 1024, ld_off[r], soff);
-    } else {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        dma16(rq, qd_s[sb][0] + wl * 4096 + r * 1024, ld_off[r], soff);
-        dma16(rd, qd_s[sb][1] + wl * 4096 + r * 1024, ld_off[r], soff);
-      }
-    }
+    for (int r = 0; r < 4; ++r) dma16(grp ? rd : rq, qd_s[sb][grp] + wl * 4096 + r * 1024, ld_off[r], soff);
     if (wv == 0) {
       const size_t t = head + (size_t)i * BK + l;
       ls = lse_to_log2(a.lse[t]);
@@ -404,58 +396,35 @@ __global__ __launch_bounds__(PART == 3 ? 512 : 256, PART == 3 ? 1 : 2) void vsa_
     f32x16 s = {}, dp = {};
     float p[16], ds[16];
     ev8 xa8, xb8;  // the B operands of this wave's last product: P (dV) or dS (dK), bf16
-    if (PART == 3) {
-      // the dV wave computes S and P and hands P (fp32) to the dK wave of the same tiles through LDS, which computes
-      // dP meanwhile: four products per pair, sixteen matrix instructions per wave and chunk in both groups
-      f32x4* pex = p_s[PART == 3 ? wl : 0];
-      if (grp == 0) {
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) s = emfma(elds16(qt, aoff[ks]), kreg[ks], s);
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 l4 = *reinterpret_cast<const f32x4*>(&st_s[sb][0][32 * qh + 8 * g + 4 * hi]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) p[4 * g + e] = exp2f_fast(fmaf(s[4 * g + e], a.scale_log2, -(l4[e] + kmask)));
-          pex[g * 64 + l] = f32x4{p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]};
-        }
-        xa8 = epack8(&p[0]);
-        xb8 = epack8(&p[8]);
-      } else {
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) dp = emfma(elds16(dt, aoff[ks]), vreg[ks], dp);
-      }
-      __syncthreads();  // P is in LDS
-      if (grp == 1) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&st_s[sb][1][32 * qh + 8 * g + 4 * hi]);
-          const f32x4 pv = pex[g * 64 + l];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) ds[4 * g + e] = pv[e] * (dp[4 * g + e] - d4[e]) * a.scale;
-        }
-        xa8 = epack8(&ds[0]);
-        xb8 = epack8(&ds[8]);
-      }
-    } else {
+    // the dV wave computes S and P and hands P (fp32) to the dK wave of the same tiles, which computes dP meanwhile
+    f32x4* pex = p_s[wl];
+    if (grp == 0) {
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) s = emfma(elds16(qt, aoff[ks]), kreg[ks], s);
-      if (grp == 1) {
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) dp = emfma(elds16(dt, aoff[ks]), vreg[ks], dp);
-      }
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const f32x4 l4 = *reinterpret_cast<const f32x4*>(&st_s[sb][0][32 * qh + 8 * g + 4 * hi]);
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&st_s[sb][1][32 * qh + 8 * g + 4 * hi]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * g + e;
-          p[r] = exp2f_fast(fmaf(s[r], a.scale_log2, -(l4[e] + kmask)));
-          ds[r] = p[r] * (dp[r] - d4[e]) * a.scale;
-        }
+        for (int e = 0; e < 4; ++e) p[4 * g + e] = exp2f_fast(fmaf(s[4 * g + e], a.scale_log2, -(l4[e] + kmask)));
+        pex[g * 64 + l] = f32x4{p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]};
       }
-      xa8 = grp == 0 ? epack8(&p[0]) : epack8(&ds[0]);
-      xb8 = grp == 0 ? epack8(&p[8]) : epack8(&ds[8]);
+      xa8 = epack8(&p[0]);
+      xb8 = epack8(&p[8]);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) dp = emfma(elds16(dt, aoff[ks]), vreg[ks], dp);
+    }
+    __syncthreads();  // P is in LDS
+    if (grp == 1) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&st_s[sb][1][32 * qh + 8 * g + 4 * hi]);
+        const f32x4 pv = pex[g * 64 + l];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ds[4 * g + e] = pv[e] * (dp[4 * g + e] - d4[e]) * a.scale;
+      }
+      xa8 = epack8(&ds[0]);
+      xb8 = epack8(&ds[8]);
     }
     // dV += P^T dO (group 0) or dK += dS^T Q (group 1): the same products on the other tile and operand
     const char* xt = grp == 0 ? dt : qt;
@@ -475,7 +444,7 @@ __global__ __launch_bounds__(PART == 3 ? 512 : 256, PART == 3 ? 1 : 2) void vsa_
 
   // sum the query-half partials: qh = 1 waves hand theirs to the qh = 0 waves of the same key half (each group in
   // its own half of the staging buffers)
-  float* xa = reinterpret_cast<float*>(&qd_s[0][0][0]) + (PART == 3 ? grp : 0) * (2 * 64 * 64) + kh * (64 * 64);
+  float* xa = reinterpret_cast<float*>(&qd_s[0][0][0]) + grp * (2 * 64 * 64) + kh * (64 * 64);
   if (qh == 1) {
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
@@ -790,8 +759,8 @@ extern "C" int ES_VSA_API(vsa_attn_bwd_kv)(const void* q, const void* k, const v
   ES_REQUIRE(balanced_launch(BH, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "VSA: row-block queues unavailable");
   a.queues = qs.counters;
   a.fixed = qs.fixed;
-  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 3, 64>), dim3((unsigned)qs.grid), dim3(512), 0, stream, a);
-  else hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<false, 3, 128>), dim3((unsigned)qs.grid), dim3(512), 0, stream, a);
+  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_kernel<false, 64>), dim3((unsigned)qs.grid), dim3(512), 0, stream, a);
+  else hipLaunchKernelGGL((vsa_bwd_kv_kernel<false, 128>), dim3((unsigned)qs.grid), dim3(512), 0, stream, a);
   return check_launch("vsa_attn_bwd_kv");
 }
 
@@ -815,8 +784,8 @@ extern "C" int ES_VSA_API(vsa_attn_bwd_kv_tasks)(const void* q, const void* k, c
   a.out_b = (e16_t*)dv;
   a.part_a = part_dk;
   a.part_b = part_dv;
-  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<true, 3, 64>), dim3((unsigned)max_tasks), dim3(512), 0, stream, a);
-  else hipLaunchKernelGGL((vsa_bwd_kv_part_kernel<true, 3, 128>), dim3((unsigned)max_tasks), dim3(512), 0, stream, a);
+  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_kernel<true, 64>), dim3((unsigned)max_tasks), dim3(512), 0, stream, a);
+  else hipLaunchKernelGGL((vsa_bwd_kv_kernel<true, 128>), dim3((unsigned)max_tasks), dim3(512), 0, stream, a);
   return check_launch("vsa_attn_bwd_kv_tasks");
 }
 
