@@ -365,25 +365,27 @@ __device__ __forceinline__ unsigned long long tier_mask(const TabArgs& a, size_t
   return nblk >= 64 ? m : (m & ((1ull << nblk) - 1ull));
 }
 
-// one workgroup per (64 table rows, head) in head-major balanced order (queues.h), 256 threads; the fine KV-owner layout (2 key halves x 2 query halves). Two passes with
-// one accumulator set each, so that two waves share a SIMD: PART 1 = dV (S, dV), PART 2 = dK (S, dP with the
-// table's V rows in registers, dK).
-template <int PART>
-__global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
+// one 512-thread workgroup per (64 table rows, head) in head-major balanced order (queues.h), one per CU, in the
+// fine KV-owner layout (2 key halves x 2 query halves) twice: a dV group of four waves (S, P, dV) and a dK group
+// (dP with the table's V rows in registers, dS from the dV group's P handed over through LDS, dK), one accumulator
+// set per wave so that two waves share a SIMD; each query block's Q / dO is staged once for both groups.
+__global__ __launch_bounds__(512, 1) void rep_bwd_tab_kernel(TabArgs a) {
   __shared__ __attribute__((aligned(16))) char qd_s[2][2][BK * 256];
   __shared__ __attribute__((aligned(16))) float st_s[2][2][BK];
+  __shared__ f32x4 p_s[4][4 * 64];  // P of each dV wave, for the dK wave of the same tiles
   // ring of the query blocks with at least one tier pair among this workgroup's blocks, and their masks, filled
   // 256 query blocks at a time by the whole workgroup (one mask per thread, ballot compaction), so the loop reads
   // its next block from LDS instead of scanning the bitmaps block by block
   constexpr int RING = 512;
   __shared__ int act_s[RING];
   __shared__ unsigned long long am_s[RING];
-  __shared__ int wcnt_s[4];
+  __shared__ int wcnt_s[8];
   int grp, bh;
   if (!balanced_head_item(a.queues, a.fixed, a.rows_pad / BK, a.BH, bh, grp)) return;
   const int tid = threadIdx.x, l = tid & 63, hi = l >> 5, lq = l & 31;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kh = wv & 1, qh = wv >> 1;
+  const int wl = wv & 3, part = wv >> 2;  // wave within its group; 0: dV, 1: dK (wave-uniform)
+  const int kh = wl & 1, qh = wl >> 1;
   const int key = 32 * kh + lq;
   const int trow = grp * BK + key;  // table row of this lane's key
   const int per_blk = a.tier == PH_B ? a.RM : 1;
@@ -398,7 +400,7 @@ __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
   unsigned ld_off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int P = (wv * 4 + i) * 64 + l, R = P >> 4;
+    const int P = (wl * 4 + i) * 64 + l, R = P >> 4;
     ld_off[i] = (unsigned)R * 256 + (unsigned)(((P & 15) ^ swz(R)) * 16);
   }
   ev8 kreg[8], vreg[8];
@@ -406,20 +408,17 @@ __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
     const size_t off = ((size_t)bh * a.rows_pad + trow) * HD + 8 * hi;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-      kreg[ks] = *reinterpret_cast<const ev8*>(a.k_tab + off + 16 * ks);
-      if (PART == 2) vreg[ks] = *reinterpret_cast<const ev8*>(a.v_tab + off + 16 * ks);
+      if (part == 0) kreg[ks] = *reinterpret_cast<const ev8*>(a.k_tab + off + 16 * ks);
+      else vreg[ks] = *reinterpret_cast<const ev8*>(a.v_tab + off + 16 * ks);
     }
   }
   // (wave 0 also loads the block's raw LSE and delta; `stats` turns them into what st_s holds once the transfers
   // have been waited for, so that the compiler's wait for these loads does not come first and wait for the
   // transfers as well)
-  auto issue = [&](int i, int sb, float& lv, float& dl) {
+  auto issue = [&](int i, int sb, float& lv, float& dl) {  // (the dV group stages Q, the dK group dO)
     const unsigned soff = (unsigned)i * (BK * 256);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      dma16(rq, qd_s[sb][0] + wv * 4096 + r * 1024, ld_off[r], soff);
-      dma16(rd, qd_s[sb][1] + wv * 4096 + r * 1024, ld_off[r], soff);
-    }
+    for (int r = 0; r < 4; ++r) dma16(part ? rd : rq, qd_s[sb][part] + wl * 4096 + r * 1024, ld_off[r], soff);
     if (wv == 0) {
       const size_t t = head + (size_t)i * BK + l;
       lv = a.lse[t];
@@ -432,15 +431,15 @@ __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
     st_s[sb][1][l] = dl;
   };
   int produced = 0, chunk = 0;  // ring entries written so far, query-block chunks (of 256) scanned so far
-  auto refill = [&]() {         // every thread; ends with a barrier
+  auto refill = [&]() {         // every thread (the masks from the first 256); ends with a barrier
     const int i = chunk * 256 + tid;
-    const unsigned long long m = i < a.NB ? tier_mask(a, (size_t)bh * a.NB + i, fb, nblk) : 0ull;
+    const unsigned long long m = (tid < 256 && i < a.NB) ? tier_mask(a, (size_t)bh * a.NB + i, fb, nblk) : 0ull;
     const unsigned long long bal = __builtin_amdgcn_ballot_w64(m != 0ull);
     if (l == 0) wcnt_s[wv] = __popcll(bal);
     __syncthreads();
     int before = 0, total = 0;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < 8; ++w) {
       const int c = wcnt_s[w];
       before += w < wv ? c : 0;
       total += c;
@@ -470,9 +469,9 @@ __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
       toff[1][db] = qh * 8192 + tile_off(rowA + 8, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
     }
   }
-  f32x16 dk[4], dv[4];
+  f32x16 acc[4];  // dV (group 0) or dK (group 1)
 #pragma unroll
-  for (int db = 0; db < 4; ++db) dk[db] = dv[db] = f32x16{};
+  for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
 
   float ls = 0.0f, dl = 0.0f;
   ensure(1);
@@ -496,34 +495,44 @@ __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
     const char* qt = qd_s[sb][0];
     const char* dt = qd_s[sb][1];
     f32x16 s = {}, dp = {};
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) s = emfma(elds16(qt, aoff[ks]), kreg[ks], s);
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
-      if (PART == 2) dp = emfma(elds16(dt, aoff[ks]), vreg[ks], dp);
     float p[16], ds[16];
+    ev8 xa8, xb8;  // the B operands of this wave's last product: P (dV) or dS (dK), bf16
+    // the dV wave computes S and P and hands P (fp32) to the dK wave of the same tiles, which computes dP meanwhile
+    f32x4* pex = p_s[wl];
+    if (part == 0) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f32x4 l4 = *reinterpret_cast<const f32x4*>(&st_s[sb][0][32 * qh + 8 * g + 4 * hi]);
-      const f32x4 d4 = *reinterpret_cast<const f32x4*>(&st_s[sb][1][32 * qh + 8 * g + 4 * hi]);
+      for (int ks = 0; ks < 8; ++ks) s = emfma(elds16(qt, aoff[ks]), kreg[ks], s);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = 4 * g + e;
-        p[r] = exp2f_fast(fmaf(s[r], a.scale_log2, kb) - l4[e]);
-        ds[r] = p[r] * (dp[r] - d4[e]) * a.scale;
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&st_s[sb][0][32 * qh + 8 * g + 4 * hi]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) p[4 * g + e] = exp2f_fast(fmaf(s[4 * g + e], a.scale_log2, kb) - l4[e]);
+        pex[g * 64 + l] = f32x4{p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]};
       }
+      xa8 = epack8(&p[0]);
+      xb8 = epack8(&p[8]);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) dp = emfma(elds16(dt, aoff[ks]), vreg[ks], dp);
     }
-    const ev8 pa = epack8(&p[0]), pb = epack8(&p[8]);
-    const ev8 sa = epack8(&ds[0]), sb8 = epack8(&ds[8]);
+    __syncthreads();  // P is in LDS
+    if (part == 1) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&st_s[sb][1][32 * qh + 8 * g + 4 * hi]);
+        const f32x4 pv = pex[g * 64 + l];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ds[4 * g + e] = pv[e] * (dp[4 * g + e] - d4[e]) * a.scale;
+      }
+      xa8 = epack8(&ds[0]);
+      xb8 = epack8(&ds[8]);
+    }
+    // dV += P^T dO (group 0) or dK += dS^T Q (group 1): the same products on the other tile and operand
+    const char* xt = part == 0 ? dt : qt;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      if (PART == 1) {
-        dv[db] = emfma(ecat_tr(lds_read_tr(dt, toff[0][db]), lds_read_tr(dt, toff[1][db])), pa, dv[db]);
-        dv[db] = emfma(ecat_tr(lds_read_tr(dt + 4096, toff[0][db]), lds_read_tr(dt + 4096, toff[1][db])), pb, dv[db]);
-      } else {
-        dk[db] = emfma(ecat_tr(lds_read_tr(qt, toff[0][db]), lds_read_tr(qt, toff[1][db])), sa, dk[db]);
-        dk[db] = emfma(ecat_tr(lds_read_tr(qt + 4096, toff[0][db]), lds_read_tr(qt + 4096, toff[1][db])), sb8, dk[db]);
-      }
+      acc[db] = emfma(ecat_tr(lds_read_tr(xt, toff[0][db]), lds_read_tr(xt, toff[1][db])), xa8, acc[db]);
+      acc[db] = emfma(ecat_tr(lds_read_tr(xt + 4096, toff[0][db]), lds_read_tr(xt + 4096, toff[1][db])), xb8, acc[db]);
     }
     dma_wait();
     if (inext < a.NB && wv == 0) stats(sb ^ 1, ls, dl);
@@ -532,8 +541,8 @@ __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
     mcur = mnext;
   }
 
-  f32x16* acc = PART == 1 ? dv : dk;
-  float* xa = reinterpret_cast<float*>(&qd_s[0][0][0]) + kh * (64 * 64);
+  // sum the query-half partials (each group in its own half of the staging buffers)
+  float* xa = reinterpret_cast<float*>(&qd_s[0][0][0]) + part * (2 * 64 * 64) + kh * (64 * 64);
   if (qh == 1) {
 #pragma unroll
     for (int db = 0; db < 4; ++db)
@@ -542,7 +551,7 @@ __global__ __launch_bounds__(256, 2) void rep_bwd_tab_kernel(TabArgs a) {
   }
   __syncthreads();
   if (qh == 1) return;
-  float* g = (PART == 1 ? a.dv_tab : a.dk_tab) + ((size_t)bh * a.rows_pad + trow) * HD;
+  float* g = (part == 0 ? a.dv_tab : a.dk_tab) + ((size_t)bh * a.rows_pad + trow) * HD;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -809,10 +818,7 @@ extern "C" int ES_VSA_API(vsa_rep_bwd_tables)(const void* q, const void* dout, c
   ES_REQUIRE(balanced_launch_queues(per_queue, stream, qs), ES_ERR_LAUNCH, "VSA2-rep: row-group queues unavailable");
   a.queues = qs.counters;
   a.fixed = qs.fixed;
-  hipLaunchKernelGGL(rep_bwd_tab_kernel<1>, dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
-  ES_REQUIRE(balanced_launch_queues(per_queue, stream, qs), ES_ERR_LAUNCH, "VSA2-rep: row-group queues unavailable");
-  a.queues = qs.counters;
-  hipLaunchKernelGGL(rep_bwd_tab_kernel<2>, dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL(rep_bwd_tab_kernel, dim3((unsigned)qs.grid), dim3(512), 0, stream, a);
   return check_launch("vsa_rep_bwd_tables");
 }
 
