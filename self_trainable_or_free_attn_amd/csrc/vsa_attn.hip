@@ -351,12 +351,9 @@ __global__ __launch_bounds__(512, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
       dl = a.delta[t];
     }
   };
-  int aoff[8], boff[8];
+  int aoff[8];
 #pragma unroll
-  for (int ks = 0; ks < 8; ++ks) {
-    aoff[ks] = qh * 8192 + tile_off(lq, 2 * ks + hi);
-    boff[ks] = kh * 8192 + tile_off(lq, 2 * ks + hi);
-  }
+  for (int ks = 0; ks < 8; ++ks) aoff[ks] = qh * 8192 + tile_off(lq, 2 * ks + hi);
   int toff[2][4];
   {
     const int g1 = (l >> 4) & 1, sub = (l & 1) * 8, rowA = 4 * hi + ((l & 15) >> 2);
