@@ -247,8 +247,6 @@ __device__ __forceinline__ unsigned okey(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__device__ __forceinline__ int wave_count(bool p) { return __popcll(__builtin_amdgcn_ballot_w64(p)); }
-
 struct TierArgs {
   const float* scores;  // [bh_count, NB, NB]
   int NB, W, bh0, rows;
