@@ -298,25 +298,23 @@ __device__ __forceinline__ bool owner_of(const VsaBwdArgs& a, int& blk, int& bh,
 // lse (natural) -> log2 domain, +inf for rows that must get P = 0
 __device__ __forceinline__ float lse_to_log2(float lse) { return lse == -INFINITY ? INFINITY : lse * LOG2E; }
 
-// The KV-owner backward: one 512-thread workgroup per (kv block, head), one per CU, in two groups of four waves
-// with one accumulator set each, so that two waves share a SIMD: the dV group computes S and P and dV += P^T dO,
-// the dK group dP = dO V^T (V in registers), dS from the dV group's P (handed over through LDS) and dK += dS^T Q.
-// Each query block's Q / dO is staged once for both (the dV group stages Q, the dK group dO): four products per
-// pair, sixteen matrix instructions per wave and chunk in both groups.
+// The KV-owner backward: one 256-thread workgroup per (kv block, head), two per CU. Wave (role, key half): a dV
+// wave computes S and P of its 32 keys against the chunk's 64 query rows and dV += P^T dO; a dK wave of the same
+// keys computes dP = dO V^T (V in registers), dS from the dV wave's P (handed over as bf16 / fp16 operands through
+// LDS) and dK += dS^T Q. Each query block's Q / dO is staged once for both roles: four products per pair, 32
+// matrix instructions per wave and chunk, and every wave's accumulators hold the full sums of its keys.
 template <bool TASKS, int DH>
-__global__ __launch_bounds__(512, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
+__global__ __launch_bounds__(256, 2) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
   constexpr int NKS = DH / 16, NDB = DH / 32;
   __shared__ __attribute__((aligned(16))) char qd_s[2][2][BK * 256];  // [buffer][Q | dO]
   __shared__ __attribute__((aligned(16))) float st_s[2][2][BK];       // [buffer][lse2 (+inf: P = 0) | delta]
-  __shared__ f32x4 p_s[4][4 * 64];  // P of each dV wave, for the dK wave of the same tiles
+  __shared__ ev8 p_s[2][4][64];  // [key half][query half x (first | second 8 rows of a lane)][lane]: the dV waves' P
   int kb, bh, beg, end, slot;
   if (!owner_of<TASKS>(a, kb, bh, beg, end, slot)) return;
   const int nc = end - beg;
   const int tid = threadIdx.x, l = tid & 63, hi = l >> 5, lq = l & 31;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wl = wv & 3;    // wave within its group
-  const int grp = wv >> 2;  // 0: dV, 1: dK (wave-uniform)
-  const int kh = wl & 1, qh = wl >> 1;
+  const int role = wv >> 1, kh = wv & 1;  // role 0: dV, 1: dK (wave-uniform)
   const int key = 32 * kh + lq;
   const int kcnt = sload(a.blk_cnt + kb);
   const bool kvalid = key < kcnt;
@@ -328,42 +326,44 @@ __global__ __launch_bounds__(512, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
   unsigned ld_off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int P = (wl * 4 + i) * 64 + l, R = P >> 4, g = (P & 15) ^ swz(R);
+    const int P = (wv * 4 + i) * 64 + l, R = P >> 4, g = (P & 15) ^ swz(R);
     ld_off[i] = g < DH / 8 ? (unsigned)R * 256 + (unsigned)(g * 16) : 0x80000000u;
   }
-  ev8 kreg[8], vreg[8];
+  ev8 kvreg[8];  // this lane's key row: K (dV wave, for S) or V (dK wave, for dP)
   {
     const size_t off = (head + (size_t)kb * BK + key) * HD + 8 * hi;
+    const e16_t* src = (role ? a.v : a.k) + off;
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      kreg[ks] = *reinterpret_cast<const ev8*>(a.k + off + 16 * ks);
-      if (grp == 1) vreg[ks] = *reinterpret_cast<const ev8*>(a.v + off + 16 * ks);
-    }
+    for (int ks = 0; ks < NKS; ++ks) kvreg[ks] = *reinterpret_cast<const ev8*>(src + 16 * ks);
   }
-  // stage query block i (the dV group Q, the dK group dO); wave 0 returns lane l's lse2 / delta of row i * 64 + l
+  // stage query block i (Q, dO: 16 rows of each per wave); wave 0 returns lane l's lse2 / delta of row i * 64 + l
   auto issue = [&](int i, int sb, float& ls, float& dl) {
     const unsigned soff = (unsigned)i * (BK * 256);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) dma16(grp ? rd : rq, qd_s[sb][grp] + wl * 4096 + r * 1024, ld_off[r], soff);
+    for (int r = 0; r < 4; ++r) {
+      dma16(rq, qd_s[sb][0] + wv * 4096 + r * 1024, ld_off[r], soff);
+      dma16(rd, qd_s[sb][1] + wv * 4096 + r * 1024, ld_off[r], soff);
+    }
     if (wv == 0) {
       const size_t t = head + (size_t)i * BK + l;
       ls = lse_to_log2(a.lse[t]);
       dl = a.delta[t];
     }
   };
+  // LDS offsets within a query half (32 rows, 8 KB); the second half adds 8192
   int aoff[8];
 #pragma unroll
-  for (int ks = 0; ks < 8; ++ks) aoff[ks] = qh * 8192 + tile_off(lq, 2 * ks + hi);
+  for (int ks = 0; ks < 8; ++ks) aoff[ks] = tile_off(lq, 2 * ks + hi);
   int toff[2][4];
   {
     const int g1 = (l >> 4) & 1, sub = (l & 1) * 8, rowA = 4 * hi + ((l & 15) >> 2);
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      toff[0][db] = qh * 8192 + tile_off(rowA, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
-      toff[1][db] = qh * 8192 + tile_off(rowA + 8, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
+      toff[0][db] = tile_off(rowA, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
+      toff[1][db] = tile_off(rowA + 8, 4 * db + 2 * g1 + ((l & 3) >> 1)) + sub;
     }
   }
-  f32x16 acc[4];  // dV (group 0) or dK (group 1)
+  f32x16 acc[4];  // dV (role 0) or dK (role 1) of this lane's key
 #pragma unroll
   for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
 
@@ -381,6 +381,7 @@ __global__ __launch_bounds__(512, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
   __syncthreads();
   // masked key columns: every row's lse2 becomes +inf for this lane, so P = 2^(s - inf) = 0 without a branch
   const float kmask = kvalid ? 0.0f : INFINITY;
+  ev8* pex = p_s[kh][0];
   for (int j = 0; j < nc; ++j) {
     const int sb = j & 1;
     int inn = 0;
@@ -390,45 +391,63 @@ __global__ __launch_bounds__(512, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
     }
     const char* qt = qd_s[sb][0];
     const char* dt = qd_s[sb][1];
-    f32x16 s = {}, dp = {};
-    float p[16], ds[16];
-    ev8 xa8, xb8;  // the B operands of this wave's last product: P (dV) or dS (dK), bf16
-    // the dV wave computes S and P and hands P (fp32) to the dK wave of the same tiles, which computes dP meanwhile
-    f32x4* pex = p_s[wl];
-    if (grp == 0) {
+    f32x16 dp[2];  // dK wave: dP of each query half
+    if (role == 0) {
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) s = emfma(elds16(qt, aoff[ks]), kreg[ks], s);
+      for (int qh = 0; qh < 2; ++qh) {
+        f32x16 s = {};
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&st_s[sb][0][32 * qh + 8 * g + 4 * hi]);
+        for (int ks = 0; ks < NKS; ++ks) s = emfma(elds16(qt, qh * 8192 + aoff[ks]), kvreg[ks], s);
+        float p[16];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) p[4 * g + e] = exp2f_fast(fmaf(s[4 * g + e], a.scale_log2, -(l4[e] + kmask)));
-        pex[g * 64 + l] = f32x4{p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]};
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 l4 = *reinterpret_cast<const f32x4*>(&st_s[sb][0][32 * qh + 8 * g + 4 * hi]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) p[4 * g + e] = exp2f_fast(fmaf(s[4 * g + e], a.scale_log2, -(l4[e] + kmask)));
+        }
+        const ev8 pa = epack8(&p[0]), pb = epack8(&p[8]);
+        pex[(2 * qh) * 64 + l] = pa;
+        pex[(2 * qh + 1) * 64 + l] = pb;
+        // dV += P^T dO (needs nothing from the dK wave, so it runs before the hand-over barrier)
+        const char* xt = dt + qh * 8192;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          acc[db] = emfma(ecat_tr(lds_read_tr(xt, toff[0][db]), lds_read_tr(xt, toff[1][db])), pa, acc[db]);
+          acc[db] = emfma(ecat_tr(lds_read_tr(xt + 4096, toff[0][db]), lds_read_tr(xt + 4096, toff[1][db])), pb, acc[db]);
+        }
       }
-      xa8 = epack8(&p[0]);
-      xb8 = epack8(&p[8]);
     } else {
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) dp = emfma(elds16(dt, aoff[ks]), vreg[ks], dp);
+      for (int qh = 0; qh < 2; ++qh) {
+        dp[qh] = f32x16{};
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) dp[qh] = emfma(elds16(dt, qh * 8192 + aoff[ks]), kvreg[ks], dp[qh]);
+      }
     }
     __syncthreads();  // P is in LDS
-    if (grp == 1) {
+    if (role == 1) {  // dS = P (dP - delta) / sqrt(D), dK += dS^T Q
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&st_s[sb][1][32 * qh + 8 * g + 4 * hi]);
-        const f32x4 pv = pex[g * 64 + l];
+      for (int qh = 0; qh < 2; ++qh) {
+        const ev8 pa = pex[(2 * qh) * 64 + l], pb = pex[(2 * qh + 1) * 64 + l];
+        float ds[16];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ds[4 * g + e] = pv[e] * (dp[4 * g + e] - d4[e]) * a.scale;
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&st_s[sb][1][32 * qh + 8 * g + 4 * hi]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g + e;
+            const float pv = r < 8 ? (float)pa[r] : (float)pb[r - 8];
+            ds[r] = pv * (dp[qh][r] - d4[e]) * a.scale;
+          }
+        }
+        const ev8 sa = epack8(&ds[0]), sb8 = epack8(&ds[8]);
+        const char* xt = qt + qh * 8192;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          acc[db] = emfma(ecat_tr(lds_read_tr(xt, toff[0][db]), lds_read_tr(xt, toff[1][db])), sa, acc[db]);
+          acc[db] = emfma(ecat_tr(lds_read_tr(xt + 4096, toff[0][db]), lds_read_tr(xt + 4096, toff[1][db])), sb8, acc[db]);
+        }
       }
-      xa8 = epack8(&ds[0]);
-      xb8 = epack8(&ds[8]);
-    }
-    // dV += P^T dO (group 0) or dK += dS^T Q (group 1): the same products on the other tile and operand
-    const char* xt = grp == 0 ? dt : qt;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      acc[db] = emfma(ecat_tr(lds_read_tr(xt, toff[0][db]), lds_read_tr(xt, toff[1][db])), xa8, acc[db]);
-      acc[db] = emfma(ecat_tr(lds_read_tr(xt + 4096, toff[0][db]), lds_read_tr(xt + 4096, toff[1][db])), xb8, acc[db]);
     }
     dma_wait();
     if (j + 1 < nc && wv == 0) {
@@ -439,26 +458,11 @@ __global__ __launch_bounds__(512, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
     inext = inn;
   }
 
-  // sum the query-half partials: qh = 1 waves hand theirs to the qh = 0 waves of the same key half (each group in
-  // its own half of the staging buffers)
-  float* xa = reinterpret_cast<float*>(&qd_s[0][0][0]) + grp * (2 * 64 * 64) + kh * (64 * 64);
-  if (qh == 1) {
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) xa[(db * 16 + r) * 64 + l] = acc[db][r];
-  }
-  __syncthreads();
-  if (qh == 1) return;
-#pragma unroll
-  for (int db = 0; db < NDB; ++db)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[db][r] += xa[(db * 16 + r) * 64 + l];
 #pragma unroll
   for (int db = NDB; db < 4; ++db) acc[db] = f32x16{};  // columns past D: zero
   const size_t tok = head + (size_t)kb * BK + key;
   if (TASKS && slot >= 0) {
-    float* pa_out = (grp == 0 ? a.part_b : a.part_a) + ((size_t)slot * BK + key) * HD;
+    float* pa_out = (role == 0 ? a.part_b : a.part_a) + ((size_t)slot * BK + key) * HD;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -470,10 +474,10 @@ __global__ __launch_bounds__(512, 1) void vsa_bwd_kv_kernel(VsaBwdArgs a) {
   // valid keys: dK or dV + add / cnt; padding keys: 0
   const float inv = kvalid ? 1.0f / (float)kcnt : 0.0f;
   const float keep = kvalid ? 1.0f : 0.0f;
-  const float* add = grp == 0 ? a.add_b : a.add_a;
+  const float* add = role == 0 ? a.add_b : a.add_a;
   const float* adp = add + ((size_t)bh * a.add_nb + kb) * HD;
-  float* out32 = grp == 0 ? a.out_b32 : a.out_a32;
-  e16_t* out16 = grp == 0 ? a.out_b : a.out_a;
+  float* out32 = role == 0 ? a.out_b32 : a.out_a32;
+  e16_t* out16 = role == 0 ? a.out_b : a.out_a;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -756,8 +760,8 @@ extern "C" int ES_VSA_API(vsa_attn_bwd_kv)(const void* q, const void* k, const v
   ES_REQUIRE(balanced_launch(BH, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "VSA: row-block queues unavailable");
   a.queues = qs.counters;
   a.fixed = qs.fixed;
-  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_kernel<false, 64>), dim3((unsigned)qs.grid), dim3(512), 0, stream, a);
-  else hipLaunchKernelGGL((vsa_bwd_kv_kernel<false, 128>), dim3((unsigned)qs.grid), dim3(512), 0, stream, a);
+  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_kernel<false, 64>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((vsa_bwd_kv_kernel<false, 128>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
   return check_launch("vsa_attn_bwd_kv");
 }
 
@@ -781,8 +785,8 @@ extern "C" int ES_VSA_API(vsa_attn_bwd_kv_tasks)(const void* q, const void* k, c
   a.out_b = (e16_t*)dv;
   a.part_a = part_dk;
   a.part_b = part_dv;
-  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_kernel<true, 64>), dim3((unsigned)max_tasks), dim3(512), 0, stream, a);
-  else hipLaunchKernelGGL((vsa_bwd_kv_kernel<true, 128>), dim3((unsigned)max_tasks), dim3(512), 0, stream, a);
+  if (D == 64) hipLaunchKernelGGL((vsa_bwd_kv_kernel<true, 64>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((vsa_bwd_kv_kernel<true, 128>), dim3((unsigned)max_tasks), dim3(256), 0, stream, a);
   return check_launch("vsa_attn_bwd_kv_tasks");
 }
 
