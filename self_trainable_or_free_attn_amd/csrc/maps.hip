@@ -31,9 +31,10 @@ __global__ __launch_bounds__(64) void means_kernel(const bf16_t* __restrict__ k,
   vm[o + 1] = f2bf(v1 / inv);
 }
 
-// Four query tiles x 16 sampled rows (rows t*128 + 8i) = 64 queries per workgroup, one head. Each wave takes
-// 32-key chunks of the block means round-robin: S = Q Kmean^T with Q as the A operand (two 32-row M tiles) and
-// the key chunk as the B operand read straight from global memory.
+// Sixteen query tiles per workgroup, one head; each wave owns four of them: 4 x 16 sampled rows (rows t*128 + 8i)
+// = 64 queries, and walks every 32-key chunk of the block means: S = Q Kmean^T with Q as the A operand (two 32-row
+// M tiles) and the key chunk as the B operand read straight from global memory, one chunk ahead. The waves are
+// independent (no barrier): a wave's four tiles get their sums, their map entries and their scales from it alone.
 __global__ __launch_bounds__(256) void estimate_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ km,
                                                        const uint8_t* __restrict__ keep,
                                                        const float* __restrict__ m_prev,
@@ -41,9 +42,9 @@ __global__ __launch_bounds__(256) void estimate_kernel(const bf16_t* __restrict_
                                                        float* __restrict__ scale_exact,
                                                        float* __restrict__ scale_skip, int L, int H, int nq, int NB,
                                                        float scale, float lb_last) {
-  __shared__ float red_num[4][4], red_den[4][4];
-  const int t0 = blockIdx.x * 4, h = blockIdx.y;
   const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, hi = l >> 5, lq = l & 31;
+  const int t0 = blockIdx.x * 16 + wv * 4, h = blockIdx.y;
+  if (t0 >= nq) return;
 
   // A operands: query qi = 32*mb + lq, tile t0 + qi/16, sample qi%16
   bf16x8 qa[2][8];
@@ -88,8 +89,8 @@ __global__ __launch_bounds__(256) void estimate_kernel(const bf16_t* __restrict_
     for (int ks = 0; ks < 8; ++ks) b[ks] = *reinterpret_cast<const bf16x8*>(kr + 16 * ks + 8 * hi);
   };
   bf16x8 bn[8];
-  if (wv < nchunks) load_b(wv, bn);
-  for (int c = wv; c < nchunks; c += 4) {
+  load_b(0, bn);
+  for (int c = 0; c < nchunks; ++c) {
     const int key = c * 32 + lq;
     const bool kvalid = key < NB;
     bf16x8 bc[8];
@@ -109,7 +110,7 @@ __global__ __launch_bounds__(256) void estimate_kernel(const bf16_t* __restrict_
         mv[tl] = map[o];
       }
     }
-    if (c + 4 < nchunks) load_b(c + 4, bn);
+    if (c + 1 < nchunks) load_b(c + 1, bn);
     f32x16 acc[2] = {f32x16{}, f32x16{}};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
@@ -143,34 +144,28 @@ __global__ __launch_bounds__(256) void estimate_kernel(const bf16_t* __restrict_
       }
     }
   }
+  // the wave's four tiles: f over each tile's rows, then the scales
 #pragma unroll
   for (int tl = 0; tl < 4; ++tl) {
-    const float a = wave_sum(num[tl]), b = wave_sum(den[tl]);
+    const float sn = wave_sum(num[tl]), sd = wave_sum(den[tl]);
+    const int tt = t0 + tl;
+    if (tt >= nq) break;
+    const int nrows = min(L - tt * BM, BM);
+    float f = 0.0f;
+    for (int r = l; r < BM; r += 64) {
+      const int row = tt * BM + r;
+      if (row < L) {
+        const size_t o = (size_t)row * H + h;
+        f += exp2f(fminf(fmaxf(m_prev[o] - m_new[o], -100.0f), 100.0f));
+      }
+    }
+    f = wave_sum(f) / (float)nrows;
     if (l == 0) {
-      red_num[wv][tl] = a;
-      red_den[wv][tl] = b;
+      const float nn = sn / (float)nrows;
+      const float c = sd > 0.0f ? fminf(fmaxf(nn / fmaxf(sd, 1e-30f), 1.0f), 64.0f) : 1.0f;
+      scale_exact[h * nq + tt] = f / (float)nrows;
+      scale_skip[h * nq + tt] = f * c;
     }
-  }
-  __syncthreads();
-  // wave wv finishes tile t0 + wv: f over its rows, then the scales
-  const int tt = t0 + wv;
-  if (tt >= nq) return;
-  const int nrows = min(L - tt * BM, BM);
-  float f = 0.0f;
-  for (int r = l; r < BM; r += 64) {
-    const int row = tt * BM + r;
-    if (row < L) {
-      const size_t o = (size_t)row * H + h;
-      f += exp2f(fminf(fmaxf(m_prev[o] - m_new[o], -100.0f), 100.0f));
-    }
-  }
-  f = wave_sum(f) / (float)nrows;
-  if (l == 0) {
-    const float nn = (red_num[0][wv] + red_num[1][wv] + red_num[2][wv] + red_num[3][wv]) / (float)nrows;
-    const float dd = red_den[0][wv] + red_den[1][wv] + red_den[2][wv] + red_den[3][wv];
-    const float c = dd > 0.0f ? fminf(fmaxf(nn / fmaxf(dd, 1e-30f), 1.0f), 64.0f) : 1.0f;
-    scale_exact[h * nq + tt] = f / (float)nrows;
-    scale_skip[h * nq + tt] = f * c;
   }
 }
 
@@ -199,7 +194,7 @@ extern "C" int es_estimate_skipped(const void* q, const void* k_mean, const uint
   const int nq = (L + BM - 1) / BM, nb = (L + BK - 1) / BK;
   const float scale = LOG2E / sqrtf((float)HD);
   const float lb_last = log2f((float)(L - (nb - 1) * BK));
-  hipLaunchKernelGGL(estimate_kernel, dim3((nq + 3) / 4, H), dim3(256), 0, stream, (const bf16_t*)q,
+  hipLaunchKernelGGL(estimate_kernel, dim3((nq + 15) / 16, H), dim3(256), 0, stream, (const bf16_t*)q,
                      (const bf16_t*)k_mean, keep, offset, lse, mass, scale_exact, scale_skip, L, H, nq, nb, scale,
                      lb_last);
   return check_launch("es_estimate_skipped");
