@@ -42,40 +42,32 @@ __device__ __forceinline__ int2 block_scan(int x, int* scan_s) {
 // [lo, hi) and at the midpoints of both halves, then takes the step at m and the step the original would take
 // next. Wave counts are popcounts of ballots (no cross-lane arithmetic); 16 rounds = 32 steps, and a step on a
 // converged interval (hi - lo <= 1) leaves lo as it is, so the result equals the 31-step search.
+// The search runs bit by bit from bit 30 down (bit 31, the sign, is clear in every value that can count): x takes
+// bit b when at least K elements are >= x | (1 << b). The count falls as x grows, so this ends at the largest x
+// whose count reaches K, which is 0 when no x >= 0 does, the bisection's answer; K <= 0 gives its upper end, +inf.
+// Values are at most +inf (no NaN patterns), so the result never passes it. One threshold per round: the cost is
+// the comparisons per element (31 here; 48 for four-way steps, 77 and 120 for eight- and sixteen-way ones, which
+// measured slower in that order), not the barriers. Waves with no valid element (`live` false) count nothing.
 template <int E>
-__device__ int kth_largest(const int (&bits)[E], int K, int* red, int& parity) {
+__device__ int kth_largest(const int (&bits)[E], int K, bool live, int* red, int& parity) {
+  if (K <= 0) return 0x7F800000;
   const int wv = threadIdx.x >> 6;
-  int lo = 0, hi = 0x7F800001;
-  for (int it = 0; it < 16; ++it) {
-    const int m = lo + (hi - lo) / 2;
-    const int ml = lo + (m - lo) / 2, mh = m + (hi - m) / 2;
-    int c[3] = {0, 0, 0};
+  int x = 0;
+  for (int b = 30; b >= 0; --b) {
+    const int t = x | (1 << b);
+    int c = 0;
+    if (live) {
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      c[0] += __builtin_popcountll(__builtin_amdgcn_ballot_w64(bits[e] >= ml));
-      c[1] += __builtin_popcountll(__builtin_amdgcn_ballot_w64(bits[e] >= m));
-      c[2] += __builtin_popcountll(__builtin_amdgcn_ballot_w64(bits[e] >= mh));
+      for (int e = 0; e < E; ++e) c += __builtin_popcountll(__builtin_amdgcn_ballot_w64(bits[e] >= t));
     }
-    int* r = red + parity * 12;
-    if ((threadIdx.x & 63) == 0) {
-      r[wv * 3 + 0] = c[0];
-      r[wv * 3 + 1] = c[1];
-      r[wv * 3 + 2] = c[2];
-    }
+    int* r = red + parity * 4;
+    if ((threadIdx.x & 63) == 0) r[wv] = c;
     __syncthreads();
-    int t[3];
-#pragma unroll
-    for (int k = 0; k < 3; ++k) t[k] = r[k] + r[3 + k] + r[6 + k] + r[9 + k];
+    const int tot = r[0] + r[1] + r[2] + r[3];
     parity ^= 1;
-    if (t[1] >= K) {
-      lo = m;
-      if (t[2] >= K) lo = mh; else hi = mh;
-    } else {
-      hi = m;
-      if (t[0] >= K) lo = ml; else hi = ml;
-    }
+    if (tot >= K) x = t;
   }
-  return lo;
+  return x;
 }
 
 template <int E>
@@ -88,7 +80,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(const float* __rest
                                                               int* __restrict__ bits_out, int nw, int* __restrict__ ridx,
                                                               int rw, int K, int R, int NB, int L, int H, int nq,
                                                               int sink, int nwords) {
-  __shared__ int red[24];
+  __shared__ int red[8];  // two rounds' per-wave counts (kth_largest)
   __shared__ int scan_s[4];
   const int t = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x;
@@ -116,7 +108,8 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(const float* __rest
     vb[e] = __float_as_int(val);
   }
   int parity = 0;
-  const float thr = __int_as_float(kth_largest<E>(vb, K, red, parity));
+  const bool live = (int)(threadIdx.x & ~63u) * E < NB;  // (wave-uniform: the wave's first block)
+  const float thr = __int_as_float(kth_largest<E>(vb, K, live, red, parity));
   bool kp[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
@@ -125,7 +118,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(const float* __rest
     r2 = (valid[e] && !kp[e]) ? r2 : -1.0f;
     rb[e] = __float_as_int(r2);
   }
-  const int rthr = kth_largest<E>(rb, R, red, parity);
+  const int rthr = kth_largest<E>(rb, R, live, red, parity);
   bool ref[E];
   int ncand_local = 0, nkeep_local = 0;
 #pragma unroll
