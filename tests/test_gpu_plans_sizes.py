@@ -58,9 +58,34 @@ def _maps(nb, case, seed):
 @pytest.mark.parametrize("nb", SIZES)
 @pytest.mark.parametrize("case", ["smooth", "ties"])
 def test_select_pack_rebuild_bit_exact_at_size(nb, case, dev):
+    top, refined = ref.budget(0.1, nb)
+    rr, rc = _check(nb, case, top, refined, dev)
+    # the case must exercise what it claims: a non-trivial refine list, and (ties) kept sets beyond the budget
+    assert (rr < nb).any()
+    if case == "ties":
+        assert (rc > top).any()
+
+
+# budgets at the ends of the K-th largest search: nothing (K = 0: the threshold is +inf, only forced and infinite
+# entries are kept), one block, every block (K = nb: at most nb values, the threshold falls to the smallest), and
+# a refine budget as large as the block count
+EDGE_BUDGETS = {"none": lambda nb: (0, 0), "one": lambda nb: (1, 1), "all": lambda nb: (nb, 0),
+                "refine_all": lambda nb: (0, nb)}
+
+
+@pytest.mark.parametrize("nb", [300, 1182])
+@pytest.mark.parametrize("case", ["smooth", "ties"])
+@pytest.mark.parametrize("budget", sorted(EDGE_BUDGETS))
+def test_select_bit_exact_at_edge_budgets(nb, case, budget, dev):
+    top, refined = EDGE_BUDGETS[budget](nb)
+    _check(nb, case, top, refined, dev)
+
+
+def _check(nb, case, top, refined, dev):
+    """select_blocks, pack_plan and rebuild_plan on one map against the oracle, byte for byte; returns the oracle's
+    refine lists and counts."""
     L, mass, keep_prev, se, ss, flags, sink = _maps(nb, case, seed=nb + (case == "ties"))
     nq = ref.cdiv(L, 128)
-    top, refined = ref.budget(0.1, nb)
     rw, words = -(-refined // 32) * 32, ref.plan_words(nb)
     print(f"[plans] nb={nb} case={case} L={L} E={max(1, ref.next_pow2(nb) // 256)} top={top} refined={refined}",
           flush=True)
@@ -82,10 +107,6 @@ def test_select_pack_rebuild_bit_exact_at_size(nb, case, dev):
     assert np.array_equal(blocks.cpu().numpy()[used], rb[used]), "blocks"
     assert np.array_equal(refine.cpu().numpy(), rr), "refine"
     assert np.array_equal(skip.cpu().numpy(), rs), "skip bits"
-    # the case must exercise what it claims: a non-trivial refine list, and (ties) kept sets beyond the budget
-    assert (rr < nb).any()
-    if case == "ties":
-        assert (rc > top).any()
 
     exact = torch.full((H, nq, words), 5, device=dev, dtype=torch.int32)
     K().pack_plan(keep, exact)
@@ -109,3 +130,4 @@ def test_select_pack_rebuild_bit_exact_at_size(nb, case, dev):
     assert np.array_equal(lmc.cpu().numpy(), omc), "mean counts"
     used = np.arange(nb)[None, None, :] < omc[..., None]
     assert np.array_equal(lm.cpu().numpy()[used], om[used]), "mean lists"
+    return rr, rc
