@@ -38,11 +38,7 @@ __device__ __forceinline__ int2 block_scan(int x, int* scan_s) {
   return make_int2(before + inc - x, total);
 }
 
-// The reference's 31-step bisection, two steps per workgroup exchange: one round counts at the midpoint m of
-// [lo, hi) and at the midpoints of both halves, then takes the step at m and the step the original would take
-// next. Wave counts are popcounts of ballots (no cross-lane arithmetic); 16 rounds = 32 steps, and a step on a
-// converged interval (hi - lo <= 1) leaves lo as it is, so the result equals the 31-step search.
-// The search runs bit by bit from bit 30 down (bit 31, the sign, is clear in every value that can count): x takes
+// The K-th largest of a (tile, head)'s values: the search runs bit by bit from bit 30 down (bit 31, the sign, is clear in every value that can count): x takes
 // bit b when at least K elements are >= x | (1 << b). The count falls as x grows, so this ends at the largest x
 // whose count reaches K, which is 0 when no x >= 0 does, the bisection's answer; K <= 0 gives its upper end, +inf.
 // Values are at most +inf (no NaN patterns), so the result never passes it. One threshold per round: the cost is
