@@ -101,11 +101,14 @@ __global__ __launch_bounds__(64) void kmeans_tab_kernel(KmArgs a) {
   }
   __syncthreads();
 
+  // A round whose assignment leaves every label as it was would rebuild the same centroids from the same members in
+  // the same order, and so would every round after it: the loop stops there with the tables, counts and labels
+  // that all a.iters rounds give.
   int cnt[RM];
   for (int it = 0; it < a.iters; ++it) {
     // assignment: lane = token
+    int best = 0;
     if (l < n) {
-      int best = 0;
       float bd = 0.0f;
 #pragma unroll
       for (int c = 0; c < RM; ++c) {
@@ -126,8 +129,9 @@ __global__ __launch_bounds__(64) void kmeans_tab_kernel(KmArgs a) {
           best = c;
         }
       }
-      lab_s[l] = best;
     }
+    if (it > 0 && __builtin_amdgcn_ballot_w64(l < n && best != lab_s[l]) == 0ull) break;  // (one wave: uniform)
+    if (l < n) lab_s[l] = best;
     __syncthreads();
     // update: lane = columns 2l, 2l + 1
     float s0[RM], s1[RM];
