@@ -170,7 +170,8 @@ __global__ __launch_bounds__(64) void kmeans_tab_kernel(KmArgs a) {
     v0[c] = 0.0f;
     v1[c] = 0.0f;
   }
-  for (int t = 0; t < n; ++t) {
+#pragma unroll 8
+  for (int t = 0; t < n; ++t) {  // (eight rows' loads in flight together; the sums take the rows in order)
     const int lb = lab_s[t];
     const unsigned u = *reinterpret_cast<const unsigned*>(vb + (size_t)t * HD + 2 * l);
     const float y0 = e2f((e16_t)(u & 0xffffu)), y1 = e2f((e16_t)(u >> 16));
