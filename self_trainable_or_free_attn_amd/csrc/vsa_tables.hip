@@ -141,6 +141,7 @@ __global__ __launch_bounds__(64) void kmeans_tab_kernel(KmArgs a) {
       s1[c] = 0.0f;
       cnt[c] = 0;
     }
+#pragma unroll 8
     for (int t = 0; t < n; ++t) {
       const int lb = lab_s[t];
       const float x0 = e2f(x_s[t][2 * l]), x1 = e2f(x_s[t][2 * l + 1]);
