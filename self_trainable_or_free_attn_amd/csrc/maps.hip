@@ -14,7 +14,8 @@ __global__ __launch_bounds__(64) void means_kernel(const bf16_t* __restrict__ k,
   const int j = blockIdx.x, h = blockIdx.y, l = threadIdx.x;
   const int n = min(L - j * BK, BK);
   float k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
-  for (int r = 0; r < n; ++r) {
+#pragma unroll 8
+  for (int r = 0; r < n; ++r) {  // (eight rows' loads in flight together; the sums take the rows in order)
     const size_t o = ((size_t)(j * BK + r) * H + h) * HD + 2 * l;
     const unsigned kw = *reinterpret_cast<const unsigned*>(k + o);
     const unsigned vw = *reinterpret_cast<const unsigned*>(v + o);

@@ -130,7 +130,8 @@ __global__ __launch_bounds__(256) void gram_reduce_kernel(float* __restrict__ gr
   const int h = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
   float* g = gram + (size_t)h * splits * HD * HD + i;
   float s = 0.0f;
-  for (int sp = 0; sp < splits; ++sp) s += g[(size_t)sp * HD * HD];
+#pragma unroll 8
+  for (int sp = 0; sp < splits; ++sp) s += g[(size_t)sp * HD * HD];  // (loads in flight together, sums in order)
   g[0] = s;
 }
 
@@ -202,7 +203,8 @@ __global__ __launch_bounds__(64) void probe_kernel(const bf16_t* __restrict__ q,
   const int blk = (int)((float)(i * (NB - 1)) / (float)(NPROBE - 1) + 0.5f);
   const int r0 = blk * BK, n = max(min(L - r0, BK), 0);
   float a = 0.f, b = 0.f;
-  for (int r = 0; r < n; ++r) {
+#pragma unroll 8
+  for (int r = 0; r < n; ++r) {  // (eight rows' loads in flight together; the sums take the rows in order)
     const unsigned w = *reinterpret_cast<const unsigned*>(q + ((size_t)(r0 + r) * H + h) * HD + 2 * l);
     a += __uint_as_float(w << 16);
     b += __uint_as_float(w & 0xffff0000u);
