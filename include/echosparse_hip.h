@@ -3,8 +3,10 @@
  * Every entry point takes caller-owned device pointers (no allocation inside), plain sizes and the HIP stream to
  * enqueue on, never synchronises, and returns an es_status; on failure es_last_error_string() holds a message.
  * es_block_attention, es_sparse_attention, es_dense_attention and es_dense_attention_kv balance their tiles over
- * the XCDs through counters in a ring of 64 slots of device memory, one slot per call: up to 63 such calls may
- * overlap on one GPU.
+ * the XCDs through counters in a ring of 64 slots of device memory, one slot per call: any number of such calls
+ * may overlap on one GPU (a call waits on its stream for the previous user of its slot). Calls recorded in a stream
+ * capture take slots from a second ring of 64 without waiting: graph replays may overlap uncaptured calls, not each
+ * other.
  * Tensor layouts are the reference's (shapes in row-major order):
  *   q, k, v            (L, H, D) bf16, D = 128                       token-major, as echosparse passes them
  *   offset, lse        (nq * 128, H) float32, log2 units, 1e30 for rows >= L
@@ -31,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ES_ABI_VERSION 1
+#define ES_ABI_VERSION 2  /* 2: lc_mid_stride, lc_stride, and the k-means labels / mid_counts of vsa_rep_unpool */
 
 enum es_status {
   ES_OK = 0,

@@ -4,7 +4,9 @@
  * allocation and no synchronisation inside, an es_status return and es_last_error_string() on failure.
  * vsa_attn_fwd, vsa_attn_bwd_kv, vsa_attn_bwd_q, vsa_rep_attn_fwd and vsa_rep_attn_bwd_q balance their row blocks
  * over the XCDs through counters in a 64-slot ring of device memory per source file, one slot per kernel launch;
- * a launch that takes a slot waits (on its stream) for the slot's previous launch, so launches may overlap freely.
+ * a launch that takes a slot waits (on its stream) for the slot's previous launch, so uncaptured launches may overlap
+ * freely; launches recorded in a stream capture use a second ring of 64 slots and do not wait, so graph replays may
+ * overlap uncaptured launches but not each other.
  * Layouts (row-major):
  *   tokens q, k, v, o, gate, dO      [BH, L, 128] bf16 (fp16: the _f16 twins), L = NB * 64, valid-first
  *                                    64-token blocks

@@ -377,12 +377,6 @@ def rebuild_plan(exact_bits, skip_bits, nb, refine_width):
     return keep, counts, blocks, refine, rcounts, means, mcounts
 
 
-def launched_tiles(L, rows):
-    """Query tiles the attention launches for `rows` (reference echosparse/kernels/sm120.py:111-120)."""
-    nq = cdiv(L, BM)
-    return nq if rows is None else cdiv(rows, BM)
-
-
 def budget(density, nb):
     """Exact blocks and refined blocks per tile (reference echosparse/attention.py:267-270)."""
     top = max(1, int(round(density * nb)))

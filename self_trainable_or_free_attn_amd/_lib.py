@@ -20,6 +20,9 @@ LIB_PATH = os.environ.get("ECHOSPARSE_HIP_LIB") or os.path.join(os.path.dirname(
                                                                 "libechosparse_hip.so")
 TORCH_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libechosparse_torch.so")
 
+# the ES_ABI_VERSION of include/echosparse_hip.h these bindings follow; a library reporting another is refused
+ABI_VERSION = 2
+
 P, I, F, Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
 LL, DB = ctypes.c_longlong, ctypes.c_double
 
@@ -100,6 +103,9 @@ def lib():
             fn = getattr(so, name)
             fn.argtypes = args
             fn.restype = res
+        if so.es_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} implements ABI version {so.es_abi_version()}, these bindings follow "
+                               f"version {ABI_VERSION}: rebuild it with build_lib")
         _lib = so
     return _lib
 

@@ -54,9 +54,10 @@ def dense_attention(q, k, v, return_lse=False):
 
 
 class _CompactState:
-    """State of one layer: the offsets of every branch and the plans (exact and skip bit masks). One branch rewrites
-    its plan in place once the step has used it; with CFG branch 0 writes the other of two plans while later
-    branches still read the current one (reference attention.py:72-96)."""
+    """Persistent per-layer state: a log2 softmax offset per branch and, per plan slot, a pair of bit masks (exact
+    blocks, skipped blocks). Without CFG a single branch overwrites the slot it has just consumed; with CFG the
+    selecting branch 0 fills the second slot for the next step, so branches 1.. of the current step keep reading an
+    unchanged first slot (reference attention.py:72-96)."""
 
     _serial = 0
 
@@ -68,9 +69,9 @@ class _CompactState:
         self.words = max(_next_pow2(nb) // 32, 4 * _cdiv(nb, 128))
         self.plans = []
         self.offsets = {}
-        self.ready = set()          # branches that have run the full step
-        self.current = None         # (plan, step) used by the branches of this step
-        self.pending = None         # (plan, step) made by branch 0 for the next step
+        self.ready = set()          # branch ids whose offset already comes from a full-block pass
+        self.current = None         # (slot, step): what this step's sparse calls read
+        self.pending = None         # (slot, step): written by branch 0, consumed from the next step on
 
     def plan(self, i):
         while len(self.plans) <= i:
@@ -85,7 +86,8 @@ class _CompactState:
 
 
 class _PlanScratch:
-    """Per-call tensors shared by all layers (reference attention.py:99-116)."""
+    """Selection and list tensors for one (L, H, refine width); every layer reuses them, since only one layer's
+    selection is live at a time (reference attention.py:99-116)."""
 
     def __init__(self, L, H, device, refine_width):
         nq, nb = _cdiv(L, BM), _cdiv(L, BK)
@@ -111,7 +113,8 @@ class _PlanScratch:
 
 
 class _Buffers:
-    """Per-call scratch for one sequence shape (reference attention.py:119-130)."""
+    """Block means, flags, representatives and the all-blocks lists for one (L, H, D), reused by every layer
+    (reference attention.py:119-130)."""
 
     def __init__(self, L, H, D, device, refine_iters, K):
         nq, nb = _cdiv(L, BM), _cdiv(L, BK)

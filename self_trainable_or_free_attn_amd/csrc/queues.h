@@ -15,8 +15,10 @@
 // A slot is reused only after its previous launch: every balanced launch records the slot's event on its stream
 // once it is enqueued (when its Queues object is released), and the next launch that takes the slot makes its own
 // stream wait for that event before clearing the counters, so launches in flight on any number of streams never
-// share counters. (Inside a stream capture there is no wait and no record: a captured graph replays its launches
-// in its own order, and replays of one graph must not overlap.)
+// share counters. Launches recorded inside a stream capture take their slots from a second ring of 64 (there is
+// no wait and no record in a capture: a graph replays its launches in its own order), so a replay never shares
+// counters with uncaptured launches; replays that overlap each other race if two of their captured launches took
+// the same slot of that ring (64 captured launches apart), so replays of captured graphs must not overlap.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -96,7 +98,7 @@ __device__ __forceinline__ bool balanced_head_item(int* queues, int fixed, int g
   return hd < heads;
 }
 
-static __device__ int es_tile_queues[64 * 8];
+static __device__ int es_tile_queues[128 * 8];
 
 static __global__ __launch_bounds__(64) void zero_queues_kernel(int* q) {
   if (threadIdx.x < 8) q[threadIdx.x] = 0;
@@ -105,10 +107,11 @@ static __global__ __launch_bounds__(64) void zero_queues_kernel(int* q) {
 // The counter ring of one GPU: the slots' device memory, one event per slot marking the end of its last launch,
 // and one host lock per slot held from the slot's hand-out until that event is recorded.
 struct QueueRing {
-  int* base = nullptr;
+  int* base = nullptr;  // 64 slots for uncaptured launches, then 64 for captured ones
   hipEvent_t done[64] = {};
   std::mutex held[64];
   std::atomic<unsigned> seq{0};
+  std::atomic<unsigned> seq_captured{0};
 };
 
 static QueueRing* queue_ring() {
@@ -146,8 +149,10 @@ struct Queues {
   ~Queues() { release(); }
   void release() {
     if (slot < 0) return;
-    if (!captured) (void)hipEventRecord(ring->done[slot], stream);
-    ring->held[slot].unlock();
+    if (!captured) {
+      (void)hipEventRecord(ring->done[slot], stream);
+      ring->held[slot].unlock();
+    }
     slot = -1;
   }
 };
@@ -159,13 +164,18 @@ static bool balanced_launch_queues(int per_queue, hipStream_t stream, Queues& ou
   out.release();
   QueueRing* r = queue_ring();
   if (r == nullptr) return false;
-  const int slot = (int)(r->seq.fetch_add(1) % 64);
-  r->held[slot].lock();
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   const bool captured = hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
-  if (!captured && hipStreamWaitEvent(stream, r->done[slot], 0) != hipSuccess) {
-    r->held[slot].unlock();
-    return false;
+  int slot;
+  if (captured) {
+    slot = 64 + (int)(r->seq_captured.fetch_add(1) % 64);
+  } else {
+    slot = (int)(r->seq.fetch_add(1) % 64);
+    r->held[slot].lock();
+    if (hipStreamWaitEvent(stream, r->done[slot], 0) != hipSuccess) {
+      r->held[slot].unlock();
+      return false;
+    }
   }
   out.ring = r;
   out.slot = slot;

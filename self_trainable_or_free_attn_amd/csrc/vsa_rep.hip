@@ -790,6 +790,8 @@ extern "C" int ES_VSA_API(vsa_rep_bwd_tables)(const void* q, const void* dout, c
   ES_REQUIRE(q && dout && k_tab && v_tab && lc && lse && delta && bits_a && bits_ab && dk_tab && dv_tab,
              ES_ERR_INVALID, "VSA2-rep: null tensor pointer");
   ES_REQUIRE(tier == 2 || tier == 4, ES_ERR_INVALID, "VSA2-rep: tier must be 2 (B, mid table) or 4 (C, tail table)");
+  ES_REQUIRE(lc_stride == 0 || lc_stride >= (L / BK) * (tier == 2 ? RM : 1), ES_ERR_INVALID,
+             "VSA2-rep: lc_stride must be 0 (shared) or >= the table's rows (NB * RM for tier 2, NB for tier 4)");
   TabArgs a = {};
   a.q = (const e16_t*)q;
   a.dout = (const e16_t*)dout;

@@ -55,7 +55,8 @@ __global__ __launch_bounds__(64) void kmeans_tab_kernel(KmArgs a) {
   __shared__ int lab_s[BK];
   __shared__ int perm_s[BK];
   const int blk = blockIdx.x, bh = blockIdx.y, l = threadIdx.x;
-  const int n = a.blk_cnt[blk];
+  // a block holds 0..64 valid keys; clamping keeps an out-of-range count inside the 64-row LDS arrays and the block
+  const int n = min(max(a.blk_cnt[blk], 0), BK);
   const size_t tok0 = (size_t)bh * a.L + (size_t)blk * BK;
   const e16_t* kb = a.k + tok0 * HD;
   const e16_t* vb = a.v + tok0 * HD;

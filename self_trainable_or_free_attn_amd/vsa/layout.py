@@ -73,38 +73,37 @@ def build_layout(shape, tile=(4, 4, 4), sub=None, R: int = 8, device="cpu") -> B
 
 
 def tail_block_counts(L_valid: int, device="cpu") -> torch.Tensor:
-    """1-D sequences: blocks of 64 consecutive tokens, the last one partial."""
-    nb = math.ceil(L_valid / 64)
-    cnt = torch.full((nb,), 64, dtype=torch.int32)
-    cnt[-1] = L_valid - 64 * (nb - 1)
-    return cnt.to(device)
+    """Valid-token count of each 64-token block when a sequence of L_valid tokens is cut into consecutive blocks:
+    64 everywhere except the final block, which keeps the remainder."""
+    starts = torch.arange(0, L_valid, 64, dtype=torch.int32)
+    return (L_valid - starts).clamp(max=64).to(torch.int32).to(device)
 
 
 def sequence_layout(n: int, device="cpu") -> BlockLayout:
-    """1-D sequences: blocks of 64 consecutive tokens, the last one partial."""
+    """Layout of a plain 1-D sequence: token i sits in slot i, the slots past n (the final block's padding) hold no
+    token (gather index -1)."""
     cnt = tail_block_counts(n)
-    gather = torch.full((cnt.numel() * 64,), -1, dtype=torch.int64)
-    gather[:n] = torch.arange(n)
+    slots = torch.arange(cnt.numel() * 64, dtype=torch.int64)
+    gather = torch.where(slots < n, slots, torch.full_like(slots, -1))
     return BlockLayout((n,), (64,), (), gather.to(device), torch.arange(n, device=device), cnt.to(device))
 
 
 def to_blocked(x: torch.Tensor, lay: BlockLayout) -> torch.Tensor:
-    """[B, H, N, ...] real tokens -> [B, H, NB * 64, ...] block-padded (padding = 0)."""
+    """Place the N real tokens of x [B, H, N, ...] into their block slots: [B, H, NB * 64, ...], zeros in the slots
+    that hold no token."""
     out = x.new_zeros(*x.shape[:2], lay.padded_len, *x.shape[3:])
-    out[:, :, lay.scatter] = x
-    return out
+    return out.index_copy(2, lay.scatter, x)
 
 
 def from_blocked(y: torch.Tensor, lay: BlockLayout) -> torch.Tensor:
-    """[B, H, NB * 64, ...] -> [B, H, N, ...] real tokens in their original order."""
-    return y[:, :, lay.scatter]
+    """Inverse of to_blocked: read every real token's slot of y [B, H, NB * 64, ...] back into the original token
+    order, [B, H, N, ...]."""
+    return y.index_select(2, lay.scatter)
 
 
 def pad_tail(x: torch.Tensor, L_valid: int) -> torch.Tensor:
-    """[B, H, L_valid, D] -> [B, H, ceil(L / 64) * 64, D], zero-padded at the end."""
-    nb = math.ceil(L_valid / 64)
-    if nb * 64 == L_valid:
+    """Extend x [B, H, L_valid, D] along the token axis with zero rows up to the next multiple of 64."""
+    extra = -L_valid % 64
+    if extra == 0:
         return x.contiguous()
-    out = x.new_zeros(*x.shape[:2], nb * 64, x.shape[3])
-    out[:, :, :L_valid] = x
-    return out
+    return torch.nn.functional.pad(x, (0, 0, 0, extra))

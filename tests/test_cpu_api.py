@@ -112,7 +112,7 @@ def test_library_exports_every_declared_entry_point():
     missing = [n for n in names if not hasattr(so, n)]
     assert not missing, missing
     so.es_abi_version.restype = ctypes.c_int
-    assert so.es_abi_version() == 1
+    assert so.es_abi_version() == 2
 
 
 def test_ctypes_signatures_cover_the_header():

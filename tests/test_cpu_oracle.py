@@ -269,6 +269,17 @@ def test_pack_rebuild_round_trip():
             assert m2[t, h, :mc[t, h]].tolist() == sorted(set(range(nb)) - listed)
 
 
+def test_plan_word_bit_order_known_value():
+    """Bit i of plan word w is block 32 w + i, and the bits of blocks nb..next_pow2(nb) - 1 are set (reference
+    echosparse/kernels/sm120.py:258-267): nb = 40 with blocks 0, 5 and 33 kept gives words 0x21 and 0xFFFFFF02;
+    the words past next_pow2(nb) / 32 keep the plans' initial -1."""
+    keep = np.zeros((1, 1, 40), np.uint8)
+    keep[0, 0, [0, 5, 33]] = 1
+    words = ref.pack_plan(keep, 4)
+    assert words.tolist() == [[[0x21, -254, -1, -1]]]
+    assert np.int32(-254).view(np.uint32) == 0xFFFFFF02
+
+
 def test_budget_known_values():
     assert ref.budget(0.10, 1182) == (118, 355)         # Wan2.1-14B 720p
     assert ref.budget(0.10, 65) == (6, 20)

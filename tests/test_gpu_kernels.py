@@ -50,10 +50,62 @@ def dense(data):
 
 def test_library_loads_and_reports_errors(dev):
     from self_trainable_or_free_attn_amd import _lib
-    assert _lib.lib().es_abi_version() == 1
+    assert _lib.lib().es_abi_version() == _lib.ABI_VERSION == 2
     q = torch.zeros(64, 1, 64, device=dev, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="head dimension must be 128"):
         _lib.call("es_block_means", q, q, q, q, 64, 1, 64)
+
+
+def test_torch_operators_refuse_views_wrong_dtypes_and_wrapping_ints(data):
+    """The generated operators check every tensor's layout and dtype against the C type and every int against its
+    C range before the launch, so a strided view or an fp32 tensor where bf16 is expected never reaches a kernel."""
+    ops = torch.ops.echosparse_gfx950
+    kd, vd = data["kd"], data["vd"]
+    km = torch.zeros(NB, H, D, device=kd.device, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="argument k must be contiguous"):
+        ops.es_block_means(kd.transpose(0, 1), vd, km, km.clone(), L, H, D)
+    with pytest.raises(RuntimeError, match="argument v must be bfloat16 or float16"):
+        ops.es_block_means(kd, vd.float(), km, km.clone(), L, H, D)
+    with pytest.raises(RuntimeError, match="argument L = 4294967360 is out of range"):
+        ops.es_block_means(kd, vd, km, km.clone(), 2 ** 32 + 64, H, D)
+    cnt = torch.zeros(NQ, H, device=kd.device, dtype=torch.int64)
+    lse = torch.zeros(NQ * 128, H, device=kd.device)
+    with pytest.raises(RuntimeError, match="argument counts must be int32"):
+        ops.es_exact_fallback(data["qd"], kd, vd, torch.empty_like(data["qd"]), cnt, cnt.int(), NB, lse,
+                              cnt.int(), L, H, D)
+    torch.cuda.synchronize()
+
+
+def test_balanced_launch_replays_in_a_graph(data):
+    """A balanced launch (dense attention) captured in a HIP graph takes its counter slot from the captured ring:
+    three replays, with uncaptured launches of the same kernel and host synchronisations between them, each write
+    the eager bytes."""
+    qd, kd, vd = data["qd"], data["kd"], data["vd"]
+    ops = torch.ops.echosparse_gfx950
+    out_e = torch.empty_like(qd)
+    lse_e = torch.empty(NQ * 128, H, device=qd.device)
+    ops.es_dense_attention(qd, kd, vd, out_e, lse_e, L, H, D)
+    torch.cuda.synchronize()
+    out_g = torch.zeros_like(qd)
+    lse_g = torch.zeros_like(lse_e)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            ops.es_dense_attention(qd, kd, vd, out_g, lse_g, L, H, D)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        log("graph replay", rep)
+        out_g.zero_()
+        lse_g.zero_()
+        g.replay()
+        other_o, other_l = torch.empty_like(qd), torch.empty_like(lse_e)
+        ops.es_dense_attention(qd, kd, vd, other_o, other_l, L, H, D)
+        torch.cuda.synchronize()
+        assert torch.equal(out_g.view(torch.int16), out_e.view(torch.int16)), rep
+        assert torch.equal(lse_g, lse_e), rep
+        assert torch.equal(other_o.view(torch.int16), out_e.view(torch.int16)), rep
 
 
 def test_torch_operator_matches_the_direct_c_call_and_compiles(data):
@@ -205,6 +257,17 @@ def test_select_blocks_edge_cases(case, dev):
     assert np.array_equal(blocks.cpu().numpy()[used], r[2][used])
     assert np.array_equal(refine.cpu().numpy(), r[3])
     assert np.array_equal(skip.cpu().numpy(), r[4])
+
+
+def test_pack_plan_bit_order_known_value(dev):
+    """The kernel's plan word layout against a literal: nb = 40 with blocks 0, 5 and 33 kept packs to 0x21,
+    0xFFFFFF02 (bit i of word w = block 32 w + i, blocks 40..63 set); rebuilding lists exactly those blocks."""
+    keep = torch.zeros(1, 1, 40, device=dev, dtype=torch.uint8)
+    keep[0, 0, [0, 5, 33]] = 1
+    exact = torch.full((1, 1, 4), -1, device=dev, dtype=torch.int32)
+    K().pack_plan(keep, exact)
+    torch.cuda.synchronize()
+    assert exact.cpu().tolist() == [[[0x21, -254, -1, -1]]]
 
 
 def test_pack_and_rebuild_bit_exact(plan, dev):
