@@ -61,7 +61,9 @@ def executed_flops(ps, D=128):
 
 
 def _host_cpu():
-    """(CPU model string, BLAS threads numpy uses) of this host."""
+    """(CPU model string, os.cpu_count(), threads the CPU baseline uses). The threads are the host's CPU share for
+    this job: OMP_NUM_THREADS when set (the GPU boxes set it to their per-GPU share, 16, whatever os.cpu_count()
+    reports for the whole machine), else os.cpu_count()."""
     model = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
@@ -71,20 +73,33 @@ def _host_cpu():
                     break
     except OSError:
         pass
-    threads = None
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max((i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"), default=None)
-    except Exception:
-        pass
-    return model, threads or 1
+    count = os.cpu_count() or 1
+    threads = int(os.environ.get("OMP_NUM_THREADS") or count)
+    return model, count, max(1, min(threads, count))
+
+
+def _timed_median(fn, runs=3):
+    """Median wall time of `runs` calls of fn (after the caller's warm-up)."""
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def _cpu_threads(n):
+    """Context that runs numpy's BLAS and torch's CPU ops on n threads."""
+    from threadpoolctl import threadpool_limits
+    torch.set_num_threads(n)
+    return threadpool_limits(limits=n)
 
 
 def cpu_baseline(q, k, v, attn, seconds):
     """The numpy oracle's fixed-offset sparse step on a bounded sample of (tile, head) pairs (head 0, first tiles),
-    timed on this host; returned as TFLOP/s on executed blocks, like `value`."""
+    timed on this host with its CPU share of BLAS threads (median of 3 runs of about seconds / 3 each); returned
+    as TFLOP/s on executed blocks, like `value`."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    import numpy as np
     from oracle import echosparse_ref as ref
     ps, buf = attn._plan_scratch, attn._buffers
     st = attn._states[1]
@@ -98,21 +113,27 @@ def cpu_baseline(q, k, v, attn, seconds):
                 log_counts=f(buf.reps.log_counts[h:h + 1]))
     counts, blocks = ps.counts[:, h:h + 1].cpu().numpy(), ps.blocks[:, h:h + 1].cpu().numpy()
     offset = f(st.offset(0)[:, h:h + 1])
-    tiles, t0, elapsed = 1, time.perf_counter(), 0.0
-    ref.fixed_offset_attention(qs, ks, vs, counts, blocks, offset, comp=comp, tiles=1)      # warm-up
-    while True:
-        t0 = time.perf_counter()
-        ref.fixed_offset_attention(qs, ks, vs, counts, blocks, offset, comp=comp, tiles=tiles)
-        elapsed = time.perf_counter() - t0
-        if elapsed >= seconds or tiles >= counts.shape[0]:
-            break
-        tiles = min(counts.shape[0], max(tiles + 1, int(tiles * seconds / max(elapsed, 1e-3) * 1.05)))
+    model, count, threads = _host_cpu()
+    per_run = seconds / 3.0
+    with _cpu_threads(threads):
+        run = lambda n: ref.fixed_offset_attention(qs, ks, vs, counts, blocks, offset, comp=comp, tiles=n)
+        run(1)                                                                              # warm-up
+        tiles = 1
+        while True:                                  # size the sample so that one run takes about seconds / 3
+            t0 = time.perf_counter()
+            run(tiles)
+            elapsed = time.perf_counter() - t0
+            if elapsed >= per_run or tiles >= counts.shape[0]:
+                break
+            tiles = min(counts.shape[0], max(tiles + 1, int(tiles * per_run / max(elapsed, 1e-3) * 1.05)))
+        elapsed = _timed_median(lambda: run(tiles))
     cols = (64 * counts[:tiles].sum() + comp["mean_counts"][:tiles].sum() + 4 * comp["refine_counts"][:tiles].sum())
     flops = 4 * 128 * 128 * float(cols)
-    model, threads = _host_cpu()
     return {"value": flops / elapsed / 1e12, "unit": "TFLOP/s (executed blocks)", "cores": threads,
-            "cpu_model": model, "kind": "port", "sample": f"numpy oracle fixed-offset sparse step (exact + mean + representative "
-            f"columns), head 0, query tiles 0..{tiles - 1} of {counts.shape[0]}, one branch; {elapsed:.1f} s",
+            "os_cpu_count": count, "cpu_model": model, "kind": "port",
+            "sample": f"numpy oracle fixed-offset sparse step (exact + mean + representative columns), head 0, query "
+                      f"tiles 0..{tiles - 1} of {counts.shape[0]}, one branch; median of 3 runs, {elapsed:.1f} s "
+                      f"each, {threads} BLAS threads",
             "ms_per_layer_extrapolated": elapsed / tiles * counts.shape[0] * q.shape[1] * 2 * 1e3}
 
 
@@ -268,7 +289,8 @@ def _events(fn, steps):
 
 
 def _vsa_cpu_baseline(q, k, v, blk, sel, seconds):
-    """The blockwise numpy port of the fine forward (oracle) on query blocks of head 0 until `seconds` pass."""
+    """The blockwise numpy port of the fine forward (oracle) on the first query blocks of head 0, sized so one run
+    takes about seconds / 3; median of 3 runs on the host's CPU share of BLAS threads."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import vsa_ref as ref
     f = lambda x: x[0].float().cpu().numpy()
@@ -276,17 +298,22 @@ def _vsa_cpu_baseline(q, k, v, blk, sel, seconds):
     cnt = blk.cpu().numpy()
     ptr, idx = sel.q2k_ptr.cpu().numpy(), sel.q2k_idx.cpu().numpy()
     nb = cnt.size
-    done, cols, t0 = 0, 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds and done < nb:
-        ref.fine_attention_blocks(qn, kn, vn, cnt, ptr, idx, 0, [done])
-        cols += int(ptr[0, 0, done + 1] - ptr[0, 0, done])
-        done += 1
-    el = time.perf_counter() - t0
+    model, count, threads = _host_cpu()
+    with _cpu_threads(threads):
+        run = lambda n: ref.fine_attention_blocks(qn, kn, vn, cnt, ptr, idx, 0, list(range(n)))
+        run(1)
+        done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds / 3.0 and done < nb:
+            ref.fine_attention_blocks(qn, kn, vn, cnt, ptr, idx, 0, [done])
+            done += 1
+        el = _timed_median(lambda: run(done))
+    cols = int(ptr[0, 0, done] - ptr[0, 0, 0])
     flops = 4.0 * 64 * 64 * q.shape[-1] * cols
     return {"value": round(flops / el / 1e12, 5), "unit": "TFLOP/s (fine forward, executed blocks)",
-            "cores": _host_cpu()[1], "cpu_model": _host_cpu()[0], "kind": "port",
+            "cores": threads, "os_cpu_count": count, "cpu_model": model, "kind": "port",
             "sample": f"blockwise numpy port of the fine forward (oracle/vsa_ref.py fine_attention_blocks), head 0, "
-                      f"query blocks 0..{done - 1} of {nb}, {cols} block pairs, {el:.1f} s, numpy's BLAS threads"}
+                      f"query blocks 0..{done - 1} of {nb}, {cols} block pairs; median of 3 runs, {el:.1f} s each, "
+                      f"{threads} BLAS threads"}
 
 
 def run_vsa_workload(args):

@@ -135,7 +135,9 @@ def fixed_offset_attention(q, k, v, counts, blocks, offset, threshold=60.0, comp
             with np.errstate(divide="ignore", invalid="ignore"):
                 lg = np.log2(total)
                 out[r0:r1, h] = acc / total[:, None]
-            lse[r0:r1, h] = prior + lg
+            # a row whose offset is the 1e30 "no row" marker (rows past a tile's valid rows) keeps it, as the
+            # kernel keeps 1e30 for rows >= L
+            lse[r0:r1, h] = np.where(prior >= 1e30, 1e30, prior + np.where(prior >= 1e30, 0.0, lg))
             lse[r1:t * BM + BM, h] = 1e30
             bad = ~((lg >= -threshold) & (lg <= threshold))
             flags[t, h] = int(bad.any())

@@ -31,6 +31,9 @@ Functions and what pins each one (tests/test_cpu_vsa_oracle.py):
                            clusters retire; centroids equal scikit-learn's Lloyd k-means started from the same seed
                            tokens for the same number of rounds
   row_tiers                exact per-row counts, A inside A|B, brute-force order with ties and -0 / +0
+  rep_fine_head            blockwise analytic forward / backward of one head: equals rep_fine_torch and its
+                           autograd gradients (contiguous and k-means groups, empty groups, empty rows)
+  rep_kv_block_grads       one kv block's dK / dV from the backward's inputs: equals rep_fine_head's rows
 """
 import math
 
@@ -398,6 +401,161 @@ def fine_attention_blocks(q, k, v, blk_cnt, ptr, idx, bh, qblocks):
         outs.append(np.where(live[:, None], o / np.where(live, l, 1)[:, None], 0))
         lses.append(np.where(live, m + np.log(np.where(live, l, 1)), -np.inf))
     return np.stack(outs), np.stack(lses)
+
+
+def rep_fine_head(q, k, v, blk_cnt, mask_a, mask_ab, RM, tables, groups, dout, o_delta=None):
+    """Blockwise float64 three-tier attention of ONE head with analytic gradients, for the sizes where
+    rep_fine_torch's [L, L + NB * RM + NB] graph does not fit: per query block one softmax over its tier-A tokens,
+    its tier-B table rows with at least one member (+ ln of the member count) and its tier-C block means (+ ln of the
+    block count) (reference experiments/vsa2_representative/vsa2_rep/reference.py:53-96). q, k, v, dout [L, D];
+    masks [NB, NB]; tables = (k_mid, v_mid [NB * RM, D], k_tail, v_tail [NB, D]) as given values; groups [L] = the
+    table row of each token (-1 on padding). delta = rowsum(dO * o_delta) (the stored O the backward consumes;
+    this function's own O when None). Table gradients reach the tokens as the adjoint of a mean: row gradient /
+    member count to each member, block-mean gradient / count to each valid token. Returns dict(o, lse, dq, dk, dv)
+    and, for element bounds, the same products over absolute values (dq_abs, dk_abs, dv_abs: |dS| |K|, |dS|^T |Q|,
+    P^T |dO| pushed through the same adjoints). Pinned against rep_fine_torch's autograd
+    (tests/test_cpu_vsa_oracle.py)."""
+    q, k, v, dout = (np.asarray(x, np.float64) for x in (q, k, v, dout))
+    L, D = q.shape
+    NB = L // BLOCK
+    cnt = np.asarray(blk_cnt, np.int64)
+    k_mid, v_mid, k_tail, v_tail = (np.asarray(t, np.float64) for t in tables)
+    grp = np.asarray(groups, np.int64)
+    ng = np.bincount(grp[grp >= 0], minlength=NB * RM)
+    ma, mab = np.asarray(mask_a, bool), np.asarray(mask_ab, bool)
+    sc = 1.0 / math.sqrt(D)
+    o = np.zeros((L, D))
+    lse = np.full(L, -np.inf)
+    dq, dq_abs = np.zeros((L, D)), np.zeros((L, D))
+    # gradients of every column source: tokens, table rows, block means (and their absolute-value twins)
+    gk = [np.zeros((L, D)), np.zeros((NB * RM, D)), np.zeros((NB, D))]
+    gv = [np.zeros_like(x) for x in gk]
+    gk_abs = [np.zeros_like(x) for x in gk]
+    gv_abs = [np.zeros_like(x) for x in gk]
+    with np.errstate(divide="ignore"):
+        ln_ng, ln_cnt = np.log(ng.astype(np.float64)), np.log(cnt.astype(np.float64))
+    for i in range(NB):
+        n = int(cnt[i])
+        ja = np.nonzero(ma[i])[0]
+        jb = np.nonzero(mab[i] & ~ma[i])[0]
+        jc = np.nonzero(~mab[i])[0]
+        tok = (np.concatenate([j * BLOCK + np.arange(cnt[j]) for j in ja]) if ja.size else np.zeros(0, np.int64))
+        rows = (jb[:, None] * RM + np.arange(RM)[None, :]).reshape(-1)
+        rows = rows[ng[rows] > 0]
+        parts = ((0, tok), (1, rows), (2, jc))
+        kc = np.concatenate([k[tok], k_mid[rows], k_tail[jc]])
+        vc = np.concatenate([v[tok], v_mid[rows], v_tail[jc]])
+        if n == 0 or kc.shape[0] == 0:
+            continue
+        bias = np.concatenate([np.zeros(tok.size), ln_ng[rows], ln_cnt[jc]])
+        r = slice(i * BLOCK, i * BLOCK + n)
+        s = q[r] @ kc.T * sc + bias[None, :]
+        m = s.max(1, keepdims=True)
+        lz = np.log(np.exp(s - m).sum(1, keepdims=True)) + m
+        p = np.exp(s - lz)
+        o[r] = p @ vc
+        lse[r] = lz[:, 0]
+        do = dout[r]
+        delta = (do * (o[r] if o_delta is None else np.asarray(o_delta[r], np.float64))).sum(1, keepdims=True)
+        ds = p * (do @ vc.T - delta)
+        dq[r] = ds @ kc * sc
+        dq_abs[r] = np.abs(ds) @ np.abs(kc) * sc
+        dkc, dvc = ds.T @ q[r] * sc, p.T @ do
+        dkc_abs, dvc_abs = np.abs(ds).T @ np.abs(q[r]) * sc, p.T @ np.abs(do)
+        off = 0
+        for src, idx in parts:
+            sl = slice(off, off + idx.size)
+            gk[src][idx] += dkc[sl]
+            gv[src][idx] += dvc[sl]
+            gk_abs[src][idx] += dkc_abs[sl]
+            gv_abs[src][idx] += dvc_abs[sl]
+            off += idx.size
+
+    valid = grp >= 0
+    blk = np.arange(L) // BLOCK
+    g_ = np.where(valid, grp, 0)
+
+    def tokens(acc):
+        t, mid, tail = acc
+        out = t.copy()
+        out += np.where(valid[:, None], mid[g_] / np.maximum(ng[g_], 1)[:, None], 0)
+        out += np.where(valid[:, None], tail[blk] / np.maximum(cnt[blk], 1)[:, None], 0)
+        return out
+
+    return dict(o=o, lse=lse, dq=dq, dk=tokens(gk), dv=tokens(gv), dq_abs=dq_abs, dk_abs=tokens(gk_abs),
+                dv_abs=tokens(gv_abs))
+
+
+def rep_kv_block_grads(q, k, v, dout, lse, delta, blk_cnt, mask_a, mask_ab, j, RM, tables, groups):
+    """dK, dV [64, D] of the tokens of kv block j of ONE head in the three-tier attention, as a function of the
+    backward's inputs: the forward's natural-log LSE [L] and delta = rowsum(dO * O) [L] of every query row (the
+    values the backward kernels consume). Each query block i contributes through the one tier that holds j in row
+    i: its tokens (tier A), its table rows with members (tier B, + ln of the member count, the row gradient shared
+    by the members / count) or its block mean (tier C, + ln of the count, shared / count). Only the columns of
+    block j are formed, so a full-size head costs O(L) products. Also returns the absolute-value products (|dS|^T
+    |Q|, P^T |dO|) through the same adjoints, for element bounds. Pinned against rep_fine_head
+    (tests/test_cpu_vsa_oracle.py)."""
+    q, k, v, dout = (np.asarray(x, np.float64) for x in (q, k, v, dout))
+    lse, delta = np.asarray(lse, np.float64), np.asarray(delta, np.float64)
+    L, D = q.shape
+    NB = L // BLOCK
+    cnt = np.asarray(blk_cnt, np.int64)
+    k_mid, v_mid, k_tail, v_tail = (np.asarray(t, np.float64) for t in tables)
+    grp = np.asarray(groups, np.int64)
+    ng = np.bincount(grp[grp >= 0], minlength=NB * RM)
+    ma, mab = np.asarray(mask_a, bool), np.asarray(mask_ab, bool)
+    sc = 1.0 / math.sqrt(D)
+    n = int(cnt[j])
+    tok = j * BLOCK + np.arange(n)
+    rows_j = j * RM + np.arange(RM)
+    rows_j = rows_j[ng[rows_j] > 0]
+    dk, dv = np.zeros((BLOCK, D)), np.zeros((BLOCK, D))
+    dk_abs, dv_abs = np.zeros((BLOCK, D)), np.zeros((BLOCK, D))
+
+    def query_rows(which):
+        qb = np.nonzero(which)[0]
+        if qb.size == 0:
+            return np.zeros(0, np.int64)
+        return np.concatenate([i * BLOCK + np.arange(cnt[i]) for i in qb])
+
+    def block(r, kc, vc, bias):
+        s = q[r] @ kc.T * sc + bias[None, :]
+        p = np.exp(s - lse[r][:, None])
+        ds = p * (dout[r] @ vc.T - delta[r][:, None])
+        return ds.T @ q[r] * sc, p.T @ dout[r], np.abs(ds).T @ np.abs(q[r]) * sc, p.T @ np.abs(dout[r])
+
+    with np.errstate(divide="ignore"):
+        # tier A: the block's tokens are columns of their own
+        r = query_rows(ma[:, j])
+        if r.size and n:
+            a, b, c, d = block(r, k[tok], v[tok], np.zeros(n))
+            dk[:n] += a
+            dv[:n] += b
+            dk_abs[:n] += c
+            dv_abs[:n] += d
+        # tier B: the table rows of block j, shared by their members
+        r = query_rows(mab[:, j] & ~ma[:, j])
+        if r.size and rows_j.size:
+            a, b, c, d = block(r, k_mid[rows_j], v_mid[rows_j], np.log(ng[rows_j].astype(np.float64)))
+            for x, y in ((dk, a), (dv, b), (dk_abs, c), (dv_abs, d)):
+                for ri, row in enumerate(rows_j):
+                    members = np.nonzero(grp[tok] == row)[0]
+                    x[members] += y[ri] / ng[row]
+        # tier C: the block mean, shared by every valid token
+        r = query_rows(~mab[:, j])
+        if r.size and n:
+            a, b, c, d = block(r, k_tail[j:j + 1], v_tail[j:j + 1], np.log(np.array([float(n)])))
+            for x, y in ((dk, a), (dv, b), (dk_abs, c), (dv_abs, d)):
+                x[:n] += y[0] / n
+    return dict(dk=dk, dv=dv, dk_abs=dk_abs, dv_abs=dv_abs)
+
+
+def contiguous_groups(blk_cnt, RM):
+    """Table row of every token for the contiguous groups of 64 / RM tokens (-1 on padding)."""
+    cnt = np.asarray(blk_cnt, np.int64)
+    L = cnt.size * BLOCK
+    t = np.arange(L)
+    return np.where(token_valid(cnt, L), (t // BLOCK) * RM + (t % BLOCK) // (BLOCK // RM), -1)
 
 
 # --------------------------------------------------------------------- seeded k-means representative tables

@@ -349,6 +349,87 @@ def test_rep_constant_groups_equal_dense_attention():
     assert np.allclose(o.numpy(), wo, atol=1e-12)
 
 
+@pytest.mark.parametrize("kmeans", [False, True])
+def test_rep_fine_head_equals_the_autograd_graph(kmeans):
+    """The blockwise analytic three-tier forward / backward of one head equals rep_fine_torch and its autograd
+    gradients: partial blocks (one with a single token, so groups are empty), a row with no tier-A block, a row
+    with no tier-C block, contiguous and k-means groups, a given stored O for delta."""
+    cnt = [64, 64, 37, 64, 1, 64, 20, 50]
+    NB, RM, D = len(cnt), 4, 16
+    L = NB * 64
+    g = torch.Generator().manual_seed(7)
+    valid = torch.as_tensor(ref.token_valid(cnt, L))[None, None, :, None].double()
+    q, k, v, do = (torch.randn(1, 1, L, D, generator=g, dtype=torch.float64) * valid for _ in range(4))
+    rng = np.random.default_rng(8)
+    a = rng.random((1, 1, NB, NB)) < 0.2
+    ab = a | (rng.random((1, 1, NB, NB)) < 0.35)
+    a[:, :, 3] = False
+    ab[:, :, 5] = True
+    if kmeans:
+        km, vm, _, _, lab = ref.kmeans_tables(k.numpy(), v.numpy(), cnt, RM, 5, 3)
+        groups = np.where(lab[0, 0] >= 0, (np.arange(L) // 64) * RM + lab[0, 0], -1)
+    else:
+        km, vm, _, _, _, _ = ref.rep_tables(k.numpy(), v.numpy(), cnt, RM, rnd=lambda x: x)
+        lab, groups = None, ref.contiguous_groups(cnt, RM)
+    _, _, kt, vt, _, _ = ref.rep_tables(k.numpy(), v.numpy(), cnt, RM, rnd=lambda x: x)
+    tables = (km, vm, kt, vt)
+    x = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    wo, wl = ref.rep_fine_torch(*x, cnt, a, ab, RM, tables=tables, labels=lab)
+    wg = torch.autograd.grad(wo, x, do)
+    got = ref.rep_fine_head(q[0, 0].numpy(), k[0, 0].numpy(), v[0, 0].numpy(), cnt, a[0, 0], ab[0, 0], RM,
+                            [t[0, 0] for t in tables], groups, do[0, 0].numpy())
+    assert np.allclose(got["o"], wo.detach().numpy()[0, 0], atol=1e-12)
+    fin = np.isfinite(wl.detach().numpy()[0, 0])
+    assert np.array_equal(np.isfinite(got["lse"]), fin)
+    assert np.allclose(got["lse"][fin], wl.detach().numpy()[0, 0][fin], atol=1e-12)
+    for name, w in zip(("dq", "dk", "dv"), wg):
+        assert np.allclose(got[name], w.numpy()[0, 0], atol=1e-10), name
+        assert (got[name + "_abs"] >= np.abs(got[name]) - 1e-12).all(), name
+    # delta from a stored O that differs by eps: delta grows by shift = eps * rowsum(dO), and the gradients are
+    # those of sum(O * dO) - sum(shift * lse), since d lse / d s = P
+    x2 = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    wo2, wl2 = ref.rep_fine_torch(*x2, cnt, a, ab, RM, tables=tables, labels=lab)
+    shift = torch.as_tensor((do[0, 0].numpy() * 1e-3).sum(1))
+    lse_fin = torch.where(torch.as_tensor(fin), wl2[0, 0], torch.zeros_like(wl2[0, 0]))
+    wg2 = torch.autograd.grad((wo2 * do).sum() - (shift * lse_fin).sum(), x2)
+    got2 = ref.rep_fine_head(q[0, 0].numpy(), k[0, 0].numpy(), v[0, 0].numpy(), cnt, a[0, 0], ab[0, 0], RM,
+                             [t[0, 0] for t in tables], groups, do[0, 0].numpy(),
+                             o_delta=wo.detach().numpy()[0, 0] + 1e-3)
+    for name, w in zip(("dq", "dk", "dv"), wg2):
+        assert np.allclose(got2[name], w.numpy()[0, 0], atol=1e-10), name
+    assert np.abs(got2["dq"] - got["dq"]).max() > 1e-6
+
+
+@pytest.mark.parametrize("kmeans", [False, True])
+def test_rep_kv_block_grads_equal_the_head_gradients(kmeans):
+    """The per-kv-block gradients from the backward's inputs (LSE, delta) equal the whole-head computation's rows,
+    for every block (full, partial, single-token with empty groups)."""
+    cnt = [64, 64, 37, 64, 1, 64, 20, 50]
+    NB, RM, D = len(cnt), 4, 16
+    L = NB * 64
+    rng = np.random.default_rng(11)
+    valid = ref.token_valid(cnt, L)[:, None]
+    q, k, v, do = (rng.standard_normal((L, D)) * valid for _ in range(4))
+    a = rng.random((NB, NB)) < 0.2
+    ab = a | (rng.random((NB, NB)) < 0.35)
+    a[3] = False
+    ab[5] = True
+    if kmeans:
+        km, vm, _, _, lab = ref.kmeans_tables(k[None, None], v[None, None], cnt, RM, 5, 3)
+        groups = np.where(lab[0, 0] >= 0, (np.arange(L) // 64) * RM + lab[0, 0], -1)
+    else:
+        km, vm, _, _, _, _ = ref.rep_tables(k[None, None], v[None, None], cnt, RM, rnd=lambda x: x)
+        groups = ref.contiguous_groups(cnt, RM)
+    _, _, kt, vt, _, _ = ref.rep_tables(k[None, None], v[None, None], cnt, RM, rnd=lambda x: x)
+    tables = [t[0, 0] for t in (km, vm, kt, vt)]
+    head = ref.rep_fine_head(q, k, v, cnt, a, ab, RM, tables, groups, do)
+    delta = (do * head["o"]).sum(1)
+    for j in range(NB):
+        got = ref.rep_kv_block_grads(q, k, v, do, head["lse"], delta, cnt, a, ab, j, RM, tables, groups)
+        for name in ("dk", "dv", "dk_abs", "dv_abs"):
+            assert np.allclose(got[name], head[name][j * 64:(j + 1) * 64], atol=1e-10), (name, j)
+
+
 def test_rep_tables_counts():
     cnt = [64, 20, 1]
     x = np.random.default_rng(4).standard_normal((1, 1, 192, 8)).astype(np.float32)

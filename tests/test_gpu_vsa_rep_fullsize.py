@@ -7,7 +7,9 @@ restatement of one softmax over the block's tier-A tokens, tier-B representative
 tier-C block means (+ ln of the block count; dQ with delta = rowsum(dO * O) of the stored bf16 O, the quantity the
 backward consumes), with the kernels' own bf16 tables (`vsa_rep_build`, bit-exact at
 small sizes) and tier bitmaps; max-abs 2e-2 / rel-L2 1e-2 (dQ: rel-L2 1e-2 and an element
-bound from the conditioning of the bf16 dS sum, see below)."""
+bound from the conditioning of the bf16 dS sum, see below). dK / dV of the sampled blocks' tokens, over every query
+block of the head (oracle/vsa_ref.py::rep_kv_block_grads from the stored LSE and delta), under the same kind of
+bound."""
 import math
 import sys
 
@@ -16,6 +18,7 @@ import pytest
 import torch
 
 from helpers import check_close, f32
+from oracle import vsa_ref
 
 pytestmark = pytest.mark.gpu
 
@@ -51,12 +54,13 @@ def test_three_tiers_full_c4_shape(dev, construction):
                          tables="kmeans" if kmeans else "contiguous", kmeans_iters=5, seed=4)
     sel = rep.route_tiers(q, k, blk, tiers, R=16)
     log("C4 full shape:", construction, "kernels")
-    qg = q.detach().clone().requires_grad_(True)
-    o, lse = rep.rep_fine_attention(qg, k, v, blk, sel, mid_reps=RM, tables=tiers.tables, kmeans_iters=5, seed=4)
-    (dq,) = torch.autograd.grad(o, (qg,), dout)
+    qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    o, lse = rep.rep_fine_attention(qg, kg, vg, blk, sel, mid_reps=RM, tables=tiers.tables, kmeans_iters=5, seed=4)
+    dq, dk, dv = torch.autograd.grad(o, (qg, kg, vg), dout)
+    del qg, kg, vg
     cnt = blk.cpu().numpy().astype(np.int64)
     if kmeans:
-        (k_mid, v_mid, _, k_tail, v_tail, _), counts, _ = _C.rep_build_kmeans(k, v, blk, RM, 5, 4)
+        (k_mid, v_mid, _, k_tail, v_tail, _), counts, labels = _C.rep_build_kmeans(k, v, blk, RM, 5, 4)
         ng_all = counts.cpu().numpy().reshape(B, H, NB, RM)                 # cluster sizes per (b, h)
     else:
         k_mid, v_mid, _, k_tail, v_tail, _ = _C.rep_build(k, v, blk, RM)
@@ -73,7 +77,6 @@ def test_three_tiers_full_c4_shape(dev, construction):
         log("C4 full shape: oracle batch", b, "head", h, "block", i)
         ng = ng_all[b, h]
         if kmeans:   # the sampled block's k-means table rows against the oracle (same seed, same (b, h, block))
-            from oracle import vsa_ref
             sl = slice(i * 64, i * 64 + 64)
             wk, wv, _, wc, _ = vsa_ref.kmeans_tables(f32(k[b, h, sl])[None, None], f32(v[b, h, sl])[None, None],
                                                      [int(cnt[i])], RM, 5, 4, bh0=b * H + h, blk0=i)
@@ -113,3 +116,26 @@ def test_three_tiers_full_c4_shape(dev, construction):
         assert (err <= bound).all(), f"dQ b{b} h{h} blk{i}: worst err / bound {float((err / bound).max()):.3g}"
         if int(cnt[i]) < 64:
             assert (go[b, h, i * 64 + int(cnt[i]):(i + 1) * 64] == 0).all()
+        # dK / dV of kv block i of this head (its tokens, and through the adjoints its tier-B table rows and its
+        # block mean), over every query block of the head, from the backward's inputs: the stored LSE and
+        # delta = rowsum(dO * O) of the bf16 O; same element bound with |dS|^T |Q| and P^T |dO|
+        if kmeans:
+            lab = labels[b, h].cpu().numpy().astype(np.int64)
+            groups = np.where(lab < RM, (np.arange(NB * 64) // 64) * RM + lab, -1)
+        else:
+            groups = vsa_ref.contiguous_groups(cnt, RM)
+        dlt_all = (dout[b, h].double().cpu().numpy() * go[b, h]).sum(1)
+        wkv = vsa_ref.rep_kv_block_grads(q[b, h].float().cpu().numpy(), k[b, h].float().cpu().numpy(),
+                                         v[b, h].float().cpu().numpy(), dout[b, h].float().cpu().numpy(),
+                                         np.where(np.isfinite(gl[b, h]), gl[b, h], 0.0), dlt_all, cnt, ma[b, h],
+                                         ma[b, h] | mb[b, h], i, RM, (kmid[:NB * RM], vmid[:NB * RM], ktail[:NB],
+                                                                     vtail[:NB]), groups)
+        n = int(cnt[i])
+        for name, got, key in (("dK", dk, "dk"), ("dV", dv, "dv")):
+            g_ = f32(got[b, h, i * 64:i * 64 + n])
+            w_ = wkv[key][:n]
+            bound = np.maximum(2e-2, 2.0 ** -8 * (wkv[key + "_abs"][:n] + np.abs(w_)))
+            err = np.abs(g_ - w_)
+            log(f"C4 {name} b{b} h{h} blk{i}: max-abs {err.max():.3g}")
+            assert (err <= bound).all(), f"{name} b{b} h{h} blk{i}: worst err / bound {float((err / bound).max()):.3g}"
+            check_close(f"{name} b{b} h{h} blk{i}", g_, w_, max_abs=np.inf)
