@@ -9,8 +9,9 @@ the ABI:
   * int / unsigned / size_t / long long become int, float / double become float; an int that does not fit the C
     type is refused (no silent wrap)
   * every tensor must be contiguous (a strided view would hand the kernel the wrong rows) and of the dtype its C
-    type names: float* float32, int* / unsigned* int32 (or uint32), uint8_t* uint8 (or bool), void* bf16 or
-    float16 (the token tensors), except a void* named workspace, which takes any dtype
+    type names: float* float32, int* / unsigned* int32 (or uint32), uint8_t* uint8 (or bool), const void* bf16
+    or float16 (the token tensors), void* also float32 (outputs some entry points write in fp32 on request), and
+    a void* named workspace any dtype
   * every operator returns nothing, like the C functions; a failing status raises RuntimeError with
     es_last_error_string(), a host tensor is refused before any launch
   * implementations for the CUDA (HIP) dispatch key, CPU (which only refuses host tensors) and Meta (no work, for
@@ -70,10 +71,13 @@ def _kind(ctype):
 
 
 def _dtype_kind(ctype, pname):
-    """The dtype check of a pointer parameter: ES_F32, ES_I32, ES_U8, ES_HALF or ES_ANY."""
+    """The dtype check of a pointer parameter: ES_F32, ES_I32, ES_U8, ES_HALF, ES_OUT or ES_ANY."""
     base = ctype.replace("const", "").replace("*", "").strip()
     if base == "void":
-        return "ES_ANY" if pname == "workspace" else "ES_HALF"
+        if pname == "workspace":
+            return "ES_ANY"
+        # a written token tensor may be an fp32 output (out_fp32 / accumulate variants)
+        return "ES_HALF" if ctype.startswith("const") else "ES_OUT"
     return {"float": "ES_F32", "int": "ES_I32", "unsigned": "ES_I32", "uint8_t": "ES_U8"}[base]
 
 
@@ -143,7 +147,7 @@ def source():
         "  }",
         "};",
         "",
-        "enum EsDtype { ES_F32, ES_I32, ES_U8, ES_HALF, ES_ANY };",
+        "enum EsDtype { ES_F32, ES_I32, ES_U8, ES_HALF, ES_OUT, ES_ANY };",
         "",
         "// the pointer of an optional tensor argument after checking its layout and its dtype against the C type",
         "inline void* es_op_data(const char* name, const char* arg, const c10::optional<at::Tensor>& t, EsDtype kind) {",
@@ -158,6 +162,10 @@ def source():
         "    case ES_I32: ok = s == at::kInt || s == at::kUInt32; want = \"int32\"; break;",
         "    case ES_U8: ok = s == at::kByte || s == at::kBool; want = \"uint8\"; break;",
         "    case ES_HALF: ok = s == at::kBFloat16 || s == at::kHalf; want = \"bfloat16 or float16\"; break;",
+        "    case ES_OUT:",
+        "      ok = s == at::kBFloat16 || s == at::kHalf || s == at::kFloat;",
+        "      want = \"bfloat16, float16 or float32\";",
+        "      break;",
         "    case ES_ANY: break;",
         "  }",
         "  TORCH_CHECK(ok, name, \": argument \", arg, \" must be \", want, \" (got \", s, \")\");",
