@@ -67,6 +67,17 @@ __device__ __forceinline__ void g2lds16(const void* gsrc, char* lds_base) {
 // The same global -> LDS transfer written as inline assembly: the compiler does not see these LDS writes, so it
 // adds no conservative vmcnt waits before LDS reads of the other buffer (it would otherwise drain the prefetch).
 // Visibility is the caller's job: dma_wait() then a barrier before any wave reads what was transferred.
+//
+// Wait states. The hardware does not interlock two producers of these transfers' operands (CDNA3 / CDNA4 ISA,
+// "manually inserted wait states"): an SALU write of M0 needs 1 wait state before an LDS-DMA instruction reads M0,
+// and a VALU write of an SGPR (v_readfirstlane, which uni() compiles to) needs 5 before a vector memory
+// instruction reads that SGPR (here the buffer resource and the scalar offset). The compiler's hazard recognizer
+// inserts them for its own instructions but treats inline assembly as opaque, and its scheduler is free to put
+// `s_mov_b32 m0, ...` or the v_readfirstlane of the resource right in front of the asm (the default build did
+// both: 80 transfers issued straight after their M0 write, 20 within 1-4 instructions of the readfirstlane of
+// their resource). The transfer then reads the previous M0 (and lands in the previous destination) or a stale
+// resource (and reads from another address, or faults). So every transfer starts with `s_nop 4`: five wait states
+// after whatever the compiler placed before it, whatever the schedule.
 typedef int srd_t __attribute__((ext_vector_type(4)));
 
 // raw buffer descriptor over `bytes` bytes from `base` (offsets past it read as zero); must be wave-uniform
@@ -97,7 +108,7 @@ __device__ __forceinline__ srd_t uni(srd_t r) {
 
 // every lane moves 16 bytes at srd + voff + soff to lds_base + 16 * lane
 __device__ __forceinline__ void dma16(srd_t r, const void* lds_base, unsigned voff, unsigned soff) {
-  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                :
                : "v"(voff), "s"(uni(r)), "s"(uni(soff)), "{m0}"(uni(lds_addr(lds_base)))
                : "memory");
@@ -105,7 +116,7 @@ __device__ __forceinline__ void dma16(srd_t r, const void* lds_base, unsigned vo
 
 // dma16 with the LDS destination given as a 32-bit LDS address (no pointer conversion)
 __device__ __forceinline__ void dma16_at(srd_t r, unsigned lds, unsigned voff, unsigned soff) {
-  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                :
                : "v"(voff), "s"(uni(r)), "s"(uni(soff)), "{m0}"(uni(lds))
                : "memory");
@@ -113,7 +124,7 @@ __device__ __forceinline__ void dma16_at(srd_t r, unsigned lds, unsigned voff, u
 
 // every lane moves 4 bytes at srd + voff + soff to lds_base + 4 * lane
 __device__ __forceinline__ void dma4(srd_t r, const void* lds_base, unsigned voff, unsigned soff) {
-  asm volatile("buffer_load_dword %0, %1, %2 offen lds"
+  asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2 offen lds"
                :
                : "v"(voff), "s"(uni(r)), "s"(uni(soff)), "{m0}"(uni(lds_addr(lds_base)))
                : "memory");
