@@ -134,10 +134,11 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
     tok_off[i] = (unsigned)R * hstride + chb[i];
   }
 
-  // wave 0 stages the list entries chunk cj needs into ids_s[cj % 3]: exact -> its block id (every lane, same
+  // wave 3 stages the list entries chunk cj needs into ids_s[cj % 4] (wave 0 writes the bias rows and wave 1 flushes
+  // the mass partials, so the per-chunk duties are spread over the waves): exact -> its block id (every lane, same
   // word); mean -> the ids of its 64 columns; rep -> the refined block of each of its 64 columns
   auto stage_ids = [&](int cj) {
-    if (MODE == COMPENSATE || wv != 0 || cj >= nc || (cj < n && g_ex == nullptr)) return;
+    if (MODE == COMPENSATE || wv != 3 || cj >= nc || (cj < n && g_ex == nullptr)) return;
     int* dst = ids_s[cj & 3];
     if (cj < n) {
       dma4(make_srd(g_ex, (unsigned)n * 4u), dst, 0, (unsigned)cj * 4u);
@@ -351,14 +352,24 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
     }
   };
 
+  // K fragments (A operands) of the chunk's first 32 keys, read into registers right after the barrier that made
+  // the chunk visible and before the next chunk's transfers are issued: the eight reads then run under the
+  // transfer issue, and the first S^T chain finds all its operands ready instead of waiting for one LDS read per
+  // MFMA (the compiler, short of registers inside the compute section, reused one register quad for them)
+  auto load_k0 = [&](int sb, bf16x8 (&kf)[8]) {
+    const char* kb = kv_s[sb][0];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) kf[ks] = lds_read16(kb, koff[ks]);
+  };
+
   // one chunk as two 32-key halves, so the matrix cores compute S^T of the second half while the VALU
   // exponentiates the first, and O^T += V^T P^T of the first half while the VALU does the second.
-  auto compute = [&](int j, int sb, auto biased_tag) {
+  auto compute = [&](int j, int sb, auto biased_tag, const bf16x8 (&kf0)[8]) {
     const char* kb = kv_s[sb][0];
     const char* vb = kv_s[sb][1];
     f32x16 s0 = {}, s1 = {};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) s0 = mfma32(lds_read16(kb, koff[ks]), qreg[ks], s0);
+    for (int ks = 0; ks < 8; ++ks) s0 = mfma32(kf0[ks], qreg[ks], s0);
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) s1 = mfma32(lds_read16(kb + 8192, koff[ks]), qreg[ks], s1);
     if (MODE != ONLINE) {
@@ -423,6 +434,8 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
     const unsigned kv_lds = uni(lds_addr(kv_s[0][0]) + (unsigned)wv * 4096u);
     for (; j + 3 < n && !(tail_block && cur_row == nb - 1); ++j) {
       const int sb = j & 1;
+      bf16x8 kf0[8];
+      load_k0(sb, kf0);
       const int next_row = listed ? __builtin_amdgcn_readfirstlane(pre_v) : j + 1;
       const int b0 = next_row * BK;
       Dma dn;
@@ -438,20 +451,20 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
 #pragma unroll
         for (int i = 0; i < 4; ++i) dma16_at(dn.rv, kd + BK * 256 + i * 1024, dn.off[i], 0u);
       }
-      if (listed && wv == 0) dma4(rex, ids_s[(j + 3) & 3], 0, (unsigned)(j + 3) * 4u);
+      if (listed && wv == 3) dma4(rex, ids_s[(j + 3) & 3], 0, (unsigned)(j + 3) * 4u);
       pre_v = listed ? ids_s[(j + 2) & 3][0] : j + 2;  // (the general loop below starts from it)
       online_biased = false;
       if (!COMP)
-        compute(j, sb, std::true_type{});
+        compute(j, sb, std::true_type{}, kf0);
       else
-        compute(j, sb, std::false_type{});
+        compute(j, sb, std::false_type{}, kf0);
       dma_wait();
       // (the compensated and online variants read the bias of an exact chunk only for the partial last block)
       if (wv == 0 && ((MODE == FIXED && !COMP) || (tail_block && next_row == nb - 1)))
         bias_s[sb ^ 1][l] = b0 + l < a.Lk ? 0.0f : -INFINITY;
       __syncthreads();
-      if (MASS && ((j & 63) == 63) && tid < 64) {
-        const int idx = (j & ~63) + tid;
+      if (MASS && ((j & 63) == 63) && wv == 1) {
+        const int idx = (j & ~63) + l;
         float m = 0.0f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) m += mass_s[r][idx & 127];
@@ -463,6 +476,8 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
   // one chunk of any kind (the general step)
   auto general_step = [&](int j) {
     const int sb = j & 1;
+    bf16x8 kf0[8];
+    load_k0(sb, kf0);
     float bnext = 0.0f;
     int next_row = 0;
     bool next_lc = false;  // the next chunk's bias comes from lc_s
@@ -482,14 +497,14 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
     const bool biased = MODE == COMPENSATE || j >= n || (tail_block && cur_row == nb - 1);
     online_biased = biased;
     if (!COMP || biased)   // (non-COMP variants: one instantiation keeps them within 256 VGPRs)
-      compute(j, sb, std::true_type{});
+      compute(j, sb, std::true_type{}, kf0);
     else
-      compute(j, sb, std::false_type{});
+      compute(j, sb, std::false_type{}, kf0);
     dma_wait();
     if (j + 1 < nc && wv == 0) bias_s[sb ^ 1][l] = next_lc ? lc_s[l] : bnext;
     __syncthreads();
-    if (MODE == FIXED && MASS && j < n && ((j & 63) == 63 || j == n - 1) && tid < 64) {
-      const int idx = (j & ~63) + tid;
+    if (MODE == FIXED && MASS && j < n && ((j & 63) == 63 || j == n - 1) && wv == 1) {
+      const int idx = (j & ~63) + l;
       if (idx <= j) {
         float m = 0.0f;
 #pragma unroll
@@ -501,6 +516,38 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
     cur_row = next_row;
     };
   if (MODE == FIXED && COMP) {
+    for (; j < nc && j < n; ++j) general_step(j);
+    // the block-mean stretch (chunk j and chunk j + 1 both mean columns): the same steps with the kind known
+    {
+      const unsigned kv_lds = uni(lds_addr(kv_s[0][0]) + (unsigned)wv * 4096u);
+      for (; j + 1 < n + cm; ++j) {
+        const int sb = j & 1;
+        bf16x8 kf0[8];
+        load_k0(sb, kf0);
+        const int* src = ids_s[(j + 1) & 3];
+        const int c0 = (j + 1 - n) * BK;
+        unsigned off[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int col = c0 + rbase + 4 * i;
+          off[i] = col < nm ? (unsigned)src[rbase + 4 * i] * hstride + chb[i] : 0x80000000u;
+        }
+        int brow = -1;
+        if (wv == 0) brow = c0 + l < nm ? src[l] : -1;
+        {
+          const unsigned kd = kv_lds + (unsigned)(sb ^ 1) * (2u * BK * 256u);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dma16_at(rkm, kd + i * 1024, off[i], 0u);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dma16_at(rvm, kd + BK * 256 + i * 1024, off[i], 0u);
+        }
+        stage_ids(j + 3);
+        compute(j, sb, std::true_type{}, kf0);
+        dma_wait();
+        if (wv == 0) bias_s[sb ^ 1][l] = brow < 0 ? -INFINITY : brow == nb - 1 ? a.tail_log2 : 6.0f;
+        __syncthreads();
+      }
+    }
     for (; j < nc && !(j >= n + cm && j + 3 < nc); ++j) general_step(j);
     // the representative stretch (chunks j .. j + 3 all representative columns): the same steps with the kind known
     const srd_t rlc = make_srd(a.log_counts + (size_t)h * nb4, (unsigned)nb4 * 4u);
@@ -508,6 +555,8 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
     const unsigned kv_lds = uni(lds_addr(kv_s[0][0]) + (unsigned)wv * 4096u);
     for (; j + 3 < nc; ++j) {
       const int sb = j & 1;
+      bf16x8 kf0[8];
+      load_k0(sb, kf0);
       const int* src = ids_s[(j + 1) & 3];
       const int c0 = (j + 1 - n - cm) * BK;
       unsigned off[4];
@@ -528,8 +577,8 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, const int h, const 
 #pragma unroll
         for (int i = 0; i < 4; ++i) dma16_at(rvr, kd + BK * 256 + i * 1024, off[i], 0u);
       }
-      if (wv == 0) dma4(rrf, ids_s[(j + 3) & 3], (unsigned)((((j + 3 - n - cm) * BK + l) >> 2) * 4), 0u);
-      compute(j, sb, std::true_type{});
+      if (wv == 3) dma4(rrf, ids_s[(j + 3) & 3], (unsigned)((((j + 3 - n - cm) * BK + l) >> 2) * 4), 0u);
+      compute(j, sb, std::true_type{}, kf0);
       dma_wait();
       if (wv == 0) bias_s[sb ^ 1][l] = brow >= 0 ? lc_s[l] : -INFINITY;
       __syncthreads();
