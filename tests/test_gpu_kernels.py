@@ -340,7 +340,8 @@ def test_representatives_match_oracle(data, reps):
     assert same.mean() > 0.9
     gk = f32(R.k)[:, :4 * NB].reshape(H, NB, 4, D)[same]
     wk = rk[:, :4 * NB].reshape(H, NB, 4, D)[same]
-    check_close("rep k", gk, wk, max_abs=5e-2)
+    # blocks with the oracle's cluster sizes hold the same members: the bf16 means of the same tokens (flat bounds)
+    log("rep k max-abs / rel-L2", *check_close("rep k", gk, wk))
 
 
 def test_sparse_attention(data, plan, reps, dev):

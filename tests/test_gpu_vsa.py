@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import check_close, f32
+from helpers import bf16_max_abs, check_close, f32
 from oracle import vsa_ref as ref
 
 pytestmark = pytest.mark.gpu
@@ -258,7 +258,8 @@ def test_fine_forward_large_logits(dev):
     o, lse = C().attn_fwd(qd, kd, vd, sel.q2k_ptr, sel.q2k_idx, blk)
     wo, wl = ref.fine_attention(f32(q), f32(k), f32(v), cnt, m)
     check_close("O", f32(o), wo)
-    check_close("lse", f32(lse), wl, max_abs=5e-2, rel=1e-3)
+    # logits reach |100| here; the LSE is a float32 value of that size, within the flat 2e-2
+    log("large-logit lse max-abs / rel-L2", *check_close("lse", f32(lse), wl, rel=1e-3))
 
 
 @pytest.mark.parametrize("seed", [0, 1])
@@ -388,16 +389,19 @@ def test_fuse_forward_backward(qkv, gate_kind, act):
     check_close("O", f32(o), wo, max_abs=max(2e-2, 2.0 ** -8 * np.abs(wo).max()))
     leaves = [ofx, ocx] + ([gx] if gx is not None else [])
     grads = torch.autograd.grad(want, leaves, dout_c.double())
-    check_close("dO_c", f32(doc)[:, :, :NB], grads[1][:, :, :NB].numpy(), max_abs=0.25, rel=1e-2)
+    # dO_c is a bf16 sum over a block's rows that reaches |30|: half a bf16 step at its largest magnitude
+    wdoc = grads[1][:, :, :NB].numpy()
+    log("dO_c max-abs / rel-L2", *check_close("dO_c", f32(doc)[:, :, :NB], wdoc, max_abs=bf16_max_abs(wdoc)))
     if gx is not None:
         # dgate is stored in bf16 and the per-token sums reach |20|: one bf16 step there is 0.125, so the absolute
         # bound scales with the magnitude (half a step), the relative-L2 bound stays 1e-2
         w = grads[2].numpy()
         check_close("dgate", f32(dgate), w, max_abs=max(2e-2, 2.0 ** -8 * np.abs(w).max()))
     want_df = (dout_c.double() * valid * of_c.double()).sum(-1)
-    check_close("delta_f", f32(delta_f), want_df.numpy(), max_abs=5e-2)
+    # delta is a float32 row sum of exact bf16 products: the flat bounds apply
+    log("delta_f max-abs / rel-L2", *check_close("delta_f", f32(delta_f), want_df.numpy()))
     want_dc = (f32(doc)[:, :, :NB].astype(np.float64) * oc.double().numpy()[:, :, :NB]).sum(-1)
-    check_close("delta_c", f32(delta_c)[:, :, :NB], want_dc, max_abs=5e-2)
+    log("delta_c max-abs / rel-L2", *check_close("delta_c", f32(delta_c)[:, :, :NB], want_dc))
     assert torch.equal(dof.cpu(), (dout_c * valid.to(torch.bfloat16)))
 
 
