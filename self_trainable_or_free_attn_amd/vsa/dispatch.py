@@ -25,18 +25,26 @@ def auto_bwd_variant(B: int, H: int, L: int, D: int, gpu_major: int) -> int:
     return 2
 
 
+def _from_environment(environ):
+    """The variant named by ECHOSPARSE_VSA_BWD_VARIANT, None when unset; a value that is not an int is refused with
+    the same message as an out-of-range one."""
+    raw = environ.get(ENV_NAME)
+    if raw is None:
+        return None
+    try:
+        return int(raw)
+    except ValueError:
+        raise ValueError(f"{ENV_NAME} must be one of {BWD_VARIANTS}, got {raw!r}") from None
+
+
 def select_bwd_variant(B: int, H: int, L: int, D: int, gpu_major: int, call: Optional[int] = None,
                        override: Optional[int] = None, environ=os.environ) -> Tuple[int, str]:
-    """(variant, source): source is "call", "set_bwd_variant", "environment" or "auto"."""
-    if call is not None:
-        return check_bwd_variant(call, "bwd_variant"), "call"
-    if override is not None:
-        return check_bwd_variant(override, "set_bwd_variant"), "set_bwd_variant"
-    raw = environ.get(ENV_NAME)
-    if raw is not None:
-        try:
-            parsed = int(raw)
-        except ValueError:
-            raise ValueError(f"{ENV_NAME} must be one of {BWD_VARIANTS}, got {raw!r}") from None
-        return check_bwd_variant(parsed, ENV_NAME), "environment"
+    """(variant, source) from the first of: the per-call argument, ops.set_bwd_variant, the environment variable,
+    the automatic rule; source is "call", "set_bwd_variant", "environment" or "auto"."""
+    candidates = (("call", "bwd_variant", lambda: call), ("set_bwd_variant", "set_bwd_variant", lambda: override),
+                  ("environment", ENV_NAME, lambda: _from_environment(environ)))
+    for source, what, value in candidates:
+        v = value()
+        if v is not None:
+            return check_bwd_variant(v, what), source
     return auto_bwd_variant(B, H, L, D, gpu_major), "auto"
