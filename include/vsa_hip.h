@@ -141,7 +141,7 @@ int vsa_router_scores(const void* qr, const void* kr, const float* lse2, const i
 
 /* Exact global top-k of fp32 scores [bh_count, NB, NB]: k = min(budget, NB^2) entries per (b, h), score desc then
  * flat index asc, into the CSR of rows bh0 .. (offsets b * k), and (bits_out != NULL) the selection bitmap rows
- * bits_out [BH, NB, ceil(NB / 32)] of those (b, h). NB <= 4096.
+ * bits_out [BH, NB, ceil(NB / 32)] of those (b, h). NB <= 46340 (NB^2 < 2^31).
  * Replaces csrc/vsa/vsa2_api.cpp:157-178 global_topk_into (topk.cu:69-578). */
 int vsa_global_topk(const float* scores, int NB, int bh0, int bh_count, long long budget, int* q2k_ptr, int* q2k_idx,
                     int* k2q_ptr, int* k2q_idx, unsigned* bits_out, void* workspace, size_t workspace_bytes,
@@ -196,14 +196,15 @@ int vsa_rep_build_kmeans(const void* k, const void* v, const int* blk_cnt, void*
 /* Per-query-block tiers (the three-tier benchmark construction's split; the reference splits by global budgets, rep_api.cpp
  * route_tiers): for every row i of the fp32 scores [bh_count, NB, NB] of (b, h) rows bh0.., the ka (tier A) and
  * kab (tiers A and B) best blocks, score desc, ties to the smaller index, -0 == +0, as ascending CSR lists with
- * offsets (bh * NB + i) * K and as selection bitmaps [BH, NB, ceil(NB / 32)]. 0 <= ka <= kab <= NB <= 2048. */
+ * offsets (bh * NB + i) * K and as selection bitmaps [BH, NB, ceil(NB / 32)]. 0 <= ka <= kab <= NB <= 8192. */
 int vsa_row_tiers(const float* scores, int NB, int bh0, int bh_count, int ka, int kab, int* a_ptr, int* a_idx,
                   int* ab_ptr, int* ab_idx, unsigned* bits_a, unsigned* bits_ab, hipStream_t stream);
 
 /* Three-tier forward: one softmax over the tier-A tokens (q2k CSR), the tier-B representatives (bits_ab & ~bits_a)
  * and the tier-C means (~bits_ab), each representative column with + log2(count); O bf16, lse natural. phases:
  * 1 | 2 | 4 selects the tiers. lc_mid_stride: 0 when lc_mid is one [NB * RM] table for every head, NB * RM when
- * it is per head (k-means tables). NB <= 2048. Replaces rep_api.cpp rep_attn_fwd (rep_attn_fwd.cu:37). */
+ * it is per head (k-means tables). NB <= 4096 (every three-tier entry point). Replaces rep_api.cpp rep_attn_fwd
+ * (rep_attn_fwd.cu:37). */
 int vsa_rep_attn_fwd(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
                      const float* lc_mid, int lc_mid_stride, const void* k_tail, const void* v_tail, const float* lc_tail,
                      const int* q2k_ptr, const int* q2k_idx, const unsigned* bits_a, const unsigned* bits_ab,

@@ -31,7 +31,7 @@ namespace {
 
 constexpr float LN2_F = 0.6931471805599453f;
 constexpr float SLACK = 8.0f;
-constexpr int REP_MAX_NB = 2048;
+constexpr int REP_MAX_NB = 4096;  // one LDS list of a query block's tier-B and tier-C blocks (disjoint: <= NB)
 enum { PH_A = 1, PH_B = 2, PH_C = 4 };
 
 struct RepArgs {
@@ -65,7 +65,9 @@ __device__ __forceinline__ unsigned row_word(const unsigned* bits, size_t row, i
 }
 
 // compact tier B (ab & ~a) and tier C (~ab) blocks of bitmap row `row` into LDS lists (wave 0)
-__device__ void build_lists(const RepArgs& a, size_t row, unsigned short* blist, unsigned short* clist, int* counts) {
+// tier-B blocks ascending into lists[0..), tier-C blocks ascending into lists[REP_MAX_NB - 1], [REP_MAX_NB - 2], ...
+// (the two never meet: a row holds at most NB <= REP_MAX_NB of them)
+__device__ void build_lists(const RepArgs& a, size_t row, unsigned short* lists, int* counts) {
   const int l = threadIdx.x & 63;
   int nb_run = 0, nc_run = 0;
   for (int w0 = 0; w0 < a.W; w0 += 64) {
@@ -90,12 +92,12 @@ __device__ void build_lists(const RepArgs& a, size_t row, unsigned short* blist,
     int ob = nb_run + ib - pb, oc = nc_run + ic - pc;
     while (bm) {
       const int b = __ffs(bm) - 1;
-      blist[ob++] = (unsigned short)(w * 32 + b);
+      lists[ob++] = (unsigned short)(w * 32 + b);
       bm &= bm - 1;
     }
     while (cm) {
       const int b = __ffs(cm) - 1;
-      clist[oc++] = (unsigned short)(w * 32 + b);
+      lists[REP_MAX_NB - 1 - oc++] = (unsigned short)(w * 32 + b);
       cm &= cm - 1;
     }
     nb_run += __shfl(ib, 63, 64);
@@ -112,7 +114,7 @@ template <bool BWD>
 __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
   __shared__ __attribute__((aligned(16))) char kv_s[2][2][BK * 256];
   __shared__ __attribute__((aligned(16))) float bias_s[2][BK];
-  __shared__ unsigned short blist[REP_MAX_NB], clist[REP_MAX_NB];
+  __shared__ unsigned short lists[REP_MAX_NB];
   __shared__ int counts[2];
 
   int bh, qb;  // XCD-aware, run-time balanced order of (query block, head) (queues.h)
@@ -127,7 +129,7 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
   const size_t tok = head + (size_t)qb * BK + qrow;
   const size_t brow = (size_t)bh * a.NB + qb;
 
-  if (wv == 0) build_lists(a, brow, blist, clist, counts);
+  if (wv == 0) build_lists(a, brow, lists, counts);
   Stream st;
   st.beg = sload(a.row_ptr + (size_t)bh * (a.NB + 1) + qb);
   st.nA = (a.phases & PH_A) ? sload(a.row_ptr + (size_t)bh * (a.NB + 1) + qb + 1) - st.beg : 0;
@@ -175,7 +177,7 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
     const int n = tb ? st.nBrows : st.nC;
     auto table_row = [&](int p) -> int {
       if (p >= n) return -1;
-      return tb ? (int)blist[p / a.RM] * a.RM + p % a.RM : (int)clist[p];
+      return tb ? (int)lists[p / a.RM] * a.RM + p % a.RM : (int)lists[REP_MAX_NB - 1 - p];
     };
     const srd_t r1 = tb ? rkm : rkt, r2 = tb ? rvm : rvt;
 #pragma unroll
@@ -687,7 +689,7 @@ using namespace es;
 static int rep_check(int BH, int L, int D, int RM) {
   ES_REQUIRE(BH > 0 && BH <= 65535 && L > 0 && L % BK == 0, ES_ERR_INVALID, "VSA2-rep: tokens must be [BH, L = NB * 64, D]");
   ES_REQUIRE(D == 64 || D == HD, ES_ERR_UNSUPPORTED, "VSA2-rep: head dim must be 64 or 128 (rows stored with 128 columns)");
-  ES_REQUIRE(L / BK <= REP_MAX_NB, ES_ERR_UNSUPPORTED, "VSA2-rep: NB <= 2048 blocks");
+  ES_REQUIRE(L / BK <= REP_MAX_NB, ES_ERR_UNSUPPORTED, "VSA2-rep: NB <= 4096 blocks");
   ES_REQUIRE(RM == 1 || RM == 2 || RM == 4 || RM == 8 || RM == 16, ES_ERR_INVALID,
              "RepTiers.mid_reps must be one of (1, 2, 4, 8, 16)");
   ES_REQUIRE((size_t)L * HD * 2 < (1ull << 31), ES_ERR_UNSUPPORTED, "VSA2-rep: one head's tokens exceed 2 GiB");

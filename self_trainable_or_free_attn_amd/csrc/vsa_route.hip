@@ -151,19 +151,29 @@ __global__ __launch_bounds__(256) void rows_select_kernel(RowsArgs a) {
 }
 
 // ------------------------------------------------------------------------------------ kv->q inversion
-// column counts of one 32-row group: gcnt[bhl][g][j]; rows >= NB have no bits set
+// column counts of one 32-row group: gcnt[bhl][g][j]; rows >= NB have no bits set. The group's bits are staged
+// in LDS COL_WORDS words (COL_WORDS * 32 columns) of every row at a time, so NB has no bound here.
+constexpr int COL_WORDS = 128;
 __global__ __launch_bounds__(256) void col_count_kernel(const unsigned* __restrict__ selbits, int* __restrict__ gcnt,
                                                         int NB, int W) {
-  __shared__ unsigned bits_s[ROWS * (MAX_NB / 32 * 2)];
+  __shared__ unsigned bits_s[ROWS * COL_WORDS];
   const int g = blockIdx.x, bhl = blockIdx.y, NG = (NB + ROWS - 1) / ROWS;
   const unsigned* src = selbits + ((size_t)bhl * NG * ROWS + (size_t)g * ROWS) * W;
   const int nrows = min(ROWS, NB - g * ROWS);
-  for (int e = threadIdx.x; e < nrows * W; e += 256) bits_s[e] = src[e];
-  __syncthreads();
-  for (int j = threadIdx.x; j < NB; j += 256) {
-    int c = 0;
-    for (int r = 0; r < nrows; ++r) c += (bits_s[r * W + (j >> 5)] >> (j & 31)) & 1u;
-    gcnt[((size_t)bhl * NG + g) * NB + j] = c;
+  for (int w0 = 0; w0 < W; w0 += COL_WORDS) {
+    const int nw = min(COL_WORDS, W - w0);
+    __syncthreads();
+    for (int e = threadIdx.x; e < nrows * nw; e += 256) {
+      const int r = e / nw, w = e - r * nw;
+      bits_s[r * COL_WORDS + w] = src[(size_t)r * W + w0 + w];
+    }
+    __syncthreads();
+    for (int j = w0 * 32 + threadIdx.x; j < min(NB, (w0 + nw) * 32); j += 256) {
+      const int wj = (j >> 5) - w0;
+      int c = 0;
+      for (int r = 0; r < nrows; ++r) c += (bits_s[r * COL_WORDS + wj] >> (j & 31)) & 1u;
+      gcnt[((size_t)bhl * NG + g) * NB + j] = c;
+    }
   }
 }
 
@@ -214,16 +224,24 @@ __global__ __launch_bounds__(1024) void col_scan_kernel(int* __restrict__ gcnt, 
 __global__ __launch_bounds__(256) void col_emit_kernel(const unsigned* __restrict__ selbits,
                                                        const int* __restrict__ goff, int* __restrict__ k2q_idx, int NB,
                                                        int W) {
-  __shared__ unsigned bits_s[ROWS * (MAX_NB / 32 * 2)];
+  __shared__ unsigned bits_s[ROWS * COL_WORDS];
   const int g = blockIdx.x, bhl = blockIdx.y, NG = (NB + ROWS - 1) / ROWS;
   const unsigned* src = selbits + ((size_t)bhl * NG * ROWS + (size_t)g * ROWS) * W;
   const int nrows = min(ROWS, NB - g * ROWS);
-  for (int e = threadIdx.x; e < nrows * W; e += 256) bits_s[e] = src[e];
-  __syncthreads();
-  for (int j = threadIdx.x; j < NB; j += 256) {
-    int n = goff[((size_t)bhl * NG + g) * NB + j];
-    for (int r = 0; r < nrows; ++r)
-      if ((bits_s[r * W + (j >> 5)] >> (j & 31)) & 1u) k2q_idx[n++] = g * ROWS + r;
+  for (int w0 = 0; w0 < W; w0 += COL_WORDS) {
+    const int nw = min(COL_WORDS, W - w0);
+    __syncthreads();
+    for (int e = threadIdx.x; e < nrows * nw; e += 256) {
+      const int r = e / nw, w = e - r * nw;
+      bits_s[r * COL_WORDS + w] = src[(size_t)r * W + w0 + w];
+    }
+    __syncthreads();
+    for (int j = w0 * 32 + threadIdx.x; j < min(NB, (w0 + nw) * 32); j += 256) {
+      const int wj = (j >> 5) - w0;
+      int n = goff[((size_t)bhl * NG + g) * NB + j];
+      for (int r = 0; r < nrows; ++r)
+        if ((bits_s[r * COL_WORDS + wj] >> (j & 31)) & 1u) k2q_idx[n++] = g * ROWS + r;
+    }
   }
 }
 
@@ -741,7 +759,6 @@ extern "C" int vsa_global_topk(const float* scores, int NB, int bh0, int bh_coun
   ES_REQUIRE(scores && q2k_ptr && k2q_ptr && workspace, ES_ERR_INVALID, "VSA: null tensor pointer");
   ES_REQUIRE(NB >= 1 && NB <= 46340 && bh0 >= 0 && bh_count >= 1 && bh_count <= 65535, ES_ERR_INVALID,
              "VSA: bad top-k shape");
-  ES_REQUIRE(NB <= MAX_NB * 2, ES_ERR_UNSUPPORTED, "VSA: global top-k supports NB <= 4096 blocks");
   ES_REQUIRE(workspace_bytes >= vsa_topk_workspace(bh_count, NB), ES_ERR_INVALID, "VSA: top-k workspace too small");
   const long long nn = (long long)NB * NB;
   const long long keff = budget < 0 ? 0 : (budget < nn ? budget : nn);
@@ -831,8 +848,8 @@ extern "C" int ES_VSA_API(vsa_router_scores)(const void* qr, const void* kr, con
 extern "C" int vsa_csr_transpose(const int* ptr, const int* idx, int NB, int bh0, int bh_count, int* out_ptr,
                                  int* out_idx, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   ES_REQUIRE(ptr && out_ptr && workspace, ES_ERR_INVALID, "VSA: null tensor pointer");
-  ES_REQUIRE(NB >= 1 && NB <= MAX_NB * 2 && bh0 >= 0 && bh_count >= 1 && bh_count <= 65535, ES_ERR_INVALID,
-             "VSA: bad CSR shape (NB <= 4096)");
+  ES_REQUIRE(NB >= 1 && NB <= 46340 && bh0 >= 0 && bh_count >= 1 && bh_count <= 65535, ES_ERR_INVALID,
+             "VSA: bad CSR shape (1 <= NB <= 46340)");
   ES_REQUIRE(workspace_bytes >= vsa_topk_workspace(bh_count, NB), ES_ERR_INVALID, "VSA: workspace too small");
   TopkCarve c;
   carve(workspace, bh_count, NB, &c);

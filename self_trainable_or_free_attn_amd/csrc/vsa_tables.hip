@@ -244,8 +244,8 @@ extern "C" int ES_VSA_API(vsa_rep_build_kmeans)(const void* k, const void* v, co
 namespace es {
 namespace {
 
-constexpr int TIER_MAX_NB = 2048;
-constexpr int TIER_CH = TIER_MAX_NB / 64;
+// keys of one row in registers, CH per lane (64 * CH >= NB): CH = 32, 64 or 128, so NB <= 8192
+constexpr int TIER_MAX_NB = 8192;
 
 // order-preserving key of a float: larger key = larger value, -0 and +0 share a key
 __device__ __forceinline__ unsigned okey(float f) {
@@ -263,6 +263,7 @@ struct TierArgs {
 };
 
 // the K-th largest key of the row (K >= 1): the largest T with #(key >= T) >= K, built bit by bit from the top
+template <int TIER_CH>
 __device__ __forceinline__ unsigned kth_key(const unsigned (&key)[TIER_CH], int nch, int NB, int K) {
   const int l = threadIdx.x & 63;
   unsigned T = 0u;
@@ -277,6 +278,7 @@ __device__ __forceinline__ unsigned kth_key(const unsigned (&key)[TIER_CH], int 
   return T;
 }
 
+template <int TIER_CH>
 __device__ __forceinline__ void emit(const unsigned (&key)[TIER_CH], int nch, int NB, int W, int K, int* ptr,
                                      int* idx, unsigned* bits, size_t bh, int i) {
   const int l = threadIdx.x & 63;
@@ -314,6 +316,7 @@ __device__ __forceinline__ void emit(const unsigned (&key)[TIER_CH], int nch, in
   }
 }
 
+template <int TIER_CH>
 __global__ __launch_bounds__(256) void row_tiers_kernel(TierArgs a) {
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
   if (r >= a.rows) return;
@@ -335,7 +338,7 @@ extern "C" int vsa_row_tiers(const float* scores, int NB, int bh0, int bh_count,
                              int* a_idx, int* ab_ptr, int* ab_idx, unsigned* bits_a, unsigned* bits_ab,
                              hipStream_t stream) {
   ES_REQUIRE(scores && a_ptr && ab_ptr && bits_a && bits_ab, ES_ERR_INVALID, "VSA2-rep: null tensor pointer");
-  ES_REQUIRE(NB >= 1 && NB <= TIER_MAX_NB, ES_ERR_UNSUPPORTED, "VSA2-rep: per-row tiers support 1 <= NB <= 2048");
+  ES_REQUIRE(NB >= 1 && NB <= TIER_MAX_NB, ES_ERR_UNSUPPORTED, "VSA2-rep: per-row tiers support 1 <= NB <= 8192");
   ES_REQUIRE(bh0 >= 0 && bh_count >= 1 && (long long)bh_count * NB < (1LL << 31), ES_ERR_INVALID,
              "VSA2-rep: bad (b,h) range");
   ES_REQUIRE(0 <= ka && ka <= kab && kab <= NB, ES_ERR_INVALID, "VSA2-rep: need 0 <= ka <= kab <= NB");
@@ -344,7 +347,13 @@ extern "C" int vsa_row_tiers(const float* scores, int NB, int bh0, int bh_count,
              "VSA2-rep: selected blocks exceed int32 CSR range");
   TierArgs a = {scores, NB, (NB + 31) / 32, bh0, bh_count * NB, ka, kab, a_ptr, a_idx, ab_ptr, ab_idx, bits_a,
                 bits_ab};
-  hipLaunchKernelGGL(row_tiers_kernel, dim3((unsigned)((a.rows + 3) / 4)), dim3(256), 0, stream, a);
+  const dim3 grid((unsigned)((a.rows + 3) / 4));
+  if (NB <= 2048)
+    hipLaunchKernelGGL(row_tiers_kernel<32>, grid, dim3(256), 0, stream, a);
+  else if (NB <= 4096)
+    hipLaunchKernelGGL(row_tiers_kernel<64>, grid, dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL(row_tiers_kernel<128>, grid, dim3(256), 0, stream, a);
   return check_launch("vsa_row_tiers");
 }
 
