@@ -144,18 +144,17 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
     f32x16 s = {};
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) s = emfma(elds16(kb, koff[ks]), qreg[ks], s);
-    float p[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) p[r] = s[r] * scale;
+    // the maximum is taken on the raw products (scale > 0: max(s) * scale is the maximum of the scaled logits, the
+    // rounding being monotone), and the scaling is folded into the multiply-add in front of each exponential
     if (ccur < BK) {  // key columns past the block's valid tokens
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        if (32 * kh + 8 * (r / 4) + 4 * hi + (r % 4) >= ccur) p[r] = -INFINITY;
+        if (32 * kh + 8 * (r / 4) + 4 * hi + (r % 4) >= ccur) s[r] = -INFINITY;
     }
-    float mx = p[0];
+    float mx = s[0];
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, p[r]);
-    mx = max_xor32(mx);
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+    mx = max_xor32(mx) * scale;
     if (__builtin_amdgcn_ballot_w64(mx > mref + RESCALE_SLACK) != 0) {
       const float mnew = fmaxf(mref, mx);
       const float alpha = mref == -INFINITY ? 0.0f : exp2f_fast(mref - mnew);
@@ -167,8 +166,9 @@ __global__ __launch_bounds__(256, 2) void vsa_fwd_kernel(VsaFwdArgs a) {
       mref = mnew;
     }
     const float msub = mref == -INFINITY ? 0.0f : mref;
+    float p[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) p[r] = exp2f_fast(p[r] - msub);
+    for (int r = 0; r < 16; ++r) p[r] = exp2f_fast(fmaf(s[r], scale, -msub));
     const ev8 pa = epack8(&p[0]), pb = epack8(&p[8]);
     lsum += esum8(pb, esum8(pa, 0.0f));
 #pragma unroll

@@ -301,7 +301,7 @@ __device__ __forceinline__ void emit(const unsigned (&key)[TIER_CH], int nch, in
   const unsigned long long below = (1ull << l) - 1ull;
 #pragma unroll
   for (int ch = 0; ch < TIER_CH; ++ch) {
-    if (ch >= nch) break;
+    if (ch >= nch) continue;  // (not a break: the loop must unroll fully so that key[] stays in registers)
     const int j = ch * 64 + l;
     const bool in = j < NB;
     const bool eq = in && key[ch] == T;
