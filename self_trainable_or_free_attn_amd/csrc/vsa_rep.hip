@@ -158,10 +158,12 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
     lrow[i] = R;
     chb[i] = (unsigned)(((P & 15) ^ swz(R)) * 16);
   }
-  // stage chunk cj into buffer sb; returns (wave 0) the bias of chunk column l
-  auto issue = [&](int cj, int sb) -> float {
+  // stage chunk cj into buffer sb; returns (wave 0) the bias of chunk column l; `plain`: a tier-A block of 64
+  // valid tokens (every bias 0)
+  auto issue = [&](int cj, int sb, bool& plain) -> float {
     char* kd = kv_s[sb][0] + wv * 4096;
     char* vd = kv_s[sb][1] + wv * 4096;
+    plain = false;
     if (cj < st.cA) {
       const int b = __builtin_amdgcn_readfirstlane(a.col_idx[st.beg + cj]);
       const unsigned soff = (unsigned)b * (BK * 256);
@@ -170,7 +172,9 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
         dma16(rk, kd + i * 1024, (unsigned)lrow[i] * 256 + chb[i], soff);
         dma16(rv, vd + i * 1024, (unsigned)lrow[i] * 256 + chb[i], soff);
       }
-      return l < sload(a.blk_cnt + b) ? 0.0f : -INFINITY;
+      const int cnt = sload(a.blk_cnt + b);
+      plain = cnt == BK;
+      return l < cnt ? 0.0f : -INFINITY;
     }
     const bool tb = cj < st.cA + st.cB;
     const int p0 = (cj - (tb ? st.cA : st.cA + st.cB)) * BK;
@@ -220,8 +224,9 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
   for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
   float lsum = 0.0f, mref = -INFINITY;
 
+  bool plain = false;  // chunk j is a tier-A block of 64 valid tokens: no bias, the scale goes into the exponent
   if (nc > 0) {
-    const float b0 = issue(0, 0);
+    const float b0 = issue(0, 0, plain);
     if (wv == 0) bias_s[0][l] = b0;
   }
   dma_wait();
@@ -229,24 +234,36 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
   for (int j = 0; j < nc; ++j) {
     const int sb = j & 1;
     float bn = 0.0f;
-    if (j + 1 < nc) bn = issue(j + 1, sb ^ 1);
+    bool plain_next = false;
+    if (j + 1 < nc) bn = issue(j + 1, sb ^ 1, plain_next);
     const char* kt = kv_s[sb][0];
     const char* vt = kv_s[sb][1];
     f32x16 s = {};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) s = emfma(elds16(kt, koff[ks]), qreg[ks], s);
     float x[16];
+    if (!plain) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bias_s[sb][32 * kh + 8 * g + 4 * hi]);
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bias_s[sb][32 * kh + 8 * g + 4 * hi]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) x[4 * g + e] = fmaf(s[4 * g + e], a.scale_log2, b4[e]);
+        for (int e = 0; e < 4; ++e) x[4 * g + e] = fmaf(s[4 * g + e], a.scale_log2, b4[e]);
+      }
     }
     if (!BWD) {
-      float mx = x[0];
+      // (a plain chunk takes its maximum on the raw products: the scale is positive and rounding monotone)
+      float mx;
+      if (plain) {
+        mx = s[0];
 #pragma unroll
-      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, x[r]);
-      mx = max_xor32(mx);
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+        mx = max_xor32(mx) * a.scale_log2;
+      } else {
+        mx = x[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, x[r]);
+        mx = max_xor32(mx);
+      }
       if (__builtin_amdgcn_ballot_w64(mx > mref + SLACK) != 0) {
         const float mnew = fmaxf(mref, mx);
         const float alpha = mref == -INFINITY ? 0.0f : exp2f_fast(mref - mnew);
@@ -258,8 +275,13 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
         mref = mnew;
       }
       const float msub = mref == -INFINITY ? 0.0f : mref;
+      if (plain) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) x[r] = exp2f_fast(x[r] - msub);
+        for (int r = 0; r < 16; ++r) x[r] = exp2f_fast(fmaf(s[r], a.scale_log2, -msub));
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[r] = exp2f_fast(x[r] - msub);
+      }
       const ev8 pa = epack8(&x[0]), pb = epack8(&x[8]);
       lsum += esum8(pb, esum8(pa, 0.0f));
 #pragma unroll
@@ -272,8 +294,13 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) dp = emfma(elds16(vt, koff[ks]), dreg[ks], dp);
       float ds[16];
+      if (plain) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) ds[r] = exp2f_fast(x[r] - ls) * (dp[r] - dl) * a.scale;
+        for (int r = 0; r < 16; ++r) ds[r] = exp2f_fast(fmaf(s[r], a.scale_log2, -ls)) * (dp[r] - dl) * a.scale;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ds[r] = exp2f_fast(x[r] - ls) * (dp[r] - dl) * a.scale;
+      }
       const ev8 sa = epack8(&ds[0]), sb8 = epack8(&ds[8]);
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
@@ -285,6 +312,7 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
     if (j + 1 < nc && wv == 0) bias_s[sb ^ 1][l] = bn;
     dma_wait();
     __syncthreads();
+    plain = plain_next;
   }
 
   // combine the two key halves of each row group through LDS
