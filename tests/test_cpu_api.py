@@ -180,3 +180,43 @@ def test_torch_operators_trace_with_meta_tensors_and_refuse_host_tensors():
     c = torch.zeros(64, 1, 128, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="es_block_means: every tensor argument must live on the GPU"):
         ops.es_block_means(c, c, c[:1], c[:1], 64, 1, 128)
+
+
+def test_block_count_limits_are_refused_before_any_launch():
+    """Each VSA entry point with a block-count limit refuses a larger NB with a message, before any HIP call:
+    route_rows NB <= 2048, the three-tier kernels NB <= 4096, the per-row tiers NB <= 8192, the global top-k and the
+    CSR transpose NB <= 46 340; the limits themselves are accepted as far as that check."""
+    so = library()
+    so.es_last_error_string.restype = ctypes.c_char_p
+    p = ctypes.c_void_p(256)
+    i, ll, sz = ctypes.c_int, ctypes.c_longlong, ctypes.c_size_t
+    null = ctypes.c_void_p(0)
+
+    def route_rows(nb, bh_count=1):
+        return so.vsa_route_rows(p, p, i(nb), i(64 * ((nb + 63) // 64)), i(0), i(bh_count), i(1), i(128), p, p, p, p,
+                                 p, sz(1 << 40), null)
+
+    def rep_fwd(nb):
+        return so.vsa_rep_attn_fwd(p, p, p, p, p, p, i(0), p, p, p, p, p, p, p, p, p, p, i(1), i(nb * 64), i(128),
+                                   i(4), i(8), null)
+
+    def row_tiers(nb):
+        return so.vsa_row_tiers(p, i(nb), i(0), i(1), i(0), i(nb + 1), p, p, p, p, p, p, null)
+
+    def global_topk(nb):
+        return so.vsa_global_topk(p, i(nb), i(0), i(1), ll(1), p, p, p, p, p, p, sz(0), null)
+
+    def csr_transpose(nb):
+        return so.vsa_csr_transpose(p, p, i(nb), i(0), i(1), p, p, p, sz(0), null)
+
+    # (name, call, the largest NB, the refusal text). At the limit a later host check must fail instead, so that no
+    # kernel ever sees these placeholder pointers: no (b, h) rows, phases 8, kab > NB, a workspace too small.
+    cases = [("route_rows", route_rows, 2048, b"NB <= 2048"), ("rep_attn_fwd", rep_fwd, 4096, b"NB <= 4096"),
+             ("row_tiers", row_tiers, 8192, b"NB <= 8192"), ("global_topk", global_topk, 46340, b"bad top-k shape"),
+             ("csr_transpose", csr_transpose, 46340, b"NB <= 46340")]
+    for name, call, limit, text in cases:
+        assert call(limit + 1) != 0, name
+        assert text in so.es_last_error_string(), (name, so.es_last_error_string())
+        assert (call(limit, 0) if name == "route_rows" else call(limit)) != 0, name
+        msg = so.es_last_error_string()
+        assert text not in msg and msg, (name, msg)
