@@ -118,7 +118,7 @@ int vsa_block_scores(const void* qc, const void* kc, void* scores, int NB, int N
                      hipStream_t stream);
 
 /* Original-VSA router: the block scores and exactly K blocks per row (score desc, ties to the smaller index,
- * -0 == +0) into the q2k / k2q CSR of rows bh0 .. (offsets (b * NB + i) * K). NB <= 2048.
+ * -0 == +0) into the q2k / k2q CSR of rows bh0 .. (offsets (b * NB + i) * K). NB <= 8192.
  * Replaces csrc/vsa/vsa2_api.cpp:284-315 route_rows (topk.cu:621-685). */
 int vsa_route_rows(const void* qc, const void* kc, int NB, int NBc_pad, int bh0, int bh_count, int K, int D,
                    int* q2k_ptr, int* q2k_idx, int* k2q_ptr, int* k2q_idx, void* workspace, size_t workspace_bytes,

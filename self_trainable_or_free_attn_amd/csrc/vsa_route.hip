@@ -29,6 +29,8 @@ namespace {
 
 constexpr int ROWS = 32;        // query-block rows per rows_select / inversion group
 constexpr int MAX_NB = 2048;    // rows_select keeps a 32 x ceil64(NB) strip of 16-bit keys in LDS (<= 128 KB)
+constexpr int WIDE_ROWS = 8;    // past MAX_NB: an 8 x ceil64(NB) strip (the rows of one S tile split over 4 workgroups)
+constexpr int MAX_NB_WIDE = 8192;
 
 // order-preserving keys: larger key = larger value; -0 and +0 share a key
 __device__ __forceinline__ unsigned key16(unsigned u) {
@@ -56,27 +58,67 @@ struct RowsArgs {
   float scale;
 };
 
-// grid (cdiv(NB, 32), bh_count), 256 threads. K < 0: scores only.
-template <bool FROM_SCORES>
+// the selection of one row whose keys stay in LDS (WIDE): the same bisection of the K-th key, count of the keys
+// above it and ascending emission with the T-equal entries taken smallest column first, as the register form below
+__device__ __forceinline__ void select_row_lds(const unsigned short* keys, int NB, int nchunk, int K, int* out,
+                                               unsigned* bits, int W) {
+  const int l = threadIdx.x & 63;
+  unsigned T = 0x10000u;
+  if (K > 0) {
+    unsigned lo = 0, hi2 = 0x10000u;
+    while (hi2 - lo > 1) {
+      const unsigned mid = (lo + hi2) >> 1;
+      int cnt = 0;
+      for (int c = 0; c < nchunk; ++c) cnt += __popcll(__builtin_amdgcn_ballot_w64(keys[64 * c + l] >= mid));
+      if (cnt >= K) lo = mid; else hi2 = mid;
+    }
+    T = lo;
+  }
+  int above = 0;
+  for (int c = 0; c < nchunk; ++c)
+    above += __popcll(__builtin_amdgcn_ballot_w64((unsigned)keys[64 * c + l] > T && 64 * c + l < NB));
+  const int take_eq = K - above;
+  int eq_run = 0, sel_run = 0;
+  for (int c = 0; c < nchunk; ++c) {
+    const int j = 64 * c + l;
+    const unsigned kv = keys[j];
+    const bool in = j < NB;
+    const bool eq = in && kv == T;
+    const unsigned long long eqb = __builtin_amdgcn_ballot_w64(eq);
+    const bool sel = in && (kv > T || (eq && eq_run + __popcll(eqb & lanes_below()) < take_eq));
+    const unsigned long long sb = __builtin_amdgcn_ballot_w64(sel);
+    if (sel) out[sel_run + __popcll(sb & lanes_below())] = j;
+    eq_run += __popcll(eqb);
+    sel_run += __popcll(sb);
+    if (l < 2 && 2 * c + l < W) bits[2 * c + l] = (unsigned)(sb >> (32 * l));
+  }
+}
+
+// grid (cdiv(NB, SR), bh_count), 256 threads, SR = 32 rows per workgroup (NB <= 2048, the keys of a row in
+// registers) or 8 (WIDE, NB <= 8192: the S tile of 32 rows is computed by each of its four workgroups, which keep
+// their 8 rows; the keys are read from LDS in every step). K < 0: scores only.
+template <bool FROM_SCORES, bool WIDE>
 __global__ __launch_bounds__(256) void rows_select_kernel(RowsArgs a) {
-  extern __shared__ __attribute__((aligned(16))) unsigned short keys_s[];  // [32][NBp]
+  constexpr int SR = WIDE ? WIDE_ROWS : ROWS;
+  extern __shared__ __attribute__((aligned(16))) unsigned short keys_s[];  // [SR][NBp]
   const int strip = blockIdx.x, bhl = blockIdx.y;
   const int NB = a.NB, NBp = (NB + 63) & ~63;
   const int l = threadIdx.x & 63, hi = l >> 5, lq = l & 31;
   const int wv = threadIdx.x >> 6;
-  const int r0 = strip * ROWS;
+  const int r0 = strip * SR;           // first row of this workgroup
+  const int t0 = r0 & ~(ROWS - 1);    // first row of its S tile
   const size_t bh = (size_t)(a.bh0 + bhl);
 
   if (FROM_SCORES) {
-    for (int e = threadIdx.x; e < ROWS * NBp; e += 256) {
+    for (int e = threadIdx.x; e < SR * NBp; e += 256) {
       const int r = e / NBp, c = e - r * NBp;
       const int row = r0 + r;
       keys_s[e] = (row < NB && c < NB) ? (unsigned short)key16(a.scores_in[((size_t)bhl * NB + row) * NB + c]) : 0;
     }
   } else {
-    // S strip: A = qc rows r0 .. r0 + 31 (registers), B = kc rows of each 32-column tile (L2)
+    // S strip: A = qc rows t0 .. t0 + 31 (registers), B = kc rows of each 32-column tile (L2)
     ev8 qa[8];
-    const e16_t* qp = a.qc + (bh * a.NBc_pad + r0 + lq) * HD + 8 * hi;
+    const e16_t* qp = a.qc + (bh * a.NBc_pad + t0 + lq) * HD + 8 * hi;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) qa[ks] = *reinterpret_cast<const ev8*>(qp + 16 * ks);
     for (int ct = wv; ct < NBp / 32; ct += 4) {
@@ -87,7 +129,8 @@ __global__ __launch_bounds__(256) void rows_select_kernel(RowsArgs a) {
       const int col = ct * 32 + lq;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int rr = 8 * (r / 4) + 4 * hi + (r % 4);
+        const int rr = t0 + 8 * (r / 4) + 4 * hi + (r % 4) - r0;  // row within this workgroup's strip
+        if (WIDE && (rr < 0 || rr >= SR)) continue;
         const e16_t s = f2e(mul_rn(e2f(f2e(acc[r])), a.scale));
         const bool in = r0 + rr < NB && col < NB;
         keys_s[rr * NBp + col] = in ? (unsigned short)key16(s) : 0;
@@ -99,7 +142,7 @@ __global__ __launch_bounds__(256) void rows_select_kernel(RowsArgs a) {
   __syncthreads();
 
   const int K = a.K, nchunk = NBp / 64;
-  for (int rr = wv; rr < ROWS; rr += 4) {
+  for (int rr = wv; rr < SR; rr += 4) {
     const int row = r0 + rr;
     if (row >= NB) break;
     const long long base = ((long long)bh * NB + row) * K;
@@ -107,6 +150,11 @@ __global__ __launch_bounds__(256) void rows_select_kernel(RowsArgs a) {
       int* ptr = a.q2k_ptr + bh * (NB + 1);
       ptr[row] = (int)base;
       if (row == NB - 1) ptr[NB] = (int)(base + K);
+    }
+    if (WIDE) {
+      select_row_lds(keys_s + rr * NBp, NB, nchunk, K, a.q2k_idx + base,
+                     a.selbits + ((size_t)bhl * (size_t)((NB + 31) & ~31) + row) * a.W, a.W);
+      continue;
     }
     unsigned kv[MAX_NB / 64];
 #pragma unroll
@@ -680,7 +728,7 @@ static int invert(const TopkCarve& c, int* k2q_ptr, int* k2q_idx, int NB, int bh
 static int rows_common(const void* qc, const void* kc, const void* scores_in, void* scores_out, int NB, int NBc_pad,
                        int bh0, int bh_count, int K, int* q2k_ptr, int* q2k_idx, int* k2q_ptr, int* k2q_idx,
                        void* workspace, size_t workspace_bytes, int D, hipStream_t stream, const char* what) {
-  ES_REQUIRE(NB >= 1 && NB <= MAX_NB, ES_ERR_UNSUPPORTED, "VSA: route_rows supports 1 <= NB <= 2048 blocks");
+  ES_REQUIRE(NB >= 1 && NB <= MAX_NB_WIDE, ES_ERR_UNSUPPORTED, "VSA: route_rows supports 1 <= NB <= 8192 blocks");
   ES_REQUIRE(bh0 >= 0 && bh_count >= 1 && bh_count <= 65535, ES_ERR_INVALID, "VSA: bad (b,h) range");
   RowsArgs a = {};
   a.qc = (const e16_t*)qc;
@@ -692,11 +740,16 @@ static int rows_common(const void* qc, const void* kc, const void* scores_in, vo
   a.bh0 = bh0;
   a.W = (NB + 31) / 32;
   a.scale = 1.0f / sqrtf((float)D);  // D: the logical head dimension (64 or 128)
-  const size_t lds = (size_t)ROWS * ((NB + 63) & ~63) * 2;
-  const dim3 grid((NB + ROWS - 1) / ROWS, bh_count);
+  const bool wide = NB > MAX_NB;
+  const int SR = wide ? WIDE_ROWS : ROWS;
+  const size_t lds = (size_t)SR * ((NB + 63) & ~63) * 2;  // <= 128 KB either way
+  const dim3 grid((NB + SR - 1) / SR, bh_count);
   if (K < 0) {  // scores only
     a.K = -1;
-    hipLaunchKernelGGL(rows_select_kernel<false>, grid, dim3(256), lds, stream, a);
+    if (wide)
+      hipLaunchKernelGGL((rows_select_kernel<false, true>), grid, dim3(256), lds, stream, a);
+    else
+      hipLaunchKernelGGL((rows_select_kernel<false, false>), grid, dim3(256), lds, stream, a);
     return check_launch(what);
   }
   ES_REQUIRE(q2k_ptr && k2q_ptr && workspace, ES_ERR_INVALID, "VSA: null tensor pointer");
@@ -716,10 +769,14 @@ static int rows_common(const void* qc, const void* kc, const void* scores_in, vo
                        NB, W, bh_count);
   hipLaunchKernelGGL(fill_base_kernel, dim3((bh_count + 255) / 256), dim3(256), 0, stream, c.base,
                      (const TopkState*)nullptr, (long long)NB * K, (const int*)nullptr, NB, bh0, bh_count);
-  if (scores_in != nullptr)
-    hipLaunchKernelGGL(rows_select_kernel<true>, grid, dim3(256), lds, stream, a);
+  if (scores_in != nullptr && wide)
+    hipLaunchKernelGGL((rows_select_kernel<true, true>), grid, dim3(256), lds, stream, a);
+  else if (scores_in != nullptr)
+    hipLaunchKernelGGL((rows_select_kernel<true, false>), grid, dim3(256), lds, stream, a);
+  else if (wide)
+    hipLaunchKernelGGL((rows_select_kernel<false, true>), grid, dim3(256), lds, stream, a);
   else
-    hipLaunchKernelGGL(rows_select_kernel<false>, grid, dim3(256), lds, stream, a);
+    hipLaunchKernelGGL((rows_select_kernel<false, false>), grid, dim3(256), lds, stream, a);
   invert(c, k2q_ptr, k2q_idx, NB, bh0, bh_count, stream);
   return check_launch(what);
 }

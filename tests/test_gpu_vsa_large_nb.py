@@ -1,6 +1,7 @@
-"""VSA2 routing and three-tier attention beyond 2048 blocks (longer videos than the HunyuanVideo benchmark clip):
-the exact global top-k and the kv->q inversion at NB = 4200, the per-query-block tiers at NB = 3000 and 5000 (the
-64- and 128-chunk register layouts), all byte for byte against the oracle; and the three-tier forward / backward at
+"""VSA routing and three-tier attention beyond 2048 blocks (longer videos than the HunyuanVideo benchmark clip):
+the original-VSA router (block scores and per-row top-K, 8 rows per workgroup past 2048 blocks) at NB = 2049, 3000
+and 5000, the exact global top-k and the kv->q inversion at NB = 4200, the per-query-block tiers at NB = 3000 and
+5000 (the 64- and 128-chunk register layouts), all byte for byte against the oracle; and the three-tier forward / backward at
 NB = 3000 (192 000 tokens, a 40-token tail block) in both constructions, O / LSE / dQ of sampled query blocks and
 dK / dV of sampled kv blocks against the float64 oracle (oracle/vsa_ref.py rep_fine_head restated per block, and
 rep_kv_block_grads), max-abs 2e-2 / rel-L2 1e-2 with the gradients' conditioning bound (see
@@ -40,6 +41,53 @@ def bitmap(mask):
     m[:, :nb] = mask
     return (m.reshape(nb, w, 32).astype(np.uint64) << np.arange(32, dtype=np.uint64)).sum(-1).astype(np.uint32) \
         .view(np.int32)
+
+
+def check_csr(q2k_ptr, q2k_idx, k2q_ptr, k2q_idx, mask):
+    qp, qi, kp, ki = (x.cpu().numpy() for x in (q2k_ptr, q2k_idx, k2q_ptr, k2q_idx))
+    rp, ri = ref.csr_from_mask(mask)
+    assert np.array_equal(qp, rp) and np.array_equal(qi[:ri.size], ri), "q2k lists differ"
+    cp, ci = ref.csr_from_mask(np.swapaxes(mask, -1, -2))
+    assert np.array_equal(kp, cp) and np.array_equal(ki[:ci.size], ci), "k2q lists differ"
+
+
+@pytest.mark.parametrize("NB,K", [(2049, 2049), (2049, 0), (3000, 150), (5000, 61)])
+def test_route_rows_beyond_2048(dev, NB, K):
+    B, H, D = 1, 2, 128
+    log("route_rows NB", NB, "K", K)
+    g = torch.Generator().manual_seed(NB + K)
+    pad = -(-NB // 64) * 64
+    qc, kc = ((torch.randn(B, H, pad, D, generator=g) * 0.5).to(torch.bfloat16).to(dev) for _ in range(2))
+    scores = C().block_scores(qc, kc, NB)
+    got = C().route_rows(qc, kc, NB, K)
+    torch.cuda.synchronize()
+    gs = f32(scores)
+    # the scores of the wide path against the float64 op: the GPU's fp32 dot differs from the exact one by at most
+    # n u sum|q k| (n = 128 terms, u = 2^-24), and the two bf16 roundings then land at most one step further each
+    h = 1
+    rows = np.r_[0:40, NB - 40:NB]
+    qh, kh = f32(qc)[0, h, rows].astype(np.float64), f32(kc)[0, h, :NB].astype(np.float64)
+    want_s = ref.block_scores(qh, kh)
+    step = np.exp2(np.floor(np.log2(np.maximum(np.abs(want_s), 2.0 ** -100))) - 7)
+    dot_err = D * 2.0 ** -24 * (np.abs(qh) @ np.abs(kh).T) / np.sqrt(D)
+    assert (np.abs(gs[h, rows] - want_s) <= 2 * step + dot_err).all()
+    assert (gs[h, rows] == want_s).mean() > 0.95
+    check_csr(*got, ref.row_topk_mask(gs.reshape(B, H, NB, NB), K))
+
+
+def test_row_topk_beyond_2048_with_ties(dev):
+    NB, K = 5000, 700
+    log("row_topk NB", NB, "K", K)
+    g = torch.Generator().manual_seed(9)
+    s = (torch.randint(-24, 24, (2, NB, NB), generator=g).float() / 8).to(torch.bfloat16)
+    s[0, 3] = -0.0
+    s[1, :, 17] = 0.0
+    i32 = dict(device=dev, dtype=torch.int32)
+    out = [torch.empty(1, 2, NB + 1, **i32), torch.empty(2 * NB * K, **i32), torch.empty(1, 2, NB + 1, **i32),
+           torch.empty(2 * NB * K, **i32)]
+    C().row_topk_into(s.to(dev), K, 0, *out)
+    torch.cuda.synchronize()
+    check_csr(*out, ref.row_topk_mask(f32(s).reshape(1, 2, NB, NB), K))
 
 
 def test_global_topk_and_inversion_beyond_4096(dev):
