@@ -203,7 +203,7 @@ int vsa_row_tiers(const float* scores, int NB, int bh0, int bh_count, int ka, in
 /* Three-tier forward: one softmax over the tier-A tokens (q2k CSR), the tier-B representatives (bits_ab & ~bits_a)
  * and the tier-C means (~bits_ab), each representative column with + log2(count); O bf16, lse natural. phases:
  * 1 | 2 | 4 selects the tiers. lc_mid_stride: 0 when lc_mid is one [NB * RM] table for every head, NB * RM when
- * it is per head (k-means tables). NB <= 4096 (every three-tier entry point). Replaces rep_api.cpp rep_attn_fwd
+ * it is per head (k-means tables). NB <= 8192 (every three-tier entry point). Replaces rep_api.cpp rep_attn_fwd
  * (rep_attn_fwd.cu:37). */
 int vsa_rep_attn_fwd(const void* q, const void* k, const void* v, const void* k_mid, const void* v_mid,
                      const float* lc_mid, int lc_mid_stride, const void* k_tail, const void* v_tail, const float* lc_tail,

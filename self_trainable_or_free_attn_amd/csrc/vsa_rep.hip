@@ -31,7 +31,9 @@ namespace {
 
 constexpr float LN2_F = 0.6931471805599453f;
 constexpr float SLACK = 8.0f;
-constexpr int REP_MAX_NB = 4096;  // one LDS list of a query block's tier-B and tier-C blocks (disjoint: <= NB)
+constexpr int REP_LIST = 4096;    // one LDS list of a query block's tier-B and tier-C blocks (disjoint: <= NB)
+constexpr int REP_MAX_NB = 8192;  // past REP_LIST blocks the forward / dQ take a list of this size (82 KB of LDS in all:
+                                  // one workgroup per CU instead of two)
 enum { PH_A = 1, PH_B = 2, PH_C = 4 };
 
 struct RepArgs {
@@ -65,8 +67,9 @@ __device__ __forceinline__ unsigned row_word(const unsigned* bits, size_t row, i
 }
 
 // compact tier B (ab & ~a) and tier C (~ab) blocks of bitmap row `row` into LDS lists (wave 0)
-// tier-B blocks ascending into lists[0..), tier-C blocks ascending into lists[REP_MAX_NB - 1], [REP_MAX_NB - 2], ...
-// (the two never meet: a row holds at most NB <= REP_MAX_NB of them)
+// tier-B blocks ascending into lists[0..), tier-C blocks ascending into lists[N - 1], [N - 2], ...
+// (the two never meet: a row holds at most NB <= N of them)
+template <int N>
 __device__ void build_lists(const RepArgs& a, size_t row, unsigned short* lists, int* counts) {
   const int l = threadIdx.x & 63;
   int nb_run = 0, nc_run = 0;
@@ -97,7 +100,7 @@ __device__ void build_lists(const RepArgs& a, size_t row, unsigned short* lists,
     }
     while (cm) {
       const int b = __ffs(cm) - 1;
-      lists[REP_MAX_NB - 1 - oc++] = (unsigned short)(w * 32 + b);
+      lists[N - 1 - oc++] = (unsigned short)(w * 32 + b);
       cm &= cm - 1;
     }
     nb_run += __shfl(ib, 63, 64);
@@ -110,11 +113,11 @@ __device__ void build_lists(const RepArgs& a, size_t row, unsigned short* lists,
 }
 
 // ------------------------------------------------------------------------------------------------ forward / dQ
-template <bool BWD>
+template <bool BWD, int LISTN>
 __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
   __shared__ __attribute__((aligned(16))) char kv_s[2][2][BK * 256];
   __shared__ __attribute__((aligned(16))) float bias_s[2][BK];
-  __shared__ unsigned short lists[REP_MAX_NB];
+  __shared__ unsigned short lists[LISTN];
   __shared__ int counts[2];
 
   int bh, qb;  // XCD-aware, run-time balanced order of (query block, head) (queues.h)
@@ -129,7 +132,7 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
   const size_t tok = head + (size_t)qb * BK + qrow;
   const size_t brow = (size_t)bh * a.NB + qb;
 
-  if (wv == 0) build_lists(a, brow, lists, counts);
+  if (wv == 0) build_lists<LISTN>(a, brow, lists, counts);
   Stream st;
   st.beg = sload(a.row_ptr + (size_t)bh * (a.NB + 1) + qb);
   st.nA = (a.phases & PH_A) ? sload(a.row_ptr + (size_t)bh * (a.NB + 1) + qb + 1) - st.beg : 0;
@@ -181,7 +184,7 @@ __global__ __launch_bounds__(256, 2) void rep_q_kernel(RepArgs a) {
     const int n = tb ? st.nBrows : st.nC;
     auto table_row = [&](int p) -> int {
       if (p >= n) return -1;
-      return tb ? (int)lists[p / a.RM] * a.RM + p % a.RM : (int)lists[REP_MAX_NB - 1 - p];
+      return tb ? (int)lists[p / a.RM] * a.RM + p % a.RM : (int)lists[LISTN - 1 - p];
     };
     const srd_t r1 = tb ? rkm : rkt, r2 = tb ? rvm : rvt;
 #pragma unroll
@@ -717,7 +720,7 @@ using namespace es;
 static int rep_check(int BH, int L, int D, int RM) {
   ES_REQUIRE(BH > 0 && BH <= 65535 && L > 0 && L % BK == 0, ES_ERR_INVALID, "VSA2-rep: tokens must be [BH, L = NB * 64, D]");
   ES_REQUIRE(D == 64 || D == HD, ES_ERR_UNSUPPORTED, "VSA2-rep: head dim must be 64 or 128 (rows stored with 128 columns)");
-  ES_REQUIRE(L / BK <= REP_MAX_NB, ES_ERR_UNSUPPORTED, "VSA2-rep: NB <= 4096 blocks");
+  ES_REQUIRE(L / BK <= REP_MAX_NB, ES_ERR_UNSUPPORTED, "VSA2-rep: NB <= 8192 blocks");
   ES_REQUIRE(RM == 1 || RM == 2 || RM == 4 || RM == 8 || RM == 16, ES_ERR_INVALID,
              "RepTiers.mid_reps must be one of (1, 2, 4, 8, 16)");
   ES_REQUIRE((size_t)L * HD * 2 < (1ull << 31), ES_ERR_UNSUPPORTED, "VSA2-rep: one head's tokens exceed 2 GiB");
@@ -778,7 +781,10 @@ extern "C" int ES_VSA_API(vsa_rep_attn_fwd)(const void* q, const void* k, const 
   ES_REQUIRE(balanced_launch(BH, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "VSA2-rep: row-block queues unavailable");
   a.queues = qs.counters;
   a.fixed = qs.fixed;
-  hipLaunchKernelGGL(rep_q_kernel<false>, dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
+  if (L / BK <= REP_LIST)
+    hipLaunchKernelGGL((rep_q_kernel<false, REP_LIST>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((rep_q_kernel<false, REP_MAX_NB>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
   return check_launch("vsa_rep_attn_fwd");
 }
 
@@ -808,7 +814,10 @@ extern "C" int ES_VSA_API(vsa_rep_attn_bwd_q)(const void* q, const void* k, cons
   ES_REQUIRE(balanced_launch(BH, a.per_xcd, stream, qs), ES_ERR_LAUNCH, "VSA2-rep: row-block queues unavailable");
   a.queues = qs.counters;
   a.fixed = qs.fixed;
-  hipLaunchKernelGGL(rep_q_kernel<true>, dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
+  if (L / BK <= REP_LIST)
+    hipLaunchKernelGGL((rep_q_kernel<true, REP_LIST>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((rep_q_kernel<true, REP_MAX_NB>), dim3((unsigned)qs.grid), dim3(256), 0, stream, a);
   return check_launch("vsa_rep_attn_bwd_q");
 }
 

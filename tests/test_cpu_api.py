@@ -184,8 +184,8 @@ def test_torch_operators_trace_with_meta_tensors_and_refuse_host_tensors():
 
 def test_block_count_limits_are_refused_before_any_launch():
     """Each VSA entry point with a block-count limit refuses a larger NB with a message, before any HIP call:
-    the three-tier kernels NB <= 4096, route_rows and the per-row tiers NB <= 8192, the global top-k and the CSR
-    transpose NB <= 46 340; the limits themselves are accepted as far as that check."""
+    route_rows, the three-tier kernels and the per-row tiers NB <= 8192, the global top-k and the CSR transpose
+    NB <= 46 340; the limits themselves are accepted as far as that check."""
     so = library()
     so.es_last_error_string.restype = ctypes.c_char_p
     p = ctypes.c_void_p(256)
@@ -211,7 +211,7 @@ def test_block_count_limits_are_refused_before_any_launch():
 
     # (name, call, the largest NB, the refusal text). At the limit a later host check must fail instead, so that no
     # kernel ever sees these placeholder pointers: no (b, h) rows, phases 8, kab > NB, a workspace too small.
-    cases = [("route_rows", route_rows, 8192, b"NB <= 8192"), ("rep_attn_fwd", rep_fwd, 4096, b"NB <= 4096"),
+    cases = [("route_rows", route_rows, 8192, b"NB <= 8192"), ("rep_attn_fwd", rep_fwd, 8192, b"NB <= 8192"),
              ("row_tiers", row_tiers, 8192, b"NB <= 8192"), ("global_topk", global_topk, 46340, b"bad top-k shape"),
              ("csr_transpose", csr_transpose, 46340, b"NB <= 46340")]
     for name, call, limit, text in cases:

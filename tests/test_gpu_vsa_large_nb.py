@@ -1,11 +1,11 @@
 """VSA routing and three-tier attention beyond 2048 blocks (longer videos than the HunyuanVideo benchmark clip):
-the original-VSA router (block scores and per-row top-K, 8 rows per workgroup past 2048 blocks) at NB = 2049, 3000
-and 5000, the exact global top-k and the kv->q inversion at NB = 4200, the per-query-block tiers at NB = 3000 and
-5000 (the 64- and 128-chunk register layouts), all byte for byte against the oracle; and the three-tier forward / backward at
-NB = 3000 (192 000 tokens, a 40-token tail block) in both constructions, O / LSE / dQ of sampled query blocks and
-dK / dV of sampled kv blocks against the float64 oracle (oracle/vsa_ref.py rep_fine_head restated per block, and
-rep_kv_block_grads), max-abs 2e-2 / rel-L2 1e-2 with the gradients' conditioning bound (see
-tests/test_gpu_vsa_rep_backward_sizes.py)."""
+* byte for byte against the oracle: the original-VSA router (block scores and per-row top-K, 8 rows per workgroup
+  past 2048 blocks) at NB = 2049, 3000 and 5000; the exact global top-k and the kv->q inversion at NB = 4200; the
+  per-query-block tiers at NB = 3000 and 5000 (the 64- and 128-chunk register layouts);
+* the three-tier forward / backward at NB = 3000 (192 000 tokens, a 40-token tail block) in both constructions and
+  at NB = 4500 (the 8192-entry block lists): O / LSE / dQ of sampled query blocks and dK / dV of sampled kv blocks
+  against the float64 oracle (oracle/vsa_ref.py rep_fine_head restated per block, and rep_kv_block_grads), max-abs
+  2e-2 / rel-L2 1e-2 with the gradients' conditioning bound (see tests/test_gpu_vsa_rep_backward_sizes.py)."""
 import math
 import sys
 
@@ -166,10 +166,11 @@ def check_bound(name, got, want, absum):
     check_close(name, got, want, max_abs=np.inf)
 
 
-@pytest.mark.parametrize("construction", ["reference", "baseline"])
-def test_three_tiers_nb_3000(dev, construction):
+@pytest.mark.parametrize("NB,construction", [(3000, "reference"), (3000, "baseline"), (4500, "reference")])
+def test_three_tiers_beyond_2048(dev, NB, construction):
+    """NB = 4500 takes the forward / dQ kernels' 8192-entry block lists (one workgroup per CU)."""
     from self_trainable_or_free_attn_amd.vsa import _C, rep
-    B, H, D, RM, NB = 1, 2, 128, 4, 3000
+    B, H, D, RM = 1, 2, 128, 4
     cnt = np.full(NB, 64)
     cnt[-1] = 40
     L = NB * 64
@@ -181,7 +182,7 @@ def test_three_tiers_nb_3000(dev, construction):
     kmeans = construction == "baseline"
     tiers = rep.RepTiers(frac_full=0.05, frac_mid=0.20, mid_reps=RM, split="per_row" if kmeans else "global",
                          tables="kmeans" if kmeans else "contiguous", kmeans_iters=5, seed=3)
-    log("NB 3000 three tiers:", construction)
+    log("NB", NB, "three tiers:", construction)
     sel = rep.route_tiers(qd, kd, blk, tiers, R=16)
     x = [t.detach().clone().requires_grad_(True) for t in (qd, kd, vd)]
     o, lse = rep.rep_fine_attention(*x, blk, sel, mid_reps=RM, tables=tiers.tables, kmeans_iters=5, seed=3)
@@ -204,7 +205,7 @@ def test_three_tiers_nb_3000(dev, construction):
         qh, kh, vh, dh = (f32(t[0, h]).astype(np.float64) for t in (q, k, v, dout))
         mah, mabh = ma[0, h], ma[0, h] | mb[0, h]
         for i in (0, 1777, NB - 1):
-            log("NB 3000:", construction, "head", h, "query block", i)
+            log("NB", NB, construction, "head", h, "query block", i)
             wo, wl, wdq, bq = _block_oracle(qh, kh, vh, dh, go[0, h], cnt, mah, mabh, RM, tables, groups, i)
             r = slice(i * 64, i * 64 + int(cnt[i]))
             check_close(f"O h{h} b{i}", go[0, h, r], wo)
