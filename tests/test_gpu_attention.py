@@ -15,8 +15,8 @@ pytestmark = pytest.mark.gpu
 L, H, D = 4152, 2, 128          # 65 kv blocks (the last has 56 tokens), 33 query tiles (the last has 56 rows)
 
 
-def steps(n, seed=0, dev="cuda"):
-    return [[x[None].to(dev) for x in s] for s in structured_qkv(L, H, D, seed=seed, steps=n)]
+def steps(n, seed=0, dev="cuda", shape=(L, H)):
+    return [[x[None].to(dev) for x in s] for s in structured_qkv(shape[0], shape[1], D, seed=seed, steps=n)]
 
 
 def dense(q, k, v):
@@ -65,13 +65,15 @@ def check_formula(out, qkv, selection, buf, branch=0):
     own (branch 0 keeps its set for its selection on the plan stream)."""
     out = out[0].float()
     q, k, v = (x[0].float() for x in qkv)
+    L, H = q.shape[0], q.shape[1]
     counts, blocks, refine = selection
     k_mean, v_mean = (buf.k_mean, buf.v_mean) if branch == 0 else (buf.k_mean1, buf.v_mean1)
     nb = k_mean.shape[0]
     block_len = torch.full((nb,), 64.0, device="cuda")
     block_len[-1] = L - 64 * (nb - 1)
+    nq = -(-L // 128)
     for h in range(H):
-        for t in (0, 7, 32):
+        for t in sorted({0, 7, nq // 2, nq - 1}):
             exact = blocks[t, h, :counts[t, h]].tolist()
             refined = [b for b in refine[t, h].tolist() if b < nb]
             means = sorted(set(range(nb)) - set(exact) - set(refined))
@@ -113,6 +115,19 @@ def test_cfg_branches_share_selection():
 
 def test_sparse_step_matches_formula():
     inputs = steps(3)
+    attn = new_attention(density=0.1)
+    run(attn, inputs[:2])
+    out, selection = call_with_selection(attn, *inputs[2], 2)
+    check_formula(out, inputs[2], selection, attn._buffers)
+
+
+@pytest.mark.parametrize("shape", [(4097, 1), (4160, 2), (8191, 3)])
+def test_sparse_step_matches_formula_at_edge_shapes(shape):
+    """A last kv block of one token (its mean is that token, its log2 count 0, its representatives one point), a
+    length that fills its last kv block but only half of its last query tile, and 128 kv blocks with a 63-token
+    tail and a 127-row last tile, at 1 and 3 heads."""
+    print("edge shape", shape, flush=True)
+    inputs = steps(3, seed=3, shape=shape)
     attn = new_attention(density=0.1)
     run(attn, inputs[:2])
     out, selection = call_with_selection(attn, *inputs[2], 2)
