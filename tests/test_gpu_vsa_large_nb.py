@@ -1,6 +1,6 @@
 """VSA routing and three-tier attention beyond 2048 blocks (longer videos than the HunyuanVideo benchmark clip):
 * byte for byte against the oracle: the original-VSA router (block scores and per-row top-K, 8 rows per workgroup
-  past 2048 blocks) at NB = 2049, 3000 and 5000; the exact global top-k and the kv->q inversion at NB = 4200; the
+  past 2048 blocks) at NB = 2049, 3000 and 5000, bf16 and fp16; the exact global top-k and the kv->q inversion at NB = 4200; the
   per-query-block tiers at NB = 3000 and 5000 (the 64- and 128-chunk register layouts);
 * the three-tier forward / backward at NB = 3000 (192 000 tokens, a 40-token tail block) in both constructions and
   at NB = 4500 (the 8192-entry block lists): O / LSE / dQ of sampled query blocks and dK / dV of sampled kv blocks
@@ -51,13 +51,16 @@ def check_csr(q2k_ptr, q2k_idx, k2q_ptr, k2q_idx, mask):
     assert np.array_equal(kp, cp) and np.array_equal(ki[:ci.size], ci), "k2q lists differ"
 
 
-@pytest.mark.parametrize("NB,K", [(2049, 2049), (2049, 0), (3000, 150), (5000, 61)])
-def test_route_rows_beyond_2048(dev, NB, K):
+@pytest.mark.parametrize("NB,K,dtype", [(2049, 2049, "bf16"), (2049, 0, "bf16"), (3000, 150, "bf16"),
+                                         (5000, 61, "bf16"), (3000, 150, "f16")])
+def test_route_rows_beyond_2048(dev, NB, K, dtype):
+    from oracle.bf16 import round_bf16, round_f16
     B, H, D = 1, 2, 128
-    log("route_rows NB", NB, "K", K)
+    log("route_rows NB", NB, "K", K, dtype)
     g = torch.Generator().manual_seed(NB + K)
     pad = -(-NB // 64) * 64
-    qc, kc = ((torch.randn(B, H, pad, D, generator=g) * 0.5).to(torch.bfloat16).to(dev) for _ in range(2))
+    tdt, rnd = (torch.bfloat16, round_bf16) if dtype == "bf16" else (torch.float16, round_f16)
+    qc, kc = ((torch.randn(B, H, pad, D, generator=g) * 0.5).to(tdt).to(dev) for _ in range(2))
     scores = C().block_scores(qc, kc, NB)
     got = C().route_rows(qc, kc, NB, K)
     torch.cuda.synchronize()
@@ -67,8 +70,9 @@ def test_route_rows_beyond_2048(dev, NB, K):
     h = 1
     rows = np.r_[0:40, NB - 40:NB]
     qh, kh = f32(qc)[0, h, rows].astype(np.float64), f32(kc)[0, h, :NB].astype(np.float64)
-    want_s = ref.block_scores(qh, kh)
-    step = np.exp2(np.floor(np.log2(np.maximum(np.abs(want_s), 2.0 ** -100))) - 7)
+    want_s = ref.block_scores(qh, kh, rnd=rnd)
+    mant = 7 if dtype == "bf16" else 10
+    step = np.exp2(np.floor(np.log2(np.maximum(np.abs(want_s), 2.0 ** -100))) - mant)
     dot_err = D * 2.0 ** -24 * (np.abs(qh) @ np.abs(kh).T) / np.sqrt(D)
     assert (np.abs(gs[h, rows] - want_s) <= 2 * step + dot_err).all()
     assert (gs[h, rows] == want_s).mean() > 0.95
