@@ -1,7 +1,7 @@
 """VSA routing and three-tier attention beyond 2048 blocks (longer videos than the HunyuanVideo benchmark clip):
 * byte for byte against the oracle: the original-VSA router (block scores and per-row top-K, 8 rows per workgroup
-  past 2048 blocks) at NB = 2049, 3000 and 5000, bf16 and fp16; the exact global top-k and the kv->q inversion at NB = 4200; the
-  per-query-block tiers at NB = 3000 and 5000 (the 64- and 128-chunk register layouts);
+  past 2048 blocks) at NB = 2049, 3000 and 5000, bf16 and fp16; the exact global top-k and the kv->q inversion at
+  NB = 4200; the per-query-block tiers at NB = 3000 and 5000 (the 64- and 128-chunk register layouts);
 * the three-tier forward / backward at NB = 3000 (192 000 tokens, a 40-token tail block) in both constructions and
   at NB = 4500 (the 8192-entry block lists): O / LSE / dQ of sampled query blocks and dK / dV of sampled kv blocks
   against the float64 oracle (oracle/vsa_ref.py rep_fine_head restated per block, and rep_kv_block_grads), max-abs
